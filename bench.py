@@ -1,0 +1,273 @@
+#!/usr/bin/env python3
+"""Benchmark of the KV-cache hot path on one MI355X (BASELINE.json metric).
+
+Workload (config 2): Qwen3-0.6B ragged batched decode over all 28 layers, fp16,
+batch 32, context lengths U[128, 4096], 16-token pages in a 16384-page pool per
+layer.  One step = for each of the 28 layers: store_kv (one new token per
+sequence) then paged decode attention, launched back to back on one stream
+through the C ABI (no Python validation inside the timed region).
+
+Reported:
+  value            paged-decode attention HBM GB/s = algorithmic decode bytes /
+                   decode kernel time, both summed over the K timed steps; the
+                   kernel time comes from HIP events recorded on the launch stream
+                   around every decode launch
+  kv_append_us_per_layer   the same events around every store_kv launch
+  roofline         the decode kernel against 8 TB/s HBM; traffic (HBM bytes per
+                   launch from rocprofv3 FETCH_SIZE/WRITE_SIZE) is read from the
+                   committed profile summary when it exists
+  append_batched   the bandwidth-sized append (28 layers x 2048 tokens, one
+                   launch) against 8 TB/s
+  cpu_baseline     the CPU oracle (plain C port of the same algorithm, one core)
+                   on a bounded sample of the same decode workload
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+METRIC = "paged-decode attn HBM GB/s (% of peak) + KV-append µs/layer, Qwen3-0.6B B=32"
+HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_config2_traffic.json")
+
+
+class HipEvents:
+    """Thin ctypes access to hipEventCreate/Record/ElapsedTime (cheap enough to bracket every launch)."""
+
+    def __init__(self):
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def create(self, n: int) -> list:
+        evs = []
+        for _ in range(n):
+            e = ctypes.c_void_p()
+            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
+                raise RuntimeError("hipEventCreate failed")
+            evs.append(e)
+        return evs
+
+    def elapsed_ms(self, a, b) -> float:
+        ms = ctypes.c_float()
+        if self.hip.hipEventElapsedTime(ctypes.byref(ms), a, b) != 0:
+            raise RuntimeError("hipEventElapsedTime failed")
+        return ms.value
+
+    def destroy(self, evs) -> None:
+        for e in evs:
+            self.hip.hipEventDestroy(e)
+
+
+def _compact(pool_layer, table, lens, bs=16):
+    import torch
+    used = sorted({int(p) for b in range(table.shape[0]) for p in table[b, :-(-int(lens[b]) // bs)]})
+    idx = torch.as_tensor(used, dtype=torch.long, device=pool_layer.device)
+    sub = pool_layer.index_select(1, idx).cpu().numpy()
+    remap = np.zeros(int(table.max()) + 1, np.int32)
+    remap[np.asarray(used)] = np.arange(len(used), dtype=np.int32)
+    t2 = np.zeros_like(table)
+    for b in range(table.shape[0]):
+        n = -(-int(lens[b]) // bs)
+        t2[b, :n] = remap[table[b, :n]]
+    return sub, t2
+
+
+def run_cpu_baseline(w, pool_layer, q, seconds: float) -> dict:
+    import oracle
+    sub, t2 = _compact(pool_layer, w.block_tables, w.seq_lens)
+    qn = q.cpu().numpy()
+    rows = 0
+    nbytes = 0
+    t0 = time.perf_counter()
+    while True:
+        for b in range(w.batch):
+            oracle.paged_attention(qn[b:b + 1], sub, t2[b:b + 1], w.seq_lens[b:b + 1])
+            rows += 1
+            nbytes += int(w.seq_lens[b]) * 2 * w.num_kv_heads * w.head_dim * 2 + 2 * w.num_q_heads * w.head_dim * 2
+            if time.perf_counter() - t0 >= seconds:
+                break
+        if time.perf_counter() - t0 >= seconds:
+            break
+    dt = time.perf_counter() - t0
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
+            "sample": f"CPU oracle (oracle/ifn_oracle.c, scalar C, 1 thread) on {rows} config-2 decode rows "
+                      f"of layer 0 ({nbytes / 1e6:.1f} MB algorithmic) in {dt:.1f} s",
+            "cpu_model": _cpu_model()}
+
+
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--cpu-seconds", type=float, default=12.0)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the hot path shards by sequence "
+              "with no exchange, so N GPUs run N independent copies of this benchmark.", file=sys.stderr)
+        return 2
+
+    import torch
+    from infurnace_amd import _capi, workloads
+
+    lib = _capi.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+    w = workloads.config2()
+    L, B, hq, hkv, d, P = w.num_layers, w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.num_pages
+    g = torch.Generator(device=dev).manual_seed(w.seed)
+    print(f"[bench] allocating {L}x{P}-page pool ({L * P * 65536 / 2**30:.1f} GiB)", file=sys.stderr, flush=True)
+    pool = torch.empty((L, 2, P, 16, hkv, d), dtype=torch.float16, device=dev)
+    for layer in range(L):
+        pool[layer].normal_(generator=g)
+    q = torch.randn((L, B, hq, d), generator=g, device=dev, dtype=torch.float16)
+    nk = torch.randn((L, B, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    nv = torch.randn((L, B, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty((L, B, hq, d), dtype=torch.float16, device=dev)
+    bt = torch.from_numpy(w.block_tables).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    slots = torch.from_numpy(w.append_slots).to(dev)
+    max_len = int(w.seq_lens.max())
+    ws_bytes = lib.ifn_paged_decode_workspace_bytes(B, hq, hkv, d, 16, max_len)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    scale = 1.0 / np.sqrt(d)
+
+    layer_bytes = pool[0].numel() * 2
+    store_args = [(pool.data_ptr() + i * layer_bytes, P, slots.data_ptr(), None, nk[i].data_ptr(), nv[i].data_ptr(),
+                   B, hkv, d, 16, stream) for i in range(L)]
+    dec_args = [(out[i].data_ptr(), q[i].data_ptr(), pool.data_ptr() + i * layer_bytes, P, bt.data_ptr(),
+                 w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, ws.data_ptr(), ws_bytes,
+                 stream) for i in range(L)]
+    store_fn, dec_fn = lib.ifn_store_kv, lib.ifn_paged_decode
+    hip = HipEvents()
+
+    def step(evs=None, base=0):
+        for i in range(L):
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 3 * i], stream)
+            rc = store_fn(*store_args[i])
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 3 * i + 1], stream)
+            rc |= dec_fn(*dec_args[i])
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 3 * i + 2], stream)
+            if rc:
+                raise RuntimeError(f"launch failed in layer {i}: {_capi.status_string(rc)}")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    K = args.steps
+    evs = hip.create(3 * L * K)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(K):
+        step(evs, 3 * L * s)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    dec_ms = [hip.elapsed_ms(evs[3 * j + 1], evs[3 * j + 2]) for j in range(L * K)]
+    app_ms = [hip.elapsed_ms(evs[3 * j], evs[3 * j + 1]) for j in range(L * K)]
+    hip.destroy(evs)
+    print(f"[bench] timed {K} steps x {L} layers in {wall:.3f} s", file=sys.stderr, flush=True)
+
+    dec_bytes = w.decode_bytes()
+    dec_s = float(np.mean(dec_ms)) / 1e3
+    gbps = dec_bytes / dec_s / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        try:
+            traffic = json.load(open(TRAFFIC_FILE)).get("hbm_bytes_per_launch")
+        except (OSError, ValueError):
+            traffic = None
+
+    # bandwidth-sized append: 28 layers x 2048 tokens in one launch (config 3 prompt)
+    w3 = workloads.config3()
+    del out
+    T3 = w3.prompt_len
+    pool3 = torch.empty((L, 2, w3.num_pages, 16, hkv, d), dtype=torch.float16, device=dev)
+    k3 = torch.randn((L, T3, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    v3 = torch.randn((L, T3, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    slots3 = torch.from_numpy((w3.block_table.astype(np.int64)[np.arange(T3) // 16] * 16
+                               + np.arange(T3) % 16).astype(np.int32)).to(dev)
+    a_args = (pool3.data_ptr(), L, w3.num_pages, slots3.data_ptr(), None, k3.data_ptr(), v3.data_ptr(), T3, hkv, d,
+              16, stream)
+    for _ in range(3):
+        lib.ifn_store_kv_layers(*a_args)
+    reps = 20
+    aev = hip.create(2 * reps)
+    torch.cuda.synchronize()
+    for r in range(reps):
+        hip.hip.hipEventRecord(aev[2 * r], stream)
+        rc = lib.ifn_store_kv_layers(*a_args)
+        hip.hip.hipEventRecord(aev[2 * r + 1], stream)
+        if rc:
+            raise RuntimeError(_capi.status_string(rc))
+    torch.cuda.synchronize()
+    a_ms = float(np.median([hip.elapsed_ms(aev[2 * r], aev[2 * r + 1]) for r in range(reps)]))
+    hip.destroy(aev)
+    a_bytes = L * T3 * (2 * 2 * hkv * d * 2 + 4)
+    a_gbps = a_bytes / (a_ms / 1e3) / 1e9
+    del pool3, k3, v3
+
+    cpu = None
+    if not args.no_cpu_baseline:
+        print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
+        cpu = run_cpu_baseline(w, pool[0], q[0], args.cpu_seconds)
+
+    result = {
+        "metric": METRIC,
+        "value": round(gbps, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": K,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall / K * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded N(0,1) fp16 pool/queries; numpy PCG64 lengths and page permutations)",
+        "config": {"workload": w.name + ", 28 layers, store_kv + paged decode per layer",
+                   "batch": B, "num_q_heads": hq, "num_kv_heads": hkv, "head_dim": d, "block_size": 16,
+                   "pages_per_layer": P, "context_tokens": int(w.seq_lens.sum()), "layers": L, "seed": w.seed},
+        "decode_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
+        "decode_us_per_layer": round(dec_s * 1e6, 3),
+        "decode_bytes_per_layer": dec_bytes,
+        "kv_append_us_per_layer": round(float(np.mean(app_ms)) * 1e3, 3),
+        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
+                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
+        "append_batched": {"workload": "store_kv_layers, 28 layers x 2048 tokens (config 3 prompt), one launch",
+                           "us": round(a_ms * 1e3, 2), "bytes": a_bytes, "GB/s": round(a_gbps, 2),
+                           "frac": round(a_gbps / HBM_PEAK_GBPS, 4)},
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

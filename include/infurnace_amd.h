@@ -1,0 +1,151 @@
+/*
+ * infurnace_amd -- C ABI of the MI355X (gfx950) KV-cache hot path.
+ *
+ * One shared library, libinfurnace_hip.so, built from infurnace_amd/csrc/.
+ * Every pointer argument is a DEVICE pointer owned by the caller (for example
+ * torch.Tensor.data_ptr() of a ROCm tensor).  `stream` is a hipStream_t (NULL
+ * = the default stream); every launch is asynchronous on it, so a store_kv
+ * followed by a paged attention call on the same stream satisfies the
+ * reference's write-before-read rule (docs/architecture.md:249-250).
+ *
+ * The library never allocates device memory.  Scratch space is a
+ * caller-provided workspace.  No C++ exception crosses this boundary: every
+ * entry point returns IFN_OK (0) or a negative IFN_ERR_* code, checked on the
+ * host before any launch (shape, alignment and workspace checks) or after it
+ * (hipGetLastError).  Entry points hold no mutable global state, so distinct
+ * streams may call them concurrently with distinct workspaces.
+ *
+ * Reference interfaces replaced (tylerguest/infurnace).  The reference's
+ * modules for this path are 0-byte placeholders; their documented contract is
+ *   docs/architecture.md:242-246   store_kv(kv_pool, slot_mapping, active_mask, new_k, new_v)
+ *                                  paged_attention(query, kv_pool, block_tables,
+ *                                                  sequence_lengths, active_mask)
+ *   docs/architecture.md:225-235   kv_pool[layer, K_or_V, physical_page, page_offset,
+ *                                  kv_head, head_dim]; slot = page * page_size + offset
+ * and the code they replace is the contiguous store + SDPA at
+ *   src/infurnace/executor/tinygrad/model.py:191-200 (decode) and :116-138 (prefill).
+ *
+ * Layouts (all C-contiguous, fp16 = IEEE binary16):
+ *   kv pool, one layer   [2][num_pages][block_size][num_kv_heads][head_dim]   (K = 0, V = 1)
+ *   kv pool, all layers  [num_layers][2][num_pages][block_size][num_kv_heads][head_dim]
+ *   new_k / new_v        [num_tokens][num_kv_heads][head_dim]
+ *   slot_mapping         int32 [num_tokens]; slot = page * block_size + offset
+ *   active_mask          uint8 [rows]; 0 = inactive (may be NULL = all active)
+ *   block_tables         int32 [batch][max_pages_per_seq]
+ *   decode query/out     [batch][num_q_heads][head_dim]
+ *   prefill query/out    [num_q_tokens][num_q_heads][head_dim]
+ * Query head h reads kv head h / (num_q_heads / num_kv_heads) (GQA, as
+ * tinygrad's scaled_dot_product_attention(enable_gqa=True) at model.py:200).
+ */
+#ifndef INFURNACE_AMD_H
+#define INFURNACE_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define IFN_OK 0
+#define IFN_ERR_INVALID_ARGUMENT (-1) /* null pointer, bad shape, bad count */
+#define IFN_ERR_UNSUPPORTED (-2)      /* (head_dim, group, block_size) not compiled */
+#define IFN_ERR_ALIGNMENT (-3)        /* device pointers must be 16-byte aligned */
+#define IFN_ERR_WORKSPACE (-4)        /* workspace missing or smaller than required */
+#define IFN_ERR_HIP (-5)              /* the HIP runtime reported a launch error */
+
+/* Human-readable name of a status code (static string, never NULL). */
+const char* ifn_status_string(int status);
+
+/* ABI version: bumped whenever a signature or layout in this header changes. */
+int ifn_abi_version(void);
+
+/*
+ * KV append: for each token t with active_mask[t] != 0 and
+ * 0 <= slot_mapping[t] < num_pages * block_size, copy new_k[t] / new_v[t]
+ * (num_kv_heads * head_dim fp16 each) into the K / V half of the layer's pool
+ * at that slot.  Every other token writes nothing (inactive rows never touch a
+ * shared dummy location).  Bit-exact copy.  Two active tokens with the same
+ * slot race; the Python wrapper rejects that in its debug check.
+ * Replaces: store_kv, docs/architecture.md:245 (placeholder
+ * src/infurnace/kernels/kv_store.py, 0 B); contiguous precedent
+ * src/infurnace/executor/tinygrad/model.py:191-196 and :134-138.
+ * Requires head_dim % 8 == 0 and 16-byte aligned pointers.
+ */
+int ifn_store_kv(void* kv_pool_layer, int64_t num_pages, const int32_t* slot_mapping,
+                 const uint8_t* active_mask, const void* new_k, const void* new_v,
+                 int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                 int32_t block_size, void* stream);
+
+/*
+ * The same append for num_layers layers in one launch: kv_pool is the full
+ * [num_layers][2][num_pages][block_size][num_kv_heads][head_dim] pool and
+ * new_k / new_v are [num_layers][num_tokens][num_kv_heads][head_dim].  The
+ * slot mapping and mask are shared by all layers (one token occupies the same
+ * slot in every layer, docs/architecture.md:225-235).
+ * Replaces: the per-layer store of model.py:134-138 repeated over the layer
+ * loop at model.py:98 (one launch instead of num_layers).
+ */
+int ifn_store_kv_layers(void* kv_pool, int32_t num_layers, int64_t num_pages,
+                        const int32_t* slot_mapping, const uint8_t* active_mask,
+                        const void* new_k, const void* new_v, int32_t num_tokens,
+                        int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                        void* stream);
+
+/* Workspace bytes ifn_paged_decode needs for these shapes (0 is never returned;
+ * a negative-valued shape returns 0 and ifn_paged_decode rejects it). */
+size_t ifn_paged_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, int32_t block_size, int32_t max_seq_len);
+
+/*
+ * Paged decode attention, one query token per sequence:
+ *   out[b, h] = softmax(scale * q[b, h] . K[b, h/g, 0:L]^T) . V[b, h/g, 0:L],
+ * L = seq_lens[b], keys gathered page by page through block_tables[b]
+ * (fp16 in, fp32 accumulation, fp16 out).  scale <= 0 selects 1/sqrt(head_dim).
+ * Rows with active_mask[b] == 0 write nothing.  An active row with L == 0
+ * writes zeros.  L is clamped to [0, max_pages_per_seq * block_size] and to
+ * max_seq_len; a page id outside [0, num_pages) contributes no keys (no
+ * out-of-bounds read).  max_seq_len is the host-side upper bound of seq_lens
+ * that sizes the launch and the workspace.
+ * The workspace must be zero-filled once when created; every call leaves its
+ * counters at zero again, so one workspace serves any number of calls on one
+ * stream (calls overlapping on two streams need two workspaces).
+ * Replaces: paged_attention (decode), docs/architecture.md:246 (placeholder
+ * src/infurnace/kernels/paged_attention.py, 0 B); contiguous semantics
+ * src/infurnace/executor/tinygrad/model.py:196-200.
+ */
+int ifn_paged_decode(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                     const int32_t* block_tables, int32_t max_pages_per_seq,
+                     const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                     int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
+                     size_t workspace_bytes, void* stream);
+
+/* Workspace bytes ifn_paged_prefill needs for these shapes. */
+size_t ifn_paged_prefill_workspace_bytes(int32_t num_q_tokens, int32_t query_start,
+                                         int32_t num_q_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t block_size);
+
+/*
+ * Causal chunked-prefill paged attention for one sequence: query row i sits at
+ * absolute position query_start + i and attends keys [0, query_start + i],
+ * read through block_table (one row of max_pages int32).  The chunk's own K/V
+ * must already be stored (append-then-attend).  fp16 in, fp32 accumulation,
+ * fp16 out; QK^T and PV run on MFMA.  scale <= 0 selects 1/sqrt(head_dim).
+ * Page ids outside [0, num_pages) contribute no keys.  The workspace follows
+ * the same zero-once rule as ifn_paged_decode.
+ * Replaces: paged_attention with a multi-token query, docs/architecture.md:246;
+ * contiguous semantics src/infurnace/executor/tinygrad/model.py:116-132
+ * (mask key_pos <= query_pos, query_pos = start_position + i).
+ */
+int ifn_paged_prefill(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                      const int32_t* block_table, int32_t max_pages, int32_t query_start,
+                      int32_t num_q_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                      int32_t head_dim, int32_t block_size, float scale, void* workspace,
+                      size_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* INFURNACE_AMD_H */

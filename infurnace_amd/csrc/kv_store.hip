@@ -1,0 +1,142 @@
+// KV append (store_kv): slot-mapped copy of new K/V rows into 16-token pages.
+//
+// Replaces the reference's documented store_kv (docs/architecture.md:245,
+// 249-253; placeholder src/infurnace/kernels/kv_store.py) whose contiguous
+// precedent is the SSA store at src/infurnace/executor/tinygrad/model.py:191-196.
+//
+// Mapping.  The work is a pure HBM copy: per token, num_kv_heads*head_dim fp16
+// of K and the same of V (4 KiB for 8 x 128).  Both the source row and the
+// destination slot row are contiguous, so the copy is cut into 16-byte chunks
+// and consecutive lanes take consecutive chunks: every wavefront load and store
+// instruction moves 64 x 16 B = 1 KiB of one contiguous row (four kv-head rows
+// of 256 B at head_dim 128), i.e. fully coalesced 128-bit global accesses.
+// A workgroup of 256 lanes owns kTok whole tokens; each lane issues all of its
+// loads before its first store so kTok x 16 B per lane are in flight.  The slot
+// and active flag are read once per token (uniform across the workgroup, so
+// they become scalar loads).  Rows that are inactive or whose slot lies outside
+// the pool write nothing.
+#include "ifn_common.hpp"
+
+namespace ifn {
+
+constexpr int kStoreThreads = 256;
+
+// Fast path: one token's K+V is exactly 256 chunks (num_kv_heads*head_dim == 1024),
+// so lane i copies chunk i of each of the kTok tokens.
+template <int kTok>
+__global__ __launch_bounds__(kStoreThreads) void store_kv_1024(
+    uint8_t* __restrict__ pool, int64_t layer_bytes, int64_t v_offset, int64_t num_slots,
+    const int32_t* __restrict__ slot_mapping, const uint8_t* __restrict__ active,
+    const uint8_t* __restrict__ nk, const uint8_t* __restrict__ nv, int64_t src_layer_bytes,
+    int32_t num_tokens) {
+  constexpr int kRowBytes = 2048;  // one token's K (or V) row: 1024 fp16
+  const int64_t layer = blockIdx.y;
+  const int lane = threadIdx.x;
+  const bool is_v = lane >= 128;
+  const int off = (lane & 127) * 16;
+  const uint8_t* src = (is_v ? nv : nk) + layer * src_layer_bytes + off;
+  uint8_t* dst = pool + layer * layer_bytes + (is_v ? v_offset : 0) + off;
+  u32x4 buf[kTok];
+  int64_t slot[kTok];
+#pragma unroll
+  for (int i = 0; i < kTok; ++i) {
+    const int t = blockIdx.x * kTok + i;
+    slot[i] = -1;
+    if (t < num_tokens && (active == nullptr || active[t] != 0)) {
+      const int64_t s = slot_mapping[t];
+      if (s >= 0 && s < num_slots) slot[i] = s;
+    }
+    if (slot[i] >= 0) buf[i] = ld16(src + int64_t(t) * kRowBytes);
+  }
+#pragma unroll
+  for (int i = 0; i < kTok; ++i)
+    if (slot[i] >= 0) st16(dst + slot[i] * kRowBytes, buf[i]);
+}
+
+// General path: any num_kv_heads*head_dim that is a multiple of 8.
+__global__ __launch_bounds__(kStoreThreads) void store_kv_generic(
+    uint8_t* __restrict__ pool, int64_t layer_bytes, int64_t v_offset, int64_t num_slots,
+    const int32_t* __restrict__ slot_mapping, const uint8_t* __restrict__ active,
+    const uint8_t* __restrict__ nk, const uint8_t* __restrict__ nv, int64_t src_layer_bytes,
+    int32_t row_chunks) {
+  const int64_t layer = blockIdx.y;
+  const int t = blockIdx.x;
+  if (active != nullptr && active[t] == 0) return;
+  const int64_t slot = slot_mapping[t];
+  if (slot < 0 || slot >= num_slots) return;
+  const int64_t row_bytes = int64_t(row_chunks) * 16;
+  const uint8_t* sk = nk + layer * src_layer_bytes + int64_t(t) * row_bytes;
+  const uint8_t* sv = nv + layer * src_layer_bytes + int64_t(t) * row_bytes;
+  uint8_t* dk = pool + layer * layer_bytes + slot * row_bytes;
+  uint8_t* dv = dk + v_offset;
+  for (int c = threadIdx.x; c < 2 * row_chunks; c += kStoreThreads) {
+    const bool is_v = c >= row_chunks;
+    const int64_t o = int64_t(is_v ? c - row_chunks : c) * 16;
+    st16((is_v ? dv : dk) + o, ld16((is_v ? sv : sk) + o));
+  }
+}
+
+static int launch_store(void* kv_pool, int32_t num_layers, int64_t num_pages,
+                        const int32_t* slot_mapping, const uint8_t* active_mask, const void* new_k,
+                        const void* new_v, int32_t num_tokens, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t block_size, void* stream) {
+  if (kv_pool == nullptr || slot_mapping == nullptr || new_k == nullptr || new_v == nullptr)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (num_layers < 1 || num_pages < 1 || num_tokens < 0 || num_kv_heads < 1 || head_dim < 1 ||
+      block_size < 1)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (head_dim % 8 != 0) return IFN_ERR_UNSUPPORTED;
+  IFN_CHECK_ALIGN16(kv_pool);
+  IFN_CHECK_ALIGN16(new_k);
+  IFN_CHECK_ALIGN16(new_v);
+  if (num_tokens == 0) return IFN_OK;
+  const int64_t row_elems = int64_t(num_kv_heads) * head_dim;
+  const int64_t num_slots = num_pages * block_size;
+  const int64_t v_offset = num_slots * row_elems * 2;
+  const int64_t layer_bytes = 2 * v_offset;
+  const int64_t src_layer_bytes = int64_t(num_tokens) * row_elems * 2;
+  hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* pool = static_cast<uint8_t*>(kv_pool);
+  const uint8_t* nk = static_cast<const uint8_t*>(new_k);
+  const uint8_t* nv = static_cast<const uint8_t*>(new_v);
+  if (row_elems == 1024) {
+    // Many tokens: 4 per workgroup for memory-level parallelism; few: 1 per
+    // workgroup so the launch spreads over more CUs.
+    if (int64_t(num_tokens) * num_layers >= 4096) {
+      dim3 grid{unsigned(ceil_div(num_tokens, 4)), unsigned(num_layers)};
+      store_kv_1024<4><<<grid, kStoreThreads, 0, s>>>(pool, layer_bytes, v_offset, num_slots,
+                                                      slot_mapping, active_mask, nk, nv,
+                                                      src_layer_bytes, num_tokens);
+    } else {
+      dim3 grid{unsigned(num_tokens), unsigned(num_layers)};
+      store_kv_1024<1><<<grid, kStoreThreads, 0, s>>>(pool, layer_bytes, v_offset, num_slots,
+                                                      slot_mapping, active_mask, nk, nv,
+                                                      src_layer_bytes, num_tokens);
+    }
+  } else {
+    dim3 grid{unsigned(num_tokens), unsigned(num_layers)};
+    store_kv_generic<<<grid, kStoreThreads, 0, s>>>(pool, layer_bytes, v_offset, num_slots,
+                                                    slot_mapping, active_mask, nk, nv,
+                                                    src_layer_bytes, int32_t(row_elems / 8));
+  }
+  return ifn_launch_status();
+}
+
+}  // namespace ifn
+
+extern "C" int ifn_store_kv(void* kv_pool_layer, int64_t num_pages, const int32_t* slot_mapping,
+                            const uint8_t* active_mask, const void* new_k, const void* new_v,
+                            int32_t num_tokens, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t block_size, void* stream) {
+  return ifn::launch_store(kv_pool_layer, 1, num_pages, slot_mapping, active_mask, new_k, new_v,
+                           num_tokens, num_kv_heads, head_dim, block_size, stream);
+}
+
+extern "C" int ifn_store_kv_layers(void* kv_pool, int32_t num_layers, int64_t num_pages,
+                                   const int32_t* slot_mapping, const uint8_t* active_mask,
+                                   const void* new_k, const void* new_v, int32_t num_tokens,
+                                   int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                   void* stream) {
+  return ifn::launch_store(kv_pool, num_layers, num_pages, slot_mapping, active_mask, new_k, new_v,
+                           num_tokens, num_kv_heads, head_dim, block_size, stream);
+}

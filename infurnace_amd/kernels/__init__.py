@@ -1,0 +1,11 @@
+"""Hot-path kernels, drop-in for the reference's ``infurnace.kernels``.
+
+``store_kv`` and ``paged_attention`` keep the documented names and positional
+arguments (reference docs/architecture.md:245-246); every call goes through
+the C ABI of libinfurnace_hip.so to hand-written gfx950 HIP kernels.
+"""
+from ._common import KVStoreError, PagedAttentionError
+from .kv_store import store_kv, store_kv_layers
+from .paged_attention import paged_attention
+
+__all__ = ["store_kv", "store_kv_layers", "paged_attention", "KVStoreError", "PagedAttentionError"]

@@ -1,0 +1,159 @@
+"""paged_attention: GQA attention that gathers K/V pages through block tables (HIP, gfx950).
+
+Mirrors the reference's documented operation
+``paged_attention(query, kv_pool, block_tables, sequence_lengths, active_mask)``
+(docs/architecture.md:242-246; src/infurnace/kernels/paged_attention.py is a
+0-byte placeholder).  It replaces the contiguous attention of
+src/infurnace/executor/tinygrad/model.py:
+
+  * decode (model.py:196-200): one query per sequence at position L-1 reads
+    keys [0, L) -- ``query`` [B, Hq, D], ``sequence_lengths`` = L per row;
+  * chunked prefill (model.py:116-132): ``query`` [T, Hq, D] of one sequence
+    with ``query_start`` = start_position; row i attends keys
+    [0, query_start + i] (mask key_pos <= query_pos, model.py:128-132).  The
+    chunk's K/V must already be in the pool (store_kv first).
+
+Both compute softmax(scale * q k^T) v with fp16 inputs, fp32 accumulation and
+fp16 output; query head h reads kv head h // (Hq // Hkv) (enable_gqa=True);
+``scale`` defaults to 1/sqrt(D) (tinygrad's default).  Inactive rows write
+nothing.
+"""
+from __future__ import annotations
+
+import math
+
+import torch
+
+from .. import _capi
+from ._common import PagedAttentionError, check_pool, current_stream, ptr
+
+__all__ = ["paged_attention", "PagedAttentionError", "workspace_for"]
+
+# One zero-initialised workspace per (device, stream): every kernel call leaves
+# the workspace's ticket counters at zero, so the buffer is reused as is.
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def workspace_for(device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+    """Zero-filled uint8 scratch of at least ``nbytes`` for calls on ``stream``."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        # grow geometrically so ragged batches do not reallocate every call
+        # (the caching allocator keeps the old block alive for work queued on this stream)
+        size = max(nbytes, 2 * ws.numel() if ws is not None else 0, 1 << 20)
+        ws = torch.zeros(size, dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
+def _check(name: str, t, shape: tuple, dtypes: tuple, device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise PagedAttentionError(f"{name} must be a torch.Tensor")
+    if t.dtype not in dtypes:
+        raise PagedAttentionError(f"{name} dtype must be one of {dtypes}, got {t.dtype}")
+    if tuple(t.shape) != tuple(shape):
+        raise PagedAttentionError(f"{name} shape must be {tuple(shape)}, got {tuple(t.shape)}")
+    if t.device != device:
+        raise PagedAttentionError(f"{name} must be on {device}, got {t.device}")
+    if not t.is_contiguous():
+        raise PagedAttentionError(f"{name} must be contiguous")
+
+
+def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: torch.Tensor,
+                    sequence_lengths: torch.Tensor | None, active_mask: torch.Tensor | None = None, *,
+                    layer: int = 0, scale: float | None = None, query_start: int | None = None,
+                    out: torch.Tensor | None = None, block_size: int = 16,
+                    max_seq_len: int | None = None) -> torch.Tensor:
+    """Paged GQA attention; returns ``out`` (allocated when None).
+
+    Decode (``query_start is None``): ``query`` [B, Hq, D] fp16,
+    ``block_tables`` int32 [B, max_pages], ``sequence_lengths`` int32 [B] on the
+    device, ``active_mask`` bool/uint8 [B] or None.  ``max_seq_len`` is an
+    optional host-side upper bound of ``sequence_lengths`` (default
+    max_pages * block_size) that sizes the launch.
+
+    Prefill (``query_start`` given): ``query`` [T, Hq, D] of one sequence,
+    ``block_tables`` int32 [max_pages] or [1, max_pages]; ``sequence_lengths`` is
+    unused on the device (keys = query_start + T) and, when it is a host value,
+    must equal query_start + T.  ``active_mask`` of one False row makes the call
+    a no-op.
+    """
+    pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
+    dev = pool_layer.device
+    if bs != block_size:
+        raise PagedAttentionError(f"kv_pool block_size {bs} != block_size argument {block_size}")
+    if not isinstance(query, torch.Tensor) or query.ndim != 3:
+        raise PagedAttentionError("query must be a rank-3 tensor ([B, Hq, D] decode or [T, Hq, D] prefill)")
+    n, hq, qd = query.shape
+    if qd != d:
+        raise PagedAttentionError(f"query head_dim {qd} != kv head_dim {d}")
+    if hq % hkv != 0:
+        raise PagedAttentionError(f"num_q_heads {hq} is not a multiple of num_kv_heads {hkv}")
+    _check("query", query, (n, hq, d), (torch.float16,), dev)
+    if out is None:
+        out = torch.zeros_like(query) if active_mask is not None else torch.empty_like(query)
+    else:
+        _check("out", out, (n, hq, d), (torch.float16,), dev)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if not scale > 0:
+        raise PagedAttentionError(f"scale must be positive, got {scale}")
+    stream = current_stream(dev)
+    lib = _capi.lib()
+
+    if query_start is None:
+        if not isinstance(block_tables, torch.Tensor) or block_tables.ndim != 2:
+            raise PagedAttentionError("block_tables must be a rank-2 [B, max_pages] int32 tensor")
+        max_pages = block_tables.shape[1]
+        _check("block_tables", block_tables, (n, max_pages), (torch.int32,), dev)
+        _check("sequence_lengths", sequence_lengths, (n,), (torch.int32,), dev)
+        if active_mask is not None:
+            _check("active_mask", active_mask, (n,), (torch.bool, torch.uint8), dev)
+        if max_pages < 1:
+            raise PagedAttentionError("block_tables must have at least one column")
+        cap = max_pages * bs
+        msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
+        if msl < 0:
+            raise PagedAttentionError("max_seq_len must be non-negative")
+        if n == 0:
+            return out
+        nbytes = lib.ifn_paged_decode_workspace_bytes(n, hq, hkv, d, bs, msl)
+        ws = workspace_for(dev, stream, nbytes)
+        _capi.call("ifn_paged_decode", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables),
+                   max_pages, ptr(sequence_lengths), ptr(active_mask), n, hq, hkv, d, bs, msl,
+                   float(scale), ptr(ws), ws.numel(), stream)
+        return out
+
+    # chunked prefill of one sequence
+    query_start = int(query_start)
+    if query_start < 0:
+        raise PagedAttentionError(f"query_start must be non-negative, got {query_start}")
+    if not isinstance(block_tables, torch.Tensor):
+        raise PagedAttentionError("block_tables must be a torch.Tensor")
+    table = block_tables.reshape(-1) if block_tables.ndim == 2 and block_tables.shape[0] == 1 else block_tables
+    if table.ndim != 1:
+        raise PagedAttentionError("prefill block_tables must be [max_pages] or [1, max_pages]")
+    max_pages = table.shape[0]
+    _check("block_tables", table, (max_pages,), (torch.int32,), dev)
+    total = query_start + n
+    if total > max_pages * bs:
+        raise PagedAttentionError(f"query_start + T = {total} exceeds the table's {max_pages * bs} slots")
+    if isinstance(sequence_lengths, torch.Tensor) and sequence_lengths.device.type == "cpu":
+        if sequence_lengths.numel() != 1 or int(sequence_lengths.reshape(-1)[0]) != total:
+            raise PagedAttentionError(f"sequence_lengths must be [{total}] (= query_start + T)")
+    elif isinstance(sequence_lengths, (list, tuple)):
+        if list(sequence_lengths) != [total]:
+            raise PagedAttentionError(f"sequence_lengths must be [{total}] (= query_start + T)")
+    if active_mask is not None:
+        if active_mask.numel() != 1:
+            raise PagedAttentionError("prefill active_mask must have exactly one element")
+        if not bool(active_mask.reshape(-1)[0]):
+            return out
+    if n == 0:
+        return out
+    nbytes = lib.ifn_paged_prefill_workspace_bytes(n, query_start, hq, hkv, d, bs)
+    ws = workspace_for(dev, stream, nbytes)
+    _capi.call("ifn_paged_prefill", ptr(out), ptr(query), ptr(pool_layer), P, ptr(table), max_pages,
+               query_start, n, hq, hkv, d, bs, float(scale), ptr(ws), ws.numel(), stream)
+    return out

@@ -1,0 +1,104 @@
+"""C-ABI boundary checks that need no GPU: the library loads, exports every
+symbol include/infurnace_amd.h declares, and rejects bad arguments on the host
+(before any HIP call) with the documented status codes."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from infurnace_amd import _capi
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(os.path.abspath(__file__))), "include", "infurnace_amd.h")
+A = 0x10000  # a 16-byte-aligned fake device address; never dereferenced (validation fails first)
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(ifn_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    syms = declared_symbols()
+    assert syms == sorted(_capi.SIGNATURES), (syms, sorted(_capi.SIGNATURES))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _capi.lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.ifn_abi_version() == _capi.ABI_VERSION
+
+
+def test_status_strings():
+    for code in (0, -1, -2, -3, -4, -5):
+        assert _capi.status_string(code) != "unknown status"
+    assert _capi.status_string(-99) == "unknown status"
+
+
+def test_store_kv_host_validation():
+    L = _capi.lib()
+    ok = dict(pool=A, P=64, slots=A, mask=None, k=A, v=A, T=4, hkv=8, d=128, bs=16)
+
+    def call(**kw):
+        a = {**ok, **kw}
+        return L.ifn_store_kv(a["pool"], a["P"], a["slots"], a["mask"], a["k"], a["v"], a["T"], a["hkv"],
+                              a["d"], a["bs"], None)
+
+    assert call(pool=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(slots=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(P=0) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(T=-1) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(d=12) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(k=A + 8) == _capi.IFN_ERR_ALIGNMENT
+    assert call(pool=A + 2) == _capi.IFN_ERR_ALIGNMENT
+    assert call(T=0) == _capi.IFN_OK  # nothing to launch
+    assert L.ifn_store_kv_layers(A, 0, 64, A, None, A, A, 4, 8, 128, 16, None) == _capi.IFN_ERR_INVALID_ARGUMENT
+
+
+def test_paged_decode_host_validation():
+    L = _capi.lib()
+    base = dict(out=A, q=A, pool=A, P=1024, bt=A, W=256, sl=A, am=None, B=32, hq=16, hkv=8, d=128, bs=16,
+                msl=4096, scale=0.0, ws=None, wsb=0)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return L.ifn_paged_decode(a["out"], a["q"], a["pool"], a["P"], a["bt"], a["W"], a["sl"], a["am"], a["B"],
+                                  a["hq"], a["hkv"], a["d"], a["bs"], a["msl"], a["scale"], a["ws"], a["wsb"], None)
+
+    assert call(out=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(hq=12, hkv=8) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(bs=32) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(hq=24) == _capi.IFN_ERR_UNSUPPORTED  # group 3 not compiled
+    assert call(d=96) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(q=A + 4) == _capi.IFN_ERR_ALIGNMENT
+    assert call() == _capi.IFN_ERR_WORKSPACE  # multi-partition launch without a workspace
+    need = L.ifn_paged_decode_workspace_bytes(32, 16, 8, 128, 16, 4096)
+    assert call(ws=A, wsb=need - 1) == _capi.IFN_ERR_WORKSPACE
+    assert call(B=0) == _capi.IFN_OK
+
+
+def test_workspace_sizes():
+    L = _capi.lib()
+    small = L.ifn_paged_decode_workspace_bytes(1, 16, 8, 128, 16, 512)
+    big = L.ifn_paged_decode_workspace_bytes(256, 16, 8, 128, 16, 8192)
+    assert 0 < small < big and big % 256 == 0
+    assert L.ifn_paged_decode_workspace_bytes(0, 16, 8, 128, 16, 512) == 0
+    # partials: 256 rows x 16 heads x (parts) x (128 + 2) floats must fit
+    assert big >= 256 * 16 * 2 * 130 * 4
+    assert L.ifn_paged_prefill_workspace_bytes(512, 1536, 16, 8, 128, 16) > 0
+
+
+def test_python_wrappers_reject_host_tensors():
+    torch = pytest.importorskip("torch")
+    from infurnace_amd.kernels import KVStoreError, PagedAttentionError, paged_attention, store_kv
+    pool = torch.zeros(2, 4, 16, 8, 128, dtype=torch.float16)
+    k = torch.zeros(1, 8, 128, dtype=torch.float16)
+    with pytest.raises(KVStoreError):
+        store_kv(pool, torch.zeros(1, dtype=torch.int32), None, k, k)
+    with pytest.raises(PagedAttentionError):
+        paged_attention(torch.zeros(1, 16, 128, dtype=torch.float16), pool, torch.zeros(1, 4, dtype=torch.int32),
+                        torch.ones(1, dtype=torch.int32), None)
+    with pytest.raises(KVStoreError):
+        store_kv(pool.float(), torch.zeros(1, dtype=torch.int32), None, k, k)

@@ -1,0 +1,252 @@
+"""Pins the CPU oracle (oracle/ifn_oracle.c) before it is trusted as the GPU checker.
+
+Each check is chosen so a plausible oracle bug fails it: a wrong rounding mode
+(numpy IEEE binary16), a wrong page/offset split (closed-form and brute-force
+slot walks), a wrong GQA head mapping or scale (torch SDPA with enable_gqa), an
+off-by-one causal bound (explicit position mask; decode == last prefill row),
+a dropped normalisation (closed forms: one key -> V row, equal keys -> mean V).
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+
+BS = 16
+
+
+# ---------------------------------------------------------------- fp16 conversions
+def test_half_to_float_exhaustive():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16).view(np.float16)
+    got = oracle.half_to_float(h)
+    ref = h.astype(np.float32)
+    nan = np.isnan(ref)
+    assert np.array_equal(got.view(np.uint32)[~nan], ref.view(np.uint32)[~nan])
+    assert np.isnan(got[nan]).all()
+
+
+def test_float_to_half_rne_ties_and_ranges():
+    rng = np.random.default_rng(0)
+    x = (rng.standard_normal(1 << 18).astype(np.float32)
+         * np.float32(2.0) ** rng.integers(-30, 17, 1 << 18).astype(np.float32))
+    h = np.arange(0, 0x7C00, dtype=np.uint32).astype(np.uint16).view(np.float16).astype(np.float64)
+    mids = ((h[:-1] + h[1:]) / 2).astype(np.float32)  # exact ties between adjacent halves
+    assert np.array_equal(mids.astype(np.float64), (h[:-1] + h[1:]) / 2)
+    edge = np.asarray([0.0, -0.0, 65504.0, 65519.996, 65520.0, 1e9, -1e9, 2.0 ** -24, 2.0 ** -25,
+                       2.0 ** -25 * 1.0000001, 2.0 ** -26, 6.1e-5, np.inf, -np.inf], np.float32)
+    allx = np.concatenate([x, mids, -mids, edge])
+    with np.errstate(over="ignore"):
+        ref = allx.astype(np.float16)
+    got = oracle.float_to_half(allx)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+# ---------------------------------------------------------------- slot mapping
+def test_slot_mapping_closed_form_and_walk():
+    rng = np.random.default_rng(1)
+    B, W = 5, 9
+    table = rng.permutation(200)[: B * W].astype(np.int32).reshape(B, W)
+    seq = rng.integers(0, B, 300).astype(np.int32)
+    pos = rng.integers(0, W * BS, 300).astype(np.int32)
+    got = oracle.slot_mapping(table, seq, pos, BS)
+    assert np.array_equal(got, table[seq, pos // BS] * BS + pos % BS)
+    # brute force: enumerate every slot of each row in logical order, then index by position
+    walks = [[p * BS + o for p in table[b] for o in range(BS)] for b in range(B)]
+    assert got.tolist() == [walks[s][p] for s, p in zip(seq, pos)]
+    with pytest.raises(ValueError):
+        oracle.slot_mapping(table, seq[:1], np.asarray([W * BS], np.int32), BS)
+
+
+# ---------------------------------------------------------------- store_kv
+def _rand16(rng, *shape):
+    return rng.standard_normal(shape, dtype=np.float32).astype(np.float16)
+
+
+def test_store_kv_equals_dense_scatter_and_spares_other_pages():
+    rng = np.random.default_rng(2)
+    P, hkv, d, T = 12, 4, 64, 40
+    pool = _rand16(rng, 2, P, BS, hkv, d)
+    before = pool.copy()
+    slots = rng.permutation(P * BS)[:T].astype(np.int32)
+    slots[3] = -1              # negative slot: skipped
+    slots[7] = P * BS + 5      # beyond the pool: skipped
+    active = rng.random(T) > 0.25
+    k, v = _rand16(rng, T, hkv, d), _rand16(rng, T, hkv, d)
+    oracle.store_kv(pool, slots, active, k, v)
+    exp = before.copy()
+    flat = exp.reshape(2, P * BS, hkv, d)
+    for t in range(T):
+        if active[t] and 0 <= slots[t] < P * BS:
+            flat[0, slots[t]] = k[t]
+            flat[1, slots[t]] = v[t]
+    assert np.array_equal(pool.view(np.uint16), exp.view(np.uint16))
+    written = {int(s) // BS for t, s in enumerate(slots) if active[t] and 0 <= s < P * BS}
+    for p in set(range(P)) - written:  # sentinel pages bit-identical
+        assert np.array_equal(pool[:, p].view(np.uint16), before[:, p].view(np.uint16))
+
+
+def test_paged_store_gather_equals_contiguous_cache():
+    """Paged write then block-table gather == the contiguous cache of buffers.py:24-45 (model.py:134-137)."""
+    rng = np.random.default_rng(3)
+    P, hkv, d, L = 20, 2, 32, 70
+    table = rng.permutation(P)[: -(-L // BS)].astype(np.int32)[None]
+    pool = np.zeros((2, P, BS, hkv, d), np.float16)
+    contiguous = np.zeros((2, L, hkv, d), np.float16)
+    k, v = _rand16(rng, L, hkv, d), _rand16(rng, L, hkv, d)
+    for start in range(0, L, 17):  # chunked appends
+        n = min(17, L - start)
+        pos = np.arange(start, start + n, dtype=np.int32)
+        sl = oracle.slot_mapping(table, np.zeros(n, np.int32), pos, BS)
+        oracle.store_kv(pool, sl, None, k[start:start + n], v[start:start + n])
+        contiguous[0, start:start + n], contiguous[1, start:start + n] = k[start:start + n], v[start:start + n]
+    gathered = pool[:, table[0]].reshape(2, -1, hkv, d)[:, :L]
+    assert np.array_equal(gathered.view(np.uint16), contiguous.view(np.uint16))
+
+
+# ---------------------------------------------------------------- attention
+def _case(rng, B, hq, hkv, d, lens, P=None, tail=False):
+    pages = [-(-int(L) // BS) for L in lens]
+    P = P or sum(pages) + 3
+    W = max(pages)
+    perm = rng.permutation(P).astype(np.int32)
+    table = np.zeros((B, W), np.int32)
+    off = 0
+    for b in range(B):
+        table[b, :pages[b]] = perm[off:off + pages[b]]
+        off += pages[b]
+    pool = _rand16(rng, 2, P, BS, hkv, d)
+    if tail:
+        pool = (pool.astype(np.float32) * np.where(rng.random(pool.shape) < 0.05, 8, 1)).astype(np.float16)
+    return pool, table, np.asarray(lens, np.int32)
+
+
+def _gather(pool, table, b, L):
+    kv = pool[:, table[b]].reshape(2, -1, pool.shape[3], pool.shape[4])[:, :L]
+    return kv[0], kv[1]  # [L, Hkv, D] each
+
+
+def _sdpa64(q, k, v, mask=None, scale=None):
+    """torch SDPA in float64 on CPU with GQA. q [T,Hq,D], k/v [L,Hkv,D]."""
+    tq = torch.from_numpy(q.astype(np.float64)).transpose(0, 1)[None]
+    tk = torch.from_numpy(k.astype(np.float64)).transpose(0, 1)[None]
+    tv = torch.from_numpy(v.astype(np.float64)).transpose(0, 1)[None]
+    m = None if mask is None else torch.from_numpy(mask)
+    o = torch.nn.functional.scaled_dot_product_attention(tq, tk, tv, attn_mask=m, enable_gqa=True, scale=scale)
+    return o[0].transpose(0, 1).numpy()
+
+
+def _fp16_close(got16, ref64):
+    """Within one fp16 ulp of the float64 reference (the oracle rounds once at the end)."""
+    g = got16.astype(np.float64)
+    ulp = np.maximum(np.abs(ref64), 2.0 ** -14) * 2.0 ** -10
+    assert np.all(np.abs(g - ref64) <= ulp + 1e-6), float(np.max(np.abs(g - ref64) / (ulp + 1e-6)))
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (4, 4, 64), (8, 1, 32)])
+def test_decode_matches_torch_sdpa_gqa(hq, hkv, d):
+    rng = np.random.default_rng(hq * 100 + hkv + d)
+    lens = [1, 15, 16, 17, 100, 257]
+    pool, table, sl = _case(rng, len(lens), hq, hkv, d, lens, tail=True)
+    q = _rand16(rng, len(lens), hq, d)
+    out = oracle.paged_attention(q, pool, table, sl)
+    for b, L in enumerate(lens):
+        k, v = _gather(pool, table, b, L)
+        _fp16_close(out[b], _sdpa64(q[b][None], k, v)[0])
+
+
+def test_prefill_matches_torch_sdpa_with_position_mask():
+    rng = np.random.default_rng(7)
+    hq, hkv, d, start, T = 16, 8, 128, 45, 38
+    pool, table, _ = _case(rng, 1, hq, hkv, d, [start + T])
+    q = _rand16(rng, 1, T, hq, d)
+    out = oracle.paged_attention(q, pool, table, np.asarray([start + T], np.int32))
+    k, v = _gather(pool, table, 0, start + T)
+    key_pos = np.arange(start + T)
+    query_pos = np.arange(start, start + T)
+    mask = key_pos[None, :] <= query_pos[:, None]  # model.py:128-132
+    _fp16_close(out[0], _sdpa64(q[0], k, v, mask=mask))
+
+
+def test_float64_brute_force_tiny():
+    rng = np.random.default_rng(8)
+    hq, hkv, d, L = 4, 2, 8, 21
+    pool, table, sl = _case(rng, 1, hq, hkv, d, [L])
+    q = _rand16(rng, 1, hq, d)
+    scale = 0.37
+    out = oracle.paged_attention(q, pool, table, sl, scale=scale)
+    k, v = _gather(pool, table, 0, L)
+    for h in range(hq):
+        g = h // (hq // hkv)
+        s = [scale * sum(float(q[0, h, i]) * float(k[j, g, i]) for i in range(d)) for j in range(L)]
+        mx = max(s)
+        w = [math.exp(x - mx) for x in s]
+        ref = np.asarray([sum(w[j] * float(v[j, g, i]) for j in range(L)) / sum(w) for i in range(d)])
+        _fp16_close(out[0, h], ref)
+
+
+def test_closed_forms():
+    rng = np.random.default_rng(9)
+    hq, hkv, d = 4, 2, 64
+    # one key: the output is exactly the V row (p = 1)
+    pool, table, sl = _case(rng, 1, hq, hkv, d, [1])
+    q = _rand16(rng, 1, hq, d)
+    out = oracle.paged_attention(q, pool, table, sl)
+    k, v = _gather(pool, table, 0, 1)
+    for h in range(hq):
+        assert np.array_equal(out[0, h].view(np.uint16), v[0, h // 2].view(np.uint16))
+    # all keys equal: uniform weights -> mean of V
+    L = 40
+    pool, table, sl = _case(rng, 1, hq, hkv, d, [L])
+    kv = pool[:, table[0]].reshape(2, -1, hkv, d)
+    kv[0, :] = kv[0, 0]
+    pool[:, table[0]] = kv.reshape(2, -1, BS, hkv, d)
+    out = oracle.paged_attention(q, pool, table, sl)
+    _, v = _gather(pool, table, 0, L)
+    for h in range(hq):
+        _fp16_close(out[0, h], v[:, h // 2].astype(np.float64).mean(0))
+    # one dominant logit selects its V row
+    pool, table, sl = _case(rng, 1, 2, 1, d, [33])
+    qq = np.zeros((1, 2, d), np.float16)
+    qq[0, :, 0] = 1.0
+    kv = pool[:, table[0]].reshape(2, -1, 1, d)
+    kv[0, :, 0, 0] = 0.0
+    kv[0, 20, 0, 0] = 2000.0
+    pool[:, table[0]] = kv.reshape(2, -1, BS, 1, d)
+    out = oracle.paged_attention(qq, pool, table, sl)
+    assert np.array_equal(out[0, 0].view(np.uint16), kv[1, 20, 0].view(np.uint16))
+
+
+def test_invariant_to_physical_page_order_and_chunking():
+    rng = np.random.default_rng(10)
+    hq, hkv, d, L = 16, 8, 128, 150
+    pool, table, sl = _case(rng, 1, hq, hkv, d, [L])
+    q = _rand16(rng, 1, L, hq, d)
+    full = oracle.paged_attention(q, pool, table, sl)
+    # relabel physical pages: same logical content, different ids
+    perm = rng.permutation(pool.shape[1])
+    pool2 = np.empty_like(pool)
+    pool2[:, perm] = pool
+    table2 = perm[table].astype(np.int32)
+    assert np.array_equal(oracle.paged_attention(q, pool2, table2, sl).view(np.uint16), full.view(np.uint16))
+    # chunked prefill == unchunked (reference tests/test_cached_forward.py:107-117)
+    parts = [oracle.paged_attention(q[:, s:e], pool, table, np.asarray([e], np.int32))
+             for s, e in [(0, 50), (50, 51), (51, 150)]]
+    assert np.array_equal(np.concatenate(parts, 1).view(np.uint16), full.view(np.uint16))
+    # decode at position L-1 == last row of the causal prefill
+    dec = oracle.paged_attention(q[:, -1], pool, table, sl)
+    assert np.array_equal(dec.view(np.uint16), full[:, -1].view(np.uint16))
+
+
+def test_inactive_rows_untouched_and_bad_tables_rejected():
+    rng = np.random.default_rng(11)
+    pool, table, sl = _case(rng, 3, 4, 2, 32, [5, 9, 30])
+    q = _rand16(rng, 3, 4, 32)
+    prior = _rand16(rng, 3, 4, 32)
+    out = oracle.paged_attention(q, pool, table, sl, active_mask=np.asarray([1, 0, 1], bool), out=prior)
+    assert np.array_equal(out[1].view(np.uint16), prior[1].view(np.uint16))
+    bad = table.copy()
+    bad[0, 0] = pool.shape[1]
+    with pytest.raises(ValueError):
+        oracle.paged_attention(q, pool, bad, sl)
