@@ -56,6 +56,40 @@ __device__ __forceinline__ float sum8(float x) {
 
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---- split-KV merge protocol shared by decode and prefill ------------------------------
+// Every workspace starts with a fixed ticket area (independent of the call's shapes, so a
+// workspace can serve calls of any shape in sequence).  It must be zero when the workspace
+// is created; each call returns the tickets it used to zero.  Partial results follow it.
+constexpr size_t kTicketBytes = size_t(256) << 10;
+constexpr int64_t kMaxTickets = int64_t(kTicketBytes / sizeof(uint32_t));
+
+// Device-coherent (agent scope) scalar store / load.  They compile to global_store/load
+// with the sc1 bit: written through to, and read from, the device coherence point, so
+// partials written on one XCD are seen by a workgroup on another without an L2
+// write-back or invalidate (which a __threadfence() would issue on every workgroup).
+__device__ __forceinline__ void st_dev(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float ld_dev(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Called by all threads after their st_dev partial stores.  Waits until every store of
+// the workgroup is acknowledged, then one thread takes a ticket; returns true in the
+// workgroup that arrives last (ticket == last), which then merges with ld_dev.
+__device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t last, uint32_t* s_ticket) {
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): stores acknowledged
+  __syncthreads();
+  if (threadIdx.x == 0)
+    *s_ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  return *s_ticket == last;
+}
+
+__device__ __forceinline__ void reset_ticket(uint32_t* counter) {
+  __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
 }  // namespace ifn
 
 // Host-side helpers shared by the entry points.

@@ -60,9 +60,10 @@ struct DecodeWorkspace {
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-static inline size_t decode_ws_layout(int32_t batch, int32_t hq, int32_t hkv, int32_t d,
-                                      int32_t max_parts, size_t* off_ml, size_t* off_o) {
-  size_t off = align256(size_t(batch) * hkv * sizeof(uint32_t));
+// Workspace: [tickets: kTicketBytes][ml][o]; the ticket area is shape-independent.
+static inline size_t decode_ws_layout(int32_t batch, int32_t hq, int32_t d, int32_t max_parts,
+                                      size_t* off_ml, size_t* off_o) {
+  size_t off = kTicketBytes;
   *off_ml = off;
   off = align256(off + size_t(batch) * hq * max_parts * 2 * sizeof(float));
   *off_o = off;
@@ -260,38 +261,33 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       out_bh[i] = f16(L > 0.f ? O / L : 0.f);
     } else {
       const int64_t slot = (bh0 + g) * max_parts + part;
-      ws.o[slot * D + d] = O;
+      st_dev(ws.o + slot * D + d, O);
       if (d == 0) {
-        ws.ml[slot * 2 + 0] = mx;
-        ws.ml[slot * 2 + 1] = L;
+        st_dev(ws.ml + slot * 2 + 0, mx);
+        st_dev(ws.ml + slot * 2 + 1, L);
       }
     }
   }
   if (nparts == 1) return;
 
   // Fused split-KV merge: the last partition to finish merges all of them.
-  __threadfence();
-  __syncthreads();
   uint32_t* counter = ws.count + int64_t(b) * num_kv_heads + kvh;
-  if (tid == 0) s_ticket = atomicAdd(counter, 1u);
-  __syncthreads();
-  if (s_ticket != uint32_t(nparts - 1)) return;
-  __threadfence();
+  if (!arrive_last(counter, uint32_t(nparts - 1), &s_ticket)) return;
   for (int i = tid; i < G * D; i += kDecodeThreads) {
     const int g = i / D;
     const int d = i % D;
     const int64_t base = (bh0 + g) * max_parts;
     float mx = kNegBig;
-    for (int pp = 0; pp < nparts; ++pp) mx = fmaxf(mx, ws.ml[(base + pp) * 2]);
+    for (int pp = 0; pp < nparts; ++pp) mx = fmaxf(mx, ld_dev(ws.ml + (base + pp) * 2));
     float L = 0.f, O = 0.f;
     for (int pp = 0; pp < nparts; ++pp) {
-      const float wt = exp2_fast(ws.ml[(base + pp) * 2] - mx);
-      L = fmaf(wt, ws.ml[(base + pp) * 2 + 1], L);
-      O = fmaf(wt, ws.o[(base + pp) * D + d], O);
+      const float wt = exp2_fast(ld_dev(ws.ml + (base + pp) * 2) - mx);
+      L = fmaf(wt, ld_dev(ws.ml + (base + pp) * 2 + 1), L);
+      O = fmaf(wt, ld_dev(ws.o + (base + pp) * D + d), O);
     }
     out_bh[i] = f16(L > 0.f ? O / L : 0.f);
   }
-  if (tid == 0) atomicExch(counter, 0u);
+  if (tid == 0) reset_ticket(counter);
 }
 
 typedef void (*DecodeKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t,
@@ -322,7 +318,7 @@ extern "C" size_t ifn_paged_decode_workspace_bytes(int32_t batch, int32_t num_q_
       max_seq_len < 0)
     return 0;
   size_t off_ml, off_o;
-  return ifn::decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim,
+  return ifn::decode_ws_layout(batch, num_q_heads, head_dim,
                                ifn::decode_max_parts(batch, num_kv_heads, max_seq_len), &off_ml,
                                &off_o);
 }
@@ -353,8 +349,8 @@ extern "C" int ifn_paged_decode(void* out, const void* query, const void* kv_poo
   const int ppp = decode_pages_per_part(batch, num_kv_heads, len_cap);
   const int max_parts = int(ceil_div(ceil_div(len_cap > 0 ? len_cap : 1, kBlock), ppp));
   size_t off_ml, off_o;
-  const size_t need = decode_ws_layout(batch, num_q_heads, num_kv_heads, head_dim, max_parts,
-                                       &off_ml, &off_o);
+  const size_t need = decode_ws_layout(batch, num_q_heads, head_dim, max_parts, &off_ml, &off_o);
+  if (int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
   if (max_parts > 1) {
     if (workspace == nullptr || workspace_bytes < need) return IFN_ERR_WORKSPACE;
     IFN_CHECK_ALIGN16(workspace);
