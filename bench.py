@@ -37,6 +37,7 @@ sys.path.insert(0, ROOT)
 
 METRIC = "paged-decode attn HBM GB/s (% of peak) + KV-append µs/layer, Qwen3-0.6B B=32"
 HBM_PEAK_GBPS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_config2_traffic.json")
 
 
@@ -117,6 +118,61 @@ def _cpu_model() -> str:
     return "unknown"
 
 
+def run_prefill(lib, hip, dev, g, stream) -> dict:
+    """Config 3: 2048-token prompt as four 512-token chunks over 28 layers; per chunk-layer
+    store_kv (512 tokens) then causal paged attention (MFMA).  Times every attention launch."""
+    import torch
+    from infurnace_amd import workloads
+    w = workloads.config3()
+    L, hq, hkv, d, C = w.num_layers, w.num_q_heads, w.num_kv_heads, w.head_dim, w.chunk
+    pool = torch.empty((L, 2, w.num_pages, 16, hkv, d), dtype=torch.float16, device=dev).normal_(generator=g)
+    q = torch.randn((L, 4, C, hq, d), generator=g, device=dev, dtype=torch.float16)
+    k = torch.randn((L, 4, C, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    v = torch.randn((L, 4, C, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty((C, hq, d), dtype=torch.float16, device=dev)
+    table = torch.from_numpy(w.block_table).to(dev)
+    pos = np.arange(w.prompt_len)
+    slots = torch.from_numpy((w.block_table.astype(np.int64)[pos // 16] * 16 + pos % 16).astype(np.int32)).to(dev)
+    ws_bytes = max(lib.ifn_paged_prefill_workspace_bytes(C, c * C, hq, hkv, d, 16) for c in range(4))
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    lb = pool[0].numel() * 2
+    scale = 1.0 / np.sqrt(d)
+
+    def one_pass(evs=None):
+        j = 0
+        for layer in range(L):
+            for c in range(4):
+                rc = lib.ifn_store_kv(pool.data_ptr() + layer * lb, w.num_pages, slots.data_ptr() + 4 * c * C, None,
+                                      k[layer, c].data_ptr(), v[layer, c].data_ptr(), C, hkv, d, 16, stream)
+                if evs is not None:
+                    hip.hip.hipEventRecord(evs[2 * j], stream)
+                rc |= lib.ifn_paged_prefill(out.data_ptr(), q[layer, c].data_ptr(), pool.data_ptr() + layer * lb,
+                                            w.num_pages, table.data_ptr(), w.block_table.shape[0], c * C, C, hq, hkv,
+                                            d, 16, scale, ws.data_ptr(), ws_bytes, stream)
+                if evs is not None:
+                    hip.hip.hipEventRecord(evs[2 * j + 1], stream)
+                if rc:
+                    raise RuntimeError(f"prefill launch failed: {rc}")
+                j += 1
+
+    one_pass()
+    torch.cuda.synchronize()
+    evs = hip.create(2 * L * 4)
+    one_pass(evs)
+    torch.cuda.synchronize()
+    ms = np.asarray([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(L * 4)]).reshape(L, 4)
+    hip.destroy(evs)
+    flops = np.asarray([w.chunk_flops(c) for c in range(4)], np.float64)
+    per_chunk_us = ms.mean(0) * 1e3
+    tflops = float(flops.sum() * L / (ms.sum() / 1e3) / 1e12)
+    return {"workload": w.name + ", 28 layers, store_kv + causal paged attention per chunk-layer",
+            "attn_us_per_chunk_layer": [round(float(x), 2) for x in per_chunk_us],
+            "attn_us_per_layer": round(float(ms.sum(1).mean() * 1e3), 2),
+            "gflop_per_layer": round(float(flops.sum() / 1e9), 3),
+            "TFLOP/s": round(tflops, 2), "mfma_peak_TFLOP/s": MFMA_F16_PEAK_TFLOPS,
+            "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -124,7 +180,14 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 chunked-prefill leg")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="short run for rocprofv3 counter passes: no CPU baseline, no prefill leg, plus one "
+                         "1 GiB elementwise copy (torch.neg) whose FETCH/WRITE counters calibrate HBM bytes")
     args = ap.parse_args()
+    if args.profile_pass:
+        args.no_cpu_baseline = True
+        args.no_prefill = True
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the hot path shards by sequence "
               "with no exchange, so N GPUs run N independent copies of this benchmark.", file=sys.stderr)
@@ -233,6 +296,17 @@ def main() -> int:
     a_gbps = a_bytes / (a_ms / 1e3) / 1e9
     del pool3, k3, v3
 
+    prefill = None
+    if not args.no_prefill:
+        prefill = run_prefill(lib, hip, dev, g, stream)
+
+    if args.profile_pass:
+        src = torch.empty(1 << 29, dtype=torch.float16, device=dev).normal_(generator=g)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)  # reads 1 GiB, writes 1 GiB: the counters' calibration kernel
+        torch.cuda.synchronize()
+        del src, dst
+
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
@@ -263,6 +337,7 @@ def main() -> int:
         "append_batched": {"workload": "store_kv_layers, 28 layers x 2048 tokens (config 3 prompt), one launch",
                            "us": round(a_ms * 1e3, 2), "bytes": a_bytes, "GB/s": round(a_gbps, 2),
                            "frac": round(a_gbps / HBM_PEAK_GBPS, 4)},
+        "prefill": prefill,
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

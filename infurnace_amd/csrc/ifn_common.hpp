@@ -54,6 +54,18 @@ __device__ __forceinline__ float sum8(float x) {
   return x;
 }
 
+// Butterfly reductions over the 64 lanes of a wavefront; every lane gets the result.
+__device__ __forceinline__ float wave_max(float x) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) x = fmaxf(x, __shfl_xor(x, o));
+  return x;
+}
+__device__ __forceinline__ float wave_sum(float x) {
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) x += __shfl_xor(x, o);
+  return x;
+}
+
 __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 // ---- split-KV merge protocol shared by decode and prefill ------------------------------
@@ -84,6 +96,14 @@ __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t last, ui
     *s_ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   return *s_ticket == last;
+}
+
+// Wave-level variant: each wavefront publishes and merges on its own (no workgroup barrier).
+__device__ __forceinline__ bool wave_arrive_last(uint32_t* counter, uint32_t last, int lane) {
+  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores acknowledged
+  uint32_t t = 0;
+  if (lane == 0) t = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return uint32_t(__builtin_amdgcn_readfirstlane(int(t))) == last;
 }
 
 __device__ __forceinline__ void reset_ticket(uint32_t* counter) {

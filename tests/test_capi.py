@@ -77,6 +77,8 @@ def test_paged_decode_host_validation():
     need = L.ifn_paged_decode_workspace_bytes(32, 16, 8, 128, 16, 4096)
     assert call(ws=A, wsb=need - 1) == _capi.IFN_ERR_WORKSPACE
     assert call(B=0) == _capi.IFN_OK
+    # beyond 64 partitions of 64 pages (65,536 tokens) a row is not supported
+    assert call(W=8192, msl=65536 + 16) == _capi.IFN_ERR_UNSUPPORTED
 
 
 def test_workspace_sizes():

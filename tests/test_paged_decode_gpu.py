@@ -206,3 +206,12 @@ def test_config5_prefix_shared_with_churn(dev):
         out = paged_attention(q, pool, to_dev(table, dev), to_dev(w.seq_lens, dev), None)
         rows = [0, 31, 63]
         assert_attn_close(out[rows], oracle_decode(pool, table, w.seq_lens, q, rows=rows), f"config5 step {step}")
+
+
+def test_long_context_uses_many_partitions(dev):
+    """A 60,000-token row splits into 64 partitions (the merge bound) beside a short row."""
+    say("decode long context 60000")
+    rng = np.random.default_rng(15)
+    pool, table, lens, q = _ragged(rng, [60000, 1000], 16, 8, 128)
+    out = paged_attention(to_dev(q, dev), to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev), None)
+    assert_attn_close(out, oracle.paged_attention(q, pool, table, lens), "long context")
