@@ -1,4 +1,4 @@
-// Paged GQA decode attention (one query token per sequence), split-KV, gfx950.
+// Paged GQA decode attention (one query token per sequence), gfx950.
 //
 // Replaces the reference's documented paged_attention for decode
 // (docs/architecture.md:246; placeholder src/infurnace/kernels/paged_attention.py)
@@ -6,339 +6,442 @@
 // read positions [0, pos], upcast fp16 K/V to fp32, scaled_dot_product_attention
 // with scale 1/sqrt(head_dim) and query head h -> kv head h / group.
 //
-// Decode is HBM-bound (about 2 FLOP per KV byte), so the design is about
-// reading every K/V byte exactly once, in DRAM-friendly order, with enough bytes
-// in flight:
+// Decode is HBM-bound (about 2 FLOP per KV byte); the kernel is built so every
+// CU streams the same number of K/V bytes at a steady rate:
 //
-//  * Workgroup = (partition of pages_per_part pages, sequence, group of 4 kv
-//    heads); wavefront w serves one kv head and all G query heads that read it,
-//    streaming every page of the partition.  Small workgroups let several share
-//    a CU, so one's prologue overlaps another's streaming.  Ragged sequences
-//    launch only the partitions they own (the rest exit at once).
+//  * Balanced flat split.  The work is the list of (row, kv head, page) units
+//    in that order -- Hkv * sum(ceil(len/16)) units of 8 KiB (one kv head's
+//    16 K rows + 16 V rows).  The grid is one 8-wave workgroup per CU (an
+//    84 KiB LDS table keeps the dispatcher at one workgroup per CU) and wave w
+//    of N takes units [w*U/N, (w+1)*U/N).  Ragged batches therefore cost every
+//    CU the same bytes; no CU idles while another streams a long row.  Each
+//    workgroup rebuilds the per-row page prefix sums in LDS from seq_lens.
+//  * A wave streams its units through an S-stage register ring: unit k+S-1 is
+//    requested while unit k is consumed, across row/head boundaries, with the
+//    next segment's query prefetched.  Page ids and unit metadata sit one per
+//    lane (64 units per window) and are read with v_readlane.
 //  * Each K/V page is fetched once and reused from registers by every query
-//    head of its GQA group.
-//  * Inside a page (16 tokens x head_dim), lane = 8*row + col: the 8 lanes of
-//    a row read one token's K row as 16 B chunks col, col+8, ..., i.e. every
-//    load instruction reads 8 tokens x 128 contiguous bytes.  Each lane holds
-//    2 tokens (row, row+8).  Page ids come from lanes via v_readlane; page k+1
-//    is in flight while page k is consumed.
-//  * q.k uses v_dot2_f32_f16 (fp16 pairs, fp32 accumulation); the 8 partial
-//    sums of a token are reduced with three DPP steps inside the row
-//    (quad_perm xor1, quad_perm xor2, row_half_mirror) -- no LDS traffic.
-//  * Online softmax in base 2 (scores pre-multiplied by scale*log2 e,
-//    v_exp_f32), kept per (lane row, head); rows merge once per partition with
-//    lane shuffles.  No LDS and no workgroup barrier at all.
-//  * Split-KV merge is fused: every partition's wave writes (m, l, o) to the
-//    workspace with device-coherent stores, then takes a ticket from a
-//    per-(sequence, kv head) counter; the last one merges all partitions
-//    (log-sum-exp weights), writes fp16 out and re-zeroes the counter.  No
+//    head of its GQA group.  Inside a page, lane = 8*row + col: every load
+//    instruction reads 8 token rows x 128 contiguous bytes; each lane holds 2
+//    tokens.  q.k uses v_dot2_f32_f16 (fp32 accumulation) and three DPP steps
+//    inside the row; the online softmax runs in base 2 per (lane row, head) and
+//    rows merge once per piece with lane shuffles.  No LDS traffic in the loop.
+//  * A (row, kv head) segment split over several waves (at most the first and
+//    last piece of each wave's range) is merged log-sum-exp style by the wave
+//    that finishes last: partials go out with device-coherent stores during
+//    the stream, and the tickets are taken once, at the end of the wave.  No
 //    second launch, no wait loop.
 #include "ifn_common.hpp"
 
+#include <atomic>
+
 namespace ifn {
 
-constexpr int kBlock = 16;           // tokens per page compiled in
-constexpr int kHeadsPerBlock = 4;    // wavefronts per workgroup, one per kv head
-constexpr int kDecodeThreads = kHeadsPerBlock * kWave;
-constexpr int kMaxPagesPerPart = 64; // page ids of a partition live in one lane each
+constexpr int kBlock = 16;               // tokens per page compiled in
+constexpr int kWavesPerBlock = 8;
+constexpr int kDecodeThreads = kWavesPerBlock * kWave;
+constexpr int kPrefixInts = 21 * 1024;   // 84 KiB of LDS: one workgroup per CU
+constexpr int kMaxBatch = kPrefixInts - 1;
+constexpr int kMaxWaves = 1024 * kWavesPerBlock;  // waves of a launch are capped at this
+constexpr int kXcds = 8;            // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 
-// Pages per partition.  Each wave streams all pages of its partition for one kv head, so
-// the partition length is the per-wave stream length: long enough to amortise the
-// prologue/epilogue, short enough that ragged batches still spread over the CUs.
-static inline int decode_pages_per_part(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
-  const int64_t seq_pages = ceil_div(max_seq_len > 0 ? max_seq_len : 1, kBlock);
-  // about 4096 waves over the launch, counting a ragged batch at half its longest row
-  int64_t ppp = ceil_div(ceil_div(seq_pages, 2) * int64_t(batch) * num_kv_heads, 4096);
-  if (ppp < 8) ppp = 8;
-  // the merge holds one partition per lane: at most kWave partitions per sequence
-  const int64_t min_ppp = ceil_div(seq_pages, kWave);
-  if (ppp < min_ppp) ppp = min_ppp;
-  if (ppp > kMaxPagesPerPart) ppp = kMaxPagesPerPart;
-  return int(ppp);
-}
-
-// Register-ring depth: as deep as the register budget of one 8-wave workgroup per CU allows.
+// Register-ring depth: as deep as 256 VGPRs (two waves per SIMD) allow.
 template <int D, int G>
 struct DecodeStages {
-  static constexpr int kRegsPerLane = G * (D / 64);  // accumulator chunks per lane
-  static constexpr int value = kRegsPerLane <= 4 ? 4 : (kRegsPerLane <= 8 ? 3 : 2);
+  static constexpr int kChunks = G * (D / 64);  // accumulator chunks per lane
+  static constexpr int value = kChunks <= 2 ? 4 : (kChunks <= 4 ? 3 : 2);
 };
 
 struct DecodeWorkspace {
-  uint32_t* count;  // [batch][num_kv_heads] tickets, zero between calls
-  float* ml;        // [batch][num_q_heads][max_parts][2] (running max in log2 units, sum)
-  float* o;         // [batch][num_q_heads][max_parts][head_dim] unnormalised outputs
+  uint32_t* count;  // [batch * num_kv_heads] tickets, zero between calls
+  float* ml;        // [slot][G][2]  (max in log2 units, sum); slot = segment + wave
+  float* o;         // [slot][G][head_dim] unnormalised outputs
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
-// Workspace: [tickets: kTicketBytes][ml][o]; the ticket area is shape-independent.
-static inline size_t decode_ws_layout(int32_t batch, int32_t hq, int32_t d, int32_t max_parts,
+// Workspace: [tickets: kTicketBytes][ml][o].  A launch of n waves publishes into at most
+// segments + n slots (slot = segment + range index).
+static inline size_t decode_ws_layout(int32_t batch, int32_t hkv, int32_t g, int32_t d, int64_t waves,
                                       size_t* off_ml, size_t* off_o) {
+  const size_t slots = size_t(waves) + size_t(batch) * hkv;
   size_t off = kTicketBytes;
   *off_ml = off;
-  off = align256(off + size_t(batch) * hq * max_parts * 2 * sizeof(float));
+  off = align256(off + slots * g * 2 * sizeof(float));
   *off_o = off;
-  off = align256(off + size_t(batch) * hq * max_parts * d * sizeof(float));
+  off = align256(off + slots * g * d * sizeof(float));
   return off;
 }
 
-// Grid (partition, sequence, group of 8 kv heads); wave w of a workgroup serves kv head
-// 8*blockIdx.z + w and all G query heads that read it.
+// Number of CUs of the current device (queried once per device; 0 when there is none).
+static int device_cu_count() {
+  static std::atomic<int> cache[64];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) {
+    const int c = cache[dev].load(std::memory_order_relaxed);
+    if (c > 0) return c;
+  }
+  int n = 0;
+  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
+  return n;
+}
+
+// Workgroups of a decode launch: one per CU (capped so waves <= kMaxWaves).
+static int decode_blocks() {
+  int cus = device_cu_count();
+  if (cus < 1) cus = 256;  // no device visible: size for an MI355X
+  return cus < kMaxWaves / kWavesPerBlock ? cus : kMaxWaves / kWavesPerBlock;
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
     int64_t num_pages, const int32_t* __restrict__ block_tables, int32_t max_pages,
-    const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active,
-    int32_t num_kv_heads, int32_t max_len, float scale_log2, int32_t pages_per_part,
-    DecodeWorkspace ws, int32_t max_parts) {
+    const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, int32_t batch,
+    int32_t num_kv_heads, int32_t max_len, float scale_log2, DecodeWorkspace ws) {
   constexpr int NC = D / 64;  // 16-byte chunks per lane per token row
-  const int part = blockIdx.x;
-  const int b = blockIdx.y;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
-  const int kvh = blockIdx.z * kHeadsPerBlock + wave;
-  if (kvh >= num_kv_heads) return;
-  const int lane = threadIdx.x % kWave;
+  constexpr int S = DecodeStages<D, G>::value;
+  __shared__ int s_off[kPrefixInts];  // s_off[b] = pages of rows < b; s_off[batch] = total
+  __shared__ int s_wsum[kWavesPerBlock];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
   const int hq = num_kv_heads * G;
-  const int64_t bh0 = int64_t(b) * hq + int64_t(kvh) * G;  // first query-head row
-  f16* out_bh = out + bh0 * D;
+  const int cap = min(max_pages * kBlock, max_len);
+  auto row_len = [&](int b) -> int {  // keys of row b; inactive rows have none
+    if (active != nullptr && active[b] == 0) return 0;
+    return min(seq_lens[b], cap);
+  };
 
-  if (active != nullptr && active[b] == 0) return;
-  int len = seq_lens[b];
-  len = min(len, max_pages * kBlock);
-  len = min(len, max_len);
-  if (len <= 0) {
-    if (part == 0)
-      for (int i = lane; i < G * D; i += kWave) out_bh[i] = f16(0.f);
-    return;
+  // 1. Exclusive prefix of pages per row, in LDS (every workgroup builds its own copy).
+  int running = 0;
+  for (int base = 0; base < batch; base += kDecodeThreads) {
+    const int i = base + tid;
+    int pages = 0;
+    if (i < batch) {
+      const int len = row_len(i);
+      pages = len > 0 ? (len + kBlock - 1) / kBlock : 0;
+    }
+    int x = pages;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == kWave - 1) s_wsum[wave] = x;
+    __syncthreads();
+    int wpre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kWavesPerBlock; ++w) {
+      const int v = s_wsum[w];
+      wpre += w < wave ? v : 0;
+      tot += v;
+    }
+    if (i < batch) s_off[i] = running + wpre + x - pages;
+    running += tot;
+    __syncthreads();
   }
-  const int seq_pages = int(ceil_div(len, kBlock));
-  const int nparts = int(ceil_div(seq_pages, pages_per_part));
-  if (part >= nparts) return;
-  const int p_begin = part * pages_per_part;
-  const int np = min(pages_per_part, seq_pages - p_begin);  // pages of this partition (<= 64)
+  if (tid == 0) s_off[batch] = running;
+  __syncthreads();
 
-  const int row = lane / 8;  // lane = 8*row + col: row -> tokens row and row+8 of a page
-  const int col = lane % 8;  //                     col -> 16-byte chunks col, col+8, ...
-
-  f16x8 qv[G][NC];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int ch = 0; ch < NC; ++ch)
-      qv[g][ch] = as_h8(ld16(q + bh0 * D + g * D + (col + 8 * ch) * 8));
-
-  float m[G], l[G], acc[G][NC][8];
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    m[g] = kNegBig;
-    l[g] = 0.f;
-#pragma unroll
-    for (int ch = 0; ch < NC; ++ch)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) acc[g][ch][e] = 0.f;
+  // Active rows with no keys get zeros (workgroup 0, one wave per row).
+  if (blockIdx.x == 0) {
+    for (int b = wave; b < batch; b += kWavesPerBlock) {
+      const bool live = active == nullptr || active[b] != 0;
+      if (live && min(seq_lens[b], cap) <= 0) {
+        for (int i = lane; i < hq * D; i += kWave) out[int64_t(b) * hq * D + i] = f16(0.f);
+      }
+    }
   }
 
-  const int64_t tok_stride = int64_t(num_kv_heads) * D;  // elements between token rows
+  const int64_t total_units = int64_t(running) * num_kv_heads;
+  if (total_units == 0) return;
+  const int64_t nw = min(int64_t(gridDim.x) * kWavesPerBlock, total_units);
+  // Static balanced split: range r covers units [T*r/nw, (T*(r+1))/nw), one per wave, so
+  // every wave streams the same number of 8 KiB units.  Workgroup i runs on XCD i % 8
+  // (round-robin dispatch); workgroups are remapped so that XCD x takes a contiguous
+  // eighth of the unit order.  Without the remap, consecutive workgroups -- and so each
+  // XCD -- would serve a fixed kv head, i.e. the same 256-byte column of every 2 KiB token
+  // row, and camp on a few of its L2 channels.  Range r publishes split-segment partials in
+  // slot segment + r (unique because ranges are ordered); the ranges covering a segment
+  // are [range_of(first unit), range_of(last unit)].
+  const int64_t nblk = gridDim.x;
+  const int64_t blk = nblk % kXcds == 0 ? (blockIdx.x % kXcds) * (nblk / kXcds) + blockIdx.x / kXcds
+                                        : int64_t(blockIdx.x);
+  const int64_t r_wave = blk * kWavesPerBlock + wave;
+  if (r_wave >= nw) return;
+  auto range_of = [&](int64_t u) -> int64_t { return ((u + 1) * nw - 1) / total_units; };
+
+  const int row = lane / 8;  // tokens row and row+8 of a page
+  const int col = lane % 8;  // 16-byte chunks col, col+8, ...
+  const int64_t tok_stride = int64_t(num_kv_heads) * D;
   const int64_t page_elems = kBlock * tok_stride;
   const int64_t v_off = num_pages * page_elems;
-  const f16* head_base = pool + int64_t(kvh) * D + int64_t(row) * tok_stride + col * 8;
-  // Lane k holds the physical id of the partition's k-th page (one load per partition);
-  // the page loop takes ids with v_readlane, so consecutive pages wait on no memory.
-  const int my_id = lane < np ? block_tables[int64_t(b) * max_pages + p_begin + lane] : 0;
 
-  // S-stage register ring: page k+S-1 is requested while page k is consumed, so a wave
-  // keeps S-1 pages in flight and its iteration time is about latency/(S-1) rather than
-  // a full memory round trip.  Loads past the partition clamp to its last page (an L2
-  // hit) so the load stream stays unconditional; consume() of those slots is skipped.
-  constexpr int S = DecodeStages<D, G>::value;
+  f16x8 qv[G][NC];
+  float m[G], l[G], acc[G][NC][8];
   u32x4 kb[S][2][NC], vb[S][2][NC];
   bool okb[S];
 
-  auto load_page = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool& ok) {
-    const int phys = __builtin_amdgcn_readlane(my_id, k < np ? k : np - 1);
-    ok = phys >= 0 && int64_t(phys) < num_pages;
-    const f16* kbase = head_base + int64_t(ok ? phys : 0) * page_elems;
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-      for (int ch = 0; ch < NC; ++ch) {
-        kr[tt][ch] = ld16(kbase + tt * 8 * tok_stride + ch * 64);
-        vr[tt][ch] = ld16(kbase + v_off + tt * 8 * tok_stride + ch * 64);
+  auto run_range = [&](int64_t r, int64_t u_lo, int64_t u_hi) {
+    int pend_n = 0, pend_seg0 = 0, pend_seg1 = 0, pend_first0 = 0, pend_first1 = 0, pend_np0 = 0, pend_np1 = 0;
+    for (int64_t u = u_lo; u < u_hi;) {  // one piece per iteration (uniform loop)
+      // unit u -> (row b, kv head, first page): last row whose first unit is <= u
+      int lo = 0, hi = batch - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (int64_t(s_off[mid]) * num_kv_heads <= u) lo = mid; else hi = mid - 1;
       }
-  };
+      const int b = __builtin_amdgcn_readfirstlane(lo);
+      const int pages_b = s_off[b + 1] - s_off[b];
+      const int64_t row_start = int64_t(s_off[b]) * num_kv_heads;
+      const int kvh = int((u - row_start) / pages_b);
+      const int64_t seg_start = row_start + int64_t(kvh) * pages_b;
+      const int64_t seg_end = seg_start + pages_b;
+      const int page0 = int(u - seg_start);
+      const int np = int(min(u_hi, seg_end) - u);  // pages of this piece
+      const int seg = b * num_kv_heads + kvh;
+      const int len = row_len(b);
+      u += np;
 
-  auto consume = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool ok) {
-    const int p = p_begin + k;
-    bool valid[2];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) valid[tt] = ok && (p * kBlock + row + 8 * tt) < len;
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt)
-      if (!valid[tt])
-#pragma unroll
-        for (int ch = 0; ch < NC; ++ch) vr[tt][ch] = u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      float s[2];
-#pragma unroll
-      for (int tt = 0; tt < 2; ++tt) {
-        float a = 0.f;
-#pragma unroll
-        for (int ch = 0; ch < NC; ++ch) a = dot8(qv[g][ch], as_h8(kr[tt][ch]), a);
-        a = sum8(a);
-        s[tt] = valid[tt] ? a * scale_log2 : -INFINITY;
-      }
-      const float mn = fmaxf(m[g], fmaxf(s[0], s[1]));
-      const float alpha = exp2_fast(m[g] - mn);
-      const float p0 = exp2_fast(s[0] - mn);
-      const float p1 = exp2_fast(s[1] - mn);
-      l[g] = l[g] * alpha + p0 + p1;
-      m[g] = mn;
-#pragma unroll
-      for (int ch = 0; ch < NC; ++ch) {
-        const f16x8 v0 = as_h8(vr[0][ch]);
-        const f16x8 v1 = as_h8(vr[1][ch]);
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-          acc[g][ch][e] = fmaf(p1, float(v1[e]), fmaf(p0, float(v0[e]), acc[g][ch][e] * alpha));
-      }
-    }
-  };
-
-#pragma unroll
-  for (int j = 0; j < S - 1; ++j) load_page(j, kb[j], vb[j], okb[j]);
-  int k = 0;
-  for (; k + S <= np; k += S) {  // steady state: every slot is consumed
-#pragma unroll
-    for (int j = 0; j < S; ++j) {
-      load_page(k + j + S - 1, kb[(j + S - 1) % S], vb[(j + S - 1) % S], okb[(j + S - 1) % S]);
-      __builtin_amdgcn_sched_barrier(0);
-      consume(k + j, kb[j], vb[j], okb[j]);
-    }
-  }
-  // tail: fewer than S pages left, all already requested (page k + j sits in slot j)
-#pragma unroll
-  for (int j = 0; j < S - 1; ++j)
-    if (k + j < np) consume(k + j, kb[j], vb[j], okb[j]);
-
-  // Merge the 8 lane rows (lanes xor 8, 16, 32 hold the other rows); afterwards every
-  // lane holds the wave's state for its column's dims.
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    float mw = m[g];
-    mw = fmaxf(mw, __shfl_xor(mw, 8));
-    mw = fmaxf(mw, __shfl_xor(mw, 16));
-    mw = fmaxf(mw, __shfl_xor(mw, 32));
-    const float sc = exp2_fast(m[g] - mw);
-    m[g] = mw;
-    float lw = l[g] * sc;
-    lw += __shfl_xor(lw, 8);
-    lw += __shfl_xor(lw, 16);
-    lw += __shfl_xor(lw, 32);
-    l[g] = lw;
-#pragma unroll
-    for (int ch = 0; ch < NC; ++ch)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        float a = acc[g][ch][e] * sc;
-        a += __shfl_xor(a, 8);
-        a += __shfl_xor(a, 16);
-        a += __shfl_xor(a, 32);
-        acc[g][ch][e] = a;
-      }
-  }
-
-  if (nparts == 1) {
-    if (row == 0) {
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
-#pragma unroll
-        for (int ch = 0; ch < NC; ++ch) {
-          f16x8 o;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) o[e] = f16(acc[g][ch][e] * inv);
-          *reinterpret_cast<f16x8*>(out_bh + g * D + (col + 8 * ch) * 8) = o;
-        }
-      }
-    }
-    return;
-  }
-
-  // Split-KV: publish this partition's (m, l, O), then the last wave to arrive for
-  // (sequence, kv head) merges all partitions with log-sum-exp weights.
-  if (row == 0) {
-#pragma unroll
-    for (int g = 0; g < G; ++g) {
-      const int64_t slot = (bh0 + g) * max_parts + part;
-#pragma unroll
-      for (int ch = 0; ch < NC; ++ch)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) st_dev(ws.o + slot * D + (col + 8 * ch) * 8 + e, acc[g][ch][e]);
-      if (col == 0) {
-        st_dev(ws.ml + slot * 2 + 0, m[g]);
-        st_dev(ws.ml + slot * 2 + 1, l[g]);
-      }
-    }
-  }
-  uint32_t* counter = ws.count + int64_t(b) * num_kv_heads + kvh;
-  if (!wave_arrive_last(counter, uint32_t(nparts - 1), lane)) return;
-
-  // Merge (nparts <= 64).  Lane pp holds partition pp's (m, l) for every head, so the
-  // weights cost one batch of loads and two wave reductions; the O partials are then read
-  // in unrolled batches of 8 partitions so each batch is one memory round trip.
-  float wgt[G], inv[G], mp[G], lp[G];
-  const bool have = lane < nparts;
-  const int pl = have ? lane : 0;  // loads stay unconditional (in-bounds), values are masked
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    mp[g] = ld_dev(ws.ml + ((bh0 + g) * max_parts + pl) * 2);
-    lp[g] = ld_dev(ws.ml + ((bh0 + g) * max_parts + pl) * 2 + 1);
-  }
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-    const float m_l = have ? mp[g] : kNegBig;
-    const float mx = wave_max(m_l);
-    wgt[g] = have ? exp2_fast(m_l - mx) : 0.f;
-    const float L = wave_sum(wgt[g] * (have ? lp[g] : 0.f));
-    inv[g] = L > 0.f ? 1.f / L : 0.f;
-  }
-  constexpr int kDw = D / kWave;  // output dims per lane per head
-  float O[G][kDw];
-#pragma unroll
-  for (int g = 0; g < G; ++g)
-#pragma unroll
-    for (int j = 0; j < kDw; ++j) O[g][j] = 0.f;
-  for (int p0 = 0; p0 < nparts; p0 += 8) {
-    float v[8][G][kDw];
-#pragma unroll
-    for (int u = 0; u < 8; ++u)
+      // query of the GQA group and the piece's page ids (64 per lane window)
+      const f16* qs = q + int64_t(seg) * G * D;  // rows (b, kvh*G + g)
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int j = 0; j < kDw; ++j)
-          v[u][g][j] = ld_dev(ws.o + ((bh0 + g) * max_parts + min(p0 + u, nparts - 1)) * D + lane + kWave * j);
+        for (int ch = 0; ch < NC; ++ch) qv[g][ch] = as_h8(ld16(qs + g * D + (col + 8 * ch) * 8));
+      const int32_t* bt = block_tables + int64_t(b) * max_pages + page0;
+      int ids0 = lane < np ? bt[lane] : 0;
+      int ids1 = lane + kWave < np ? bt[lane + kWave] : 0;
+      int cur_w = 0;
+      auto page_id = [&](int k) -> int {
+        const int j = k & (kWave - 1);
+        return (k >> 6) == cur_w ? __builtin_amdgcn_readlane(ids0, j) : __builtin_amdgcn_readlane(ids1, j);
+      };
+      auto shift = [&](int k) {  // consume enters the next 64-page window of the piece
+        if ((k >> 6) != cur_w) {
+          ids0 = ids1;
+          cur_w = k >> 6;
+          const int nxt = kWave * (cur_w + 1) + lane;
+          ids1 = nxt < np ? bt[nxt] : 0;
+        }
+      };
+      const f16* head_base = pool + int64_t(kvh) * D + int64_t(row) * tok_stride + col * 8;
+      auto load_page = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool& ok) {
+        const int phys = page_id(k < np ? k : np - 1);  // past the end: re-read the last page (L2 hit)
+        ok = phys >= 0 && int64_t(phys) < num_pages;
+        const f16* base = head_base + int64_t(ok ? phys : 0) * page_elems;
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+          for (int ch = 0; ch < NC; ++ch) {
+            kr[tt][ch] = ld16(base + tt * 8 * tok_stride + ch * 64);
+            vr[tt][ch] = ld16(base + v_off + tt * 8 * tok_stride + ch * 64);
+          }
+      };
+      auto consume = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool ok) {
+        const int p = page0 + k;
+        bool valid[2];
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) valid[tt] = ok && (p * kBlock + row + 8 * tt) < len;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+          if (!valid[tt])
+#pragma unroll
+            for (int ch = 0; ch < NC; ++ch) vr[tt][ch] = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          float sc[2];
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            float a = 0.f;
+#pragma unroll
+            for (int ch = 0; ch < NC; ++ch) a = dot8(qv[g][ch], as_h8(kr[tt][ch]), a);
+            a = sum8(a);
+            sc[tt] = valid[tt] ? a * scale_log2 : -INFINITY;
+          }
+          const float mn = fmaxf(m[g], fmaxf(sc[0], sc[1]));
+          const float alpha = exp2_fast(m[g] - mn);
+          const float p0 = exp2_fast(sc[0] - mn);
+          const float p1 = exp2_fast(sc[1] - mn);
+          l[g] = l[g] * alpha + p0 + p1;
+          m[g] = mn;
+#pragma unroll
+          for (int ch = 0; ch < NC; ++ch) {
+            const f16x8 v0 = as_h8(vr[0][ch]);
+            const f16x8 v1 = as_h8(vr[1][ch]);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              acc[g][ch][e] = fmaf(p1, float(v1[e]), fmaf(p0, float(v0[e]), acc[g][ch][e] * alpha));
+          }
+        }
+      };
+
 #pragma unroll
       for (int g = 0; g < G; ++g) {
-        const float wu = __builtin_bit_cast(
-            float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt[g]), min(p0 + u, kWave - 1)));
+        m[g] = kNegBig;
+        l[g] = 0.f;
 #pragma unroll
-        for (int j = 0; j < kDw; ++j) O[g][j] = fmaf(wu, v[u][g][j], O[g][j]);
+        for (int ch = 0; ch < NC; ++ch)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[g][ch][e] = 0.f;
       }
-  }
+      // S-stage register ring over the piece: page k+S-1 is requested while page k is
+      // consumed; the scheduling barriers keep the loads ahead of the arithmetic.
 #pragma unroll
-  for (int g = 0; g < G; ++g)
+      for (int j = 0; j < S - 1; ++j) load_page(j, kb[j], vb[j], okb[j]);
+      int k = 0;
+      for (; k + S <= np; k += S) {
 #pragma unroll
-    for (int j = 0; j < kDw; ++j) out_bh[g * D + lane + kWave * j] = f16(O[g][j] * inv[g]);
-  if (lane == 0) reset_ticket(counter);
+        for (int j = 0; j < S; ++j) {
+          shift(k + j);
+          load_page(k + j + S - 1, kb[(j + S - 1) % S], vb[(j + S - 1) % S], okb[(j + S - 1) % S]);
+          __builtin_amdgcn_sched_barrier(0);
+          consume(k + j, kb[j], vb[j], okb[j]);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < S - 1; ++j)  // tail: fewer than S pages left, all requested
+        if (k + j < np) {
+          shift(k + j);
+          consume(k + j, kb[j], vb[j], okb[j]);
+        }
+
+      // merge the 8 lane rows; then every lane holds the piece's state for its dims
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float mw = m[g];
+        mw = fmaxf(mw, __shfl_xor(mw, 8));
+        mw = fmaxf(mw, __shfl_xor(mw, 16));
+        mw = fmaxf(mw, __shfl_xor(mw, 32));
+        const float scl = exp2_fast(m[g] - mw);
+        m[g] = mw;
+        float lw = l[g] * scl;
+        lw += __shfl_xor(lw, 8);
+        lw += __shfl_xor(lw, 16);
+        lw += __shfl_xor(lw, 32);
+        l[g] = lw;
+#pragma unroll
+        for (int ch = 0; ch < NC; ++ch)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            float a2 = acc[g][ch][e] * scl;
+            a2 += __shfl_xor(a2, 8);
+            a2 += __shfl_xor(a2, 16);
+            a2 += __shfl_xor(a2, 32);
+            acc[g][ch][e] = a2;
+          }
+      }
+      const int64_t w_first = range_of(seg_start);
+      const int np_seg = int(range_of(seg_end - 1) - w_first + 1);
+      if (np_seg == 1) {  // this wave held the whole segment: write the output
+        if (row == 0) {
+          f16* o = out + int64_t(seg) * G * D;
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
+#pragma unroll
+            for (int ch = 0; ch < NC; ++ch) {
+              f16x8 v;
+#pragma unroll
+              for (int e = 0; e < 8; ++e) v[e] = f16(acc[g][ch][e] * inv);
+              *reinterpret_cast<f16x8*>(o + g * D + (col + 8 * ch) * 8) = v;
+            }
+          }
+        }
+      } else {  // one of several pieces: publish (m, l, O) in slot = segment + range
+        const int64_t slot = int64_t(seg) + r;
+        if (row == 0) {
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+#pragma unroll
+            for (int ch = 0; ch < NC; ++ch)
+#pragma unroll
+              for (int e = 0; e < 8; ++e)
+                st_dev(ws.o + (slot * G + g) * D + (col + 8 * ch) * 8 + e, acc[g][ch][e]);
+            if (col == 0) {
+              st_dev(ws.ml + (slot * G + g) * 2 + 0, m[g]);
+              st_dev(ws.ml + (slot * G + g) * 2 + 1, l[g]);
+            }
+          }
+        }
+        // only the first and the last piece of a wave's range can be a split segment
+        if (pend_n == 0) {
+          pend_seg0 = seg; pend_first0 = int(w_first); pend_np0 = np_seg;
+        } else {
+          pend_seg1 = seg; pend_first1 = int(w_first); pend_np1 = np_seg;
+        }
+        pend_n = pend_n + 1;
+      }
+    }
+    if (pend_n == 0) return;
+      // Tickets for the range's split segments (at most its first and last piece).
+    __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave acknowledged
+    uint32_t t = 0;
+    if (lane < pend_n)
+      t = __hip_atomic_fetch_add(ws.count + (lane == 0 ? pend_seg0 : pend_seg1), 1u, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    for (int i = 0; i < pend_n; ++i) {
+      const uint32_t ti = uint32_t(__builtin_amdgcn_readlane(int(t), i));
+      const int seg = i == 0 ? pend_seg0 : pend_seg1;
+      const int npieces = i == 0 ? pend_np0 : pend_np1;
+      if (ti != uint32_t(npieces - 1)) continue;
+      // Merge pieces slot = seg + w for w = first .. first + npieces - 1 (log-sum-exp weights).
+      const int64_t base = int64_t(seg) + (i == 0 ? pend_first0 : pend_first1);
+      f16* o = out + int64_t(seg) * G * D;
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float mx = kNegBig;
+        for (int c0 = 0; c0 < npieces; c0 += kWave) {
+          const int pi = min(c0 + lane, npieces - 1);
+          mx = fmaxf(mx, wave_max(ld_dev(ws.ml + ((base + pi) * G + g) * 2)));
+        }
+        float L = 0.f;
+        float O[D / kWave];
+#pragma unroll
+        for (int j = 0; j < D / kWave; ++j) O[j] = 0.f;
+        for (int c0 = 0; c0 < npieces; c0 += kWave) {
+          const bool have = c0 + lane < npieces;
+          const int pi = have ? c0 + lane : npieces - 1;
+          const float mp = ld_dev(ws.ml + ((base + pi) * G + g) * 2);
+          const float lp = ld_dev(ws.ml + ((base + pi) * G + g) * 2 + 1);
+          const float wgt = have ? exp2_fast(mp - mx) : 0.f;
+          L += wave_sum(wgt * lp);
+          const int cnt = min(kWave, npieces - c0);
+          for (int c1 = 0; c1 < cnt; c1 += 8) {
+            float v[8][D / kWave];
+#pragma unroll
+            for (int uu = 0; uu < 8; ++uu)
+#pragma unroll
+              for (int j = 0; j < D / kWave; ++j)
+                v[uu][j] = ld_dev(ws.o + ((base + c0 + min(c1 + uu, cnt - 1)) * G + g) * D + lane + kWave * j);
+#pragma unroll
+            for (int uu = 0; uu < 8; ++uu) {
+              const float wu = __builtin_bit_cast(
+                  float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), min(c1 + uu, kWave - 1)));
+              const float wz = c1 + uu < cnt ? wu : 0.f;
+#pragma unroll
+              for (int j = 0; j < D / kWave; ++j) O[j] = fmaf(wz, v[uu][j], O[j]);
+            }
+          }
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+#pragma unroll
+        for (int j = 0; j < D / kWave; ++j) o[g * D + lane + kWave * j] = f16(O[j] * inv);
+      }
+      if (lane == 0) reset_ticket(ws.count + seg);
+    }
+  };
+
+  run_range(r_wave, total_units * r_wave / nw, total_units * (r_wave + 1) / nw);
 }
 
 typedef void (*DecodeKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t,
-                             const int32_t*, const uint8_t*, int32_t, int32_t, float, int32_t,
-                             DecodeWorkspace, int32_t);
+                             const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, float,
+                             DecodeWorkspace);
 
 static DecodeKernel pick_decode(int d, int g) {
 #define IFN_DECODE_CASE(DD, GG) \
@@ -350,23 +453,17 @@ static DecodeKernel pick_decode(int d, int g) {
   return nullptr;
 }
 
-static int decode_max_parts(int32_t batch, int32_t hkv, int32_t max_seq_len) {
-  const int ppp = decode_pages_per_part(batch, hkv, max_seq_len);
-  return int(ceil_div(ceil_div(max_seq_len > 0 ? max_seq_len : 1, kBlock), ppp));
-}
-
 }  // namespace ifn
 
 extern "C" size_t ifn_paged_decode_workspace_bytes(int32_t batch, int32_t num_q_heads,
                                                    int32_t num_kv_heads, int32_t head_dim,
                                                    int32_t block_size, int32_t max_seq_len) {
   if (batch < 1 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 || block_size < 1 ||
-      max_seq_len < 0)
+      max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
     return 0;
   size_t off_ml, off_o;
-  return ifn::decode_ws_layout(batch, num_q_heads, head_dim,
-                               ifn::decode_max_parts(batch, num_kv_heads, max_seq_len), &off_ml,
-                               &off_o);
+  return ifn::decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
+                               int64_t(ifn::decode_blocks()) * ifn::kWavesPerBlock, &off_ml, &off_o);
 }
 
 extern "C" int ifn_paged_decode(void* out, const void* query, const void* kv_pool_layer,
@@ -384,34 +481,29 @@ extern "C" int ifn_paged_decode(void* out, const void* query, const void* kv_poo
       num_kv_heads < 1 || head_dim < 1 || max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
     return IFN_ERR_INVALID_ARGUMENT;
   if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
-  if (ceil_div(max_seq_len, kBlock) > int64_t(kWave) * kMaxPagesPerPart) return IFN_ERR_UNSUPPORTED;
+  if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
   DecodeKernel k = pick_decode(head_dim, num_q_heads / num_kv_heads);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);
   if (batch == 0) return IFN_OK;
-  const int32_t len_cap = max_seq_len < max_pages_per_seq * kBlock ? max_seq_len
-                                                                    : max_pages_per_seq * kBlock;
-  const int ppp = decode_pages_per_part(batch, num_kv_heads, len_cap);
-  const int max_parts = int(ceil_div(ceil_div(len_cap > 0 ? len_cap : 1, kBlock), ppp));
+  const int blocks = decode_blocks();
   size_t off_ml, off_o;
-  const size_t need = decode_ws_layout(batch, num_q_heads, head_dim, max_parts, &off_ml, &off_o);
-  if (int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
-  if (max_parts > 1) {
-    if (workspace == nullptr || workspace_bytes < need) return IFN_ERR_WORKSPACE;
-    IFN_CHECK_ALIGN16(workspace);
-  }
+  const size_t need = decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
+                                       int64_t(blocks) * kWavesPerBlock, &off_ml, &off_o);
+  if (workspace == nullptr || workspace_bytes < need) return IFN_ERR_WORKSPACE;
+  IFN_CHECK_ALIGN16(workspace);
+  if (device_cu_count() < 1) return IFN_ERR_HIP;
   DecodeWorkspace ws;
   uint8_t* wsb = static_cast<uint8_t*>(workspace);
   ws.count = reinterpret_cast<uint32_t*>(wsb);
   ws.ml = reinterpret_cast<float*>(wsb + off_ml);
   ws.o = reinterpret_cast<float*>(wsb + off_o);
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
-  dim3 grid{unsigned(max_parts), unsigned(batch), unsigned(ceil_div(num_kv_heads, kHeadsPerBlock))};
-  k<<<grid, kDecodeThreads, 0, reinterpret_cast<hipStream_t>(stream)>>>(
+  k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
-      seq_lens, active_mask, num_kv_heads, len_cap, scale * kLog2e, ppp, ws, max_parts);
+      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws);
   return ifn_launch_status();
 }

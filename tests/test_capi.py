@@ -77,8 +77,7 @@ def test_paged_decode_host_validation():
     need = L.ifn_paged_decode_workspace_bytes(32, 16, 8, 128, 16, 4096)
     assert call(ws=A, wsb=need - 1) == _capi.IFN_ERR_WORKSPACE
     assert call(B=0) == _capi.IFN_OK
-    # beyond 64 partitions of 64 pages (65,536 tokens) a row is not supported
-    assert call(W=8192, msl=65536 + 16) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(B=21504) == _capi.IFN_ERR_UNSUPPORTED  # batch beyond the LDS prefix table
 
 
 def test_workspace_sizes():
@@ -87,8 +86,8 @@ def test_workspace_sizes():
     big = L.ifn_paged_decode_workspace_bytes(256, 16, 8, 128, 16, 8192)
     assert 0 < small < big and big % 256 == 0
     assert L.ifn_paged_decode_workspace_bytes(0, 16, 8, 128, 16, 512) == 0
-    # partials: 256 rows x 16 heads x (parts) x (128 + 2) floats must fit
-    assert big >= 256 * 16 * 2 * 130 * 4
+    # partial slots: one per (row, kv head) and per wave of the launch, G x (128 + 2) floats each
+    assert big >= (256 * 8 + 2048) * 2 * 130 * 4  # one slot per (row, kv head) and per wave (256 CUs x 8)
     assert L.ifn_paged_prefill_workspace_bytes(512, 1536, 16, 8, 128, 16) > 0
 
 
