@@ -40,8 +40,8 @@ namespace ifn {
 constexpr int kBlock = 16;               // tokens per page compiled in
 constexpr int kWavesPerBlock = 8;
 constexpr int kDecodeThreads = kWavesPerBlock * kWave;
-constexpr int kPrefixInts = 21 * 1024;   // 84 KiB of LDS: one workgroup per CU
-constexpr int kMaxBatch = kPrefixInts - 1;
+constexpr int kRowInts = 10752;         // per-row LDS tables: 2 x 42 KiB, so one workgroup per CU
+constexpr int kMaxBatch = kRowInts - 1;
 constexpr int kMaxWaves = 1024 * kWavesPerBlock;  // waves of a launch are capped at this
 constexpr int kXcds = 8;            // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 
@@ -95,6 +95,29 @@ static int decode_blocks() {
   return cus < kMaxWaves / kWavesPerBlock ? cus : kMaxWaves / kWavesPerBlock;
 }
 
+// Sum over the 8 lane rows (lane = 8*row + col) of x[e], scattered so that the lane of row r
+// returns the total of element e = r: three halving steps (xor 32, 16, 8 exchange 4, 2, 1
+// values) instead of an all-reduce of all 8.  The selects are two-way on a row bit.
+__device__ __forceinline__ float row_reduce_scatter(const float (&x)[8], int row) {
+  const bool b2 = (row & 4) != 0, b1 = (row & 2) != 0, b0 = (row & 1) != 0;
+  float h[4], q[2];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float keep = b2 ? x[e + 4] : x[e];
+    const float send = b2 ? x[e] : x[e + 4];
+    h[e] = keep + __shfl_xor(send, 32);
+  }
+#pragma unroll
+  for (int e = 0; e < 2; ++e) {
+    const float keep = b1 ? h[e + 2] : h[e];
+    const float send = b1 ? h[e] : h[e + 2];
+    q[e] = keep + __shfl_xor(send, 16);
+  }
+  const float keep = b0 ? q[1] : q[0];
+  const float send = b0 ? q[0] : q[1];
+  return keep + __shfl_xor(send, 8);
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
@@ -103,7 +126,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     int32_t num_kv_heads, int32_t max_len, float scale_log2, DecodeWorkspace ws) {
   constexpr int NC = D / 64;  // 16-byte chunks per lane per token row
   constexpr int S = DecodeStages<D, G>::value;
-  __shared__ int s_off[kPrefixInts];  // s_off[b] = pages of rows < b; s_off[batch] = total
+  __shared__ int s_off[kRowInts];  // s_off[b] = pages of rows < b; s_off[batch] = total
+  __shared__ int s_len[kRowInts];  // keys of row b (0 for inactive rows)
   __shared__ int s_wsum[kWavesPerBlock];
 
   const int tid = threadIdx.x;
@@ -112,8 +136,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   const int hq = num_kv_heads * G;
   const int cap = min(max_pages * kBlock, max_len);
   auto row_len = [&](int b) -> int {  // keys of row b; inactive rows have none
-    if (active != nullptr && active[b] == 0) return 0;
-    return min(seq_lens[b], cap);
+    const int sl = seq_lens[b];                       // both loads issue before either is used
+    const int act = active != nullptr ? int(active[b]) : 1;
+    return act != 0 ? min(sl, cap) : 0;
   };
 
   // 1. Exclusive prefix of pages per row, in LDS (every workgroup builds its own copy).
@@ -123,6 +148,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     int pages = 0;
     if (i < batch) {
       const int len = row_len(i);
+      s_len[i] = len;
       pages = len > 0 ? (len + kBlock - 1) / kBlock : 0;
     }
     int x = pages;
@@ -151,7 +177,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   if (blockIdx.x == 0) {
     for (int b = wave; b < batch; b += kWavesPerBlock) {
       const bool live = active == nullptr || active[b] != 0;
-      if (live && min(seq_lens[b], cap) <= 0) {
+      if (live && s_len[b] <= 0) {
         for (int i = lane; i < hq * D; i += kWave) out[int64_t(b) * hq * D + i] = f16(0.f);
       }
     }
@@ -204,7 +230,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       const int page0 = int(u - seg_start);
       const int np = int(min(u_hi, seg_end) - u);  // pages of this piece
       const int seg = b * num_kv_heads + kvh;
-      const int len = row_len(b);
+      const int len = s_len[b];
       u += np;
 
       // query of the GQA group and the piece's page ids (64 per lane window)
@@ -310,7 +336,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
           consume(k + j, kb[j], vb[j], okb[j]);
         }
 
-      // merge the 8 lane rows; then every lane holds the piece's state for its dims
+      // Merge the 8 lane rows: (m, l) by butterflies; O by a reduce-scatter after which lane
+      // 8*row + col holds element e = row of its column, i.e. output dim (col + 8*ch)*8 + row.
+      float o_red[G][NC];
 #pragma unroll
       for (int g = 0; g < G; ++g) {
         float mw = m[g];
@@ -325,47 +353,34 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
         lw += __shfl_xor(lw, 32);
         l[g] = lw;
 #pragma unroll
-        for (int ch = 0; ch < NC; ++ch)
+        for (int ch = 0; ch < NC; ++ch) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            float a2 = acc[g][ch][e] * scl;
-            a2 += __shfl_xor(a2, 8);
-            a2 += __shfl_xor(a2, 16);
-            a2 += __shfl_xor(a2, 32);
-            acc[g][ch][e] = a2;
-          }
+          for (int e = 0; e < 8; ++e) acc[g][ch][e] *= scl;
+          o_red[g][ch] = row_reduce_scatter(acc[g][ch], row);
+        }
       }
       const int64_t w_first = range_of(seg_start);
       const int np_seg = int(range_of(seg_end - 1) - w_first + 1);
       if (np_seg == 1) {  // this wave held the whole segment: write the output
-        if (row == 0) {
-          f16* o = out + int64_t(seg) * G * D;
+        f16* o = out + int64_t(seg) * G * D;
 #pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
+        for (int g = 0; g < G; ++g) {
+          const float inv = l[g] > 0.f ? 1.f / l[g] : 0.f;
 #pragma unroll
-            for (int ch = 0; ch < NC; ++ch) {
-              f16x8 v;
-#pragma unroll
-              for (int e = 0; e < 8; ++e) v[e] = f16(acc[g][ch][e] * inv);
-              *reinterpret_cast<f16x8*>(o + g * D + (col + 8 * ch) * 8) = v;
-            }
-          }
+          for (int ch = 0; ch < NC; ++ch) o[g * D + (col + 8 * ch) * 8 + row] = f16(o_red[g][ch] * inv);
         }
       } else {  // one of several pieces: publish (m, l, O) in slot = segment + range
         const int64_t slot = int64_t(seg) + r;
-        if (row == 0) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int ch = 0; ch < NC; ++ch)  // 64 lanes cover 64 consecutive floats
+            st_dev(ws.o + (slot * G + g) * D + (col + 8 * ch) * 8 + row, o_red[g][ch]);
+        if (lane == 0) {
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-#pragma unroll
-            for (int ch = 0; ch < NC; ++ch)
-#pragma unroll
-              for (int e = 0; e < 8; ++e)
-                st_dev(ws.o + (slot * G + g) * D + (col + 8 * ch) * 8 + e, acc[g][ch][e]);
-            if (col == 0) {
-              st_dev(ws.ml + (slot * G + g) * 2 + 0, m[g]);
-              st_dev(ws.ml + (slot * G + g) * 2 + 1, l[g]);
-            }
+            st_dev(ws.ml + (slot * G + g) * 2 + 0, m[g]);
+            st_dev(ws.ml + (slot * G + g) * 2 + 1, l[g]);
           }
         }
         // only the first and the last piece of a wave's range can be a split segment
@@ -378,7 +393,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       }
     }
     if (pend_n == 0) return;
-      // Tickets for the range's split segments (at most its first and last piece).
+    // Tickets for the range's split segments (at most its first and last piece).
     __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave acknowledged
     uint32_t t = 0;
     if (lane < pend_n)
