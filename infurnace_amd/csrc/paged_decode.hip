@@ -118,6 +118,80 @@ __device__ __forceinline__ float row_reduce_scatter(const float (&x)[8], int row
   return keep + __shfl_xor(send, 8);
 }
 
+// Log-sum-exp merge of the partial states in workspace slots base .. base + npieces - 1 into the
+// G output rows at o (one wave).  Pieces are taken 64 at a time, one per lane, with a running
+// maximum; the (m, l) loads and the first batch of O loads are issued together so that the
+// common case (npieces <= batch) costs a single round trip to device-coherent memory.
+template <int D, int G>
+__device__ __forceinline__ void merge_pieces(f16* __restrict__ o, const DecodeWorkspace& ws, int64_t base,
+                                             int npieces, int lane) {
+  constexpr int NC = D / kWave;
+  constexpr int kPB = 64 / (G * NC) < 2 ? 2 : (64 / (G * NC) > 16 ? 16 : 64 / (G * NC));
+  float mx[G], L[G], O[G][NC];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    mx[g] = kNegBig;
+    L[g] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) O[g][j] = 0.f;
+  }
+  for (int c0 = 0; c0 < npieces; c0 += kWave) {
+    const int cnt = min(kWave, npieces - c0);
+    const bool have = lane < cnt;
+    const int64_t my_slot = base + c0 + (have ? lane : cnt - 1);
+    float mp[G], lp[G], v[kPB][G][NC];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      mp[g] = ld_dev(ws.ml + (my_slot * G + g) * 2);
+      lp[g] = ld_dev(ws.ml + (my_slot * G + g) * 2 + 1);
+    }
+    auto load_batch = [&](int c1) {
+#pragma unroll
+      for (int uu = 0; uu < kPB; ++uu) {
+        const int64_t sl = base + c0 + min(c1 + uu, cnt - 1);
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int j = 0; j < NC; ++j) v[uu][g][j] = ld_dev(ws.o + (sl * G + g) * D + lane + kWave * j);
+      }
+    };
+    load_batch(0);
+    float w[G];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      const float nm = fmaxf(mx[g], wave_max(have ? mp[g] : kNegBig));
+      const float sc = exp2_fast(mx[g] - nm);
+      mx[g] = nm;
+      w[g] = have ? exp2_fast(mp[g] - nm) : 0.f;
+      L[g] = L[g] * sc + wave_sum(w[g] * lp[g]);
+#pragma unroll
+      for (int j = 0; j < NC; ++j) O[g][j] *= sc;
+    }
+    for (int c1 = 0;;) {
+#pragma unroll
+      for (int uu = 0; uu < kPB; ++uu) {
+        const int src = min(c1 + uu, kWave - 1);
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float wu = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w[g]), src));
+          const float wz = c1 + uu < cnt ? wu : 0.f;
+#pragma unroll
+          for (int j = 0; j < NC; ++j) O[g][j] = fmaf(wz, v[uu][g][j], O[g][j]);
+        }
+      }
+      c1 += kPB;
+      if (c1 >= cnt) break;
+      load_batch(c1);
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float inv = L[g] > 0.f ? 1.f / L[g] : 0.f;
+#pragma unroll
+    for (int j = 0; j < NC; ++j) o[g * D + lane + kWave * j] = f16(O[g][j] * inv);
+  }
+}
+
 template <int D, int G>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
@@ -405,48 +479,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       const int npieces = i == 0 ? pend_np0 : pend_np1;
       if (ti != uint32_t(npieces - 1)) continue;
       // Merge pieces slot = seg + w for w = first .. first + npieces - 1 (log-sum-exp weights).
-      const int64_t base = int64_t(seg) + (i == 0 ? pend_first0 : pend_first1);
-      f16* o = out + int64_t(seg) * G * D;
-#pragma unroll
-      for (int g = 0; g < G; ++g) {
-        float mx = kNegBig;
-        for (int c0 = 0; c0 < npieces; c0 += kWave) {
-          const int pi = min(c0 + lane, npieces - 1);
-          mx = fmaxf(mx, wave_max(ld_dev(ws.ml + ((base + pi) * G + g) * 2)));
-        }
-        float L = 0.f;
-        float O[D / kWave];
-#pragma unroll
-        for (int j = 0; j < D / kWave; ++j) O[j] = 0.f;
-        for (int c0 = 0; c0 < npieces; c0 += kWave) {
-          const bool have = c0 + lane < npieces;
-          const int pi = have ? c0 + lane : npieces - 1;
-          const float mp = ld_dev(ws.ml + ((base + pi) * G + g) * 2);
-          const float lp = ld_dev(ws.ml + ((base + pi) * G + g) * 2 + 1);
-          const float wgt = have ? exp2_fast(mp - mx) : 0.f;
-          L += wave_sum(wgt * lp);
-          const int cnt = min(kWave, npieces - c0);
-          for (int c1 = 0; c1 < cnt; c1 += 8) {
-            float v[8][D / kWave];
-#pragma unroll
-            for (int uu = 0; uu < 8; ++uu)
-#pragma unroll
-              for (int j = 0; j < D / kWave; ++j)
-                v[uu][j] = ld_dev(ws.o + ((base + c0 + min(c1 + uu, cnt - 1)) * G + g) * D + lane + kWave * j);
-#pragma unroll
-            for (int uu = 0; uu < 8; ++uu) {
-              const float wu = __builtin_bit_cast(
-                  float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, wgt), min(c1 + uu, kWave - 1)));
-              const float wz = c1 + uu < cnt ? wu : 0.f;
-#pragma unroll
-              for (int j = 0; j < D / kWave; ++j) O[j] = fmaf(wz, v[uu][j], O[j]);
-            }
-          }
-        }
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-#pragma unroll
-        for (int j = 0; j < D / kWave; ++j) o[g * D + lane + kWave * j] = f16(O[j] * inv);
-      }
+      merge_pieces<D, G>(out + int64_t(seg) * G * D, ws, int64_t(seg) + (i == 0 ? pend_first0 : pend_first1),
+                         npieces, lane);
       if (lane == 0) reset_ticket(ws.count + seg);
     }
   };
