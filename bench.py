@@ -41,12 +41,18 @@ MFMA_F16_PEAK_TFLOPS = 2500.0  # dense fp16 MFMA, MI355X
 TRAFFIC_FILE = os.path.join(ROOT, "profiles", "decode_config2_traffic.json")
 
 
+HIP_EVENT_DISABLE_SYSTEM_FENCE = 0x20000000  # hip_runtime_api.h: no cache writeback/invalidate on record
+
+
 class HipEvents:
-    """Thin ctypes access to hipEventCreate/Record/ElapsedTime (cheap enough to bracket every launch)."""
+    """Thin ctypes access to hipEventCreateWithFlags/Record/ElapsedTime, cheap enough to bracket every
+    launch.  The events are created with hipEventDisableSystemFence: a default event record performs a
+    system-scope release (L2 writeback + invalidate) that lands inside the measured interval and slows
+    the next kernel; these events only time work, and elapsed times are read after a device sync."""
 
     def __init__(self):
         self.hip = ctypes.CDLL("libamdhip64.so")
-        self.hip.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
         self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p, ctypes.c_void_p]
         self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
@@ -55,8 +61,8 @@ class HipEvents:
         evs = []
         for _ in range(n):
             e = ctypes.c_void_p()
-            if self.hip.hipEventCreate(ctypes.byref(e)) != 0:
-                raise RuntimeError("hipEventCreate failed")
+            if self.hip.hipEventCreateWithFlags(ctypes.byref(e), HIP_EVENT_DISABLE_SYSTEM_FENCE) != 0:
+                raise RuntimeError("hipEventCreateWithFlags failed")
             evs.append(e)
         return evs
 
