@@ -11,26 +11,28 @@
 //
 //  * Balanced flat split.  The work is the list of (row, kv head, page) units
 //    in that order -- Hkv * sum(ceil(len/16)) units of 8 KiB (one kv head's
-//    16 K rows + 16 V rows).  The grid is one 8-wave workgroup per CU (an
-//    84 KiB LDS table keeps the dispatcher at one workgroup per CU) and wave w
-//    of N takes units [w*U/N, (w+1)*U/N).  Ragged batches therefore cost every
-//    CU the same bytes; no CU idles while another streams a long row.  Each
-//    workgroup rebuilds the per-row page prefix sums in LDS from seq_lens.
-//  * A wave streams its units through an S-stage register ring: unit k+S-1 is
-//    requested while unit k is consumed, across row/head boundaries, with the
-//    next segment's query prefetched.  Page ids and unit metadata sit one per
-//    lane (64 units per window) and are read with v_readlane.
+//    16 K rows + 16 V rows).  The grid is one 8-wave workgroup per CU (two
+//    42 KiB LDS tables, page prefix sums and row lengths, keep the dispatcher
+//    at one workgroup per CU) and wave w of N takes units [w*U/N, (w+1)*U/N).
+//    Ragged batches therefore cost every wave the same bytes.  Workgroups are
+//    remapped so that each XCD streams a contiguous eighth of the list.
+//  * A wave's range is cut into pieces at (row, kv head) segment boundaries.
+//    Inside a piece an S-stage register ring requests page k+S-1 while page k
+//    is consumed; page ids sit one per lane (64 per window), read with
+//    v_readlane.
 //  * Each K/V page is fetched once and reused from registers by every query
 //    head of its GQA group.  Inside a page, lane = 8*row + col: every load
 //    instruction reads 8 token rows x 128 contiguous bytes; each lane holds 2
 //    tokens.  q.k uses v_dot2_f32_f16 (fp32 accumulation) and three DPP steps
-//    inside the row; the online softmax runs in base 2 per (lane row, head) and
-//    rows merge once per piece with lane shuffles.  No LDS traffic in the loop.
+//    inside the row; the online softmax runs in base 2 per (lane row, head).
+//    At the end of a piece the 8 lane rows merge: (m, l) by butterflies, O by
+//    a reduce-scatter that leaves lane 8*row + col holding element `row` of
+//    its column, so partial and output stores are contiguous across lanes.
 //  * A (row, kv head) segment split over several waves (at most the first and
 //    last piece of each wave's range) is merged log-sum-exp style by the wave
-//    that finishes last: partials go out with device-coherent stores during
-//    the stream, and the tickets are taken once, at the end of the wave.  No
-//    second launch, no wait loop.
+//    that finishes last: partials go out with device-coherent stores, the
+//    tickets are taken once, at the end of the wave, and the merge issues all
+//    its loads in one round trip.  No second launch, no wait loop.
 #include "ifn_common.hpp"
 
 #include <atomic>
