@@ -8,9 +8,19 @@
 // The QK^T and PV contractions are dense, so they run on
 // v_mfma_f32_32x32x16_f16 (32x32 output tile, K = 16 per instruction):
 //
-//  * Workgroup = (key split, block of queries, kv head).  Its waves cover every
-//    query head of the GQA group: wave w takes head w % G and the 32-query
-//    sub-block w / G, so each K/V tile staged in LDS is shared by all G heads.
+//  * Workgroup = (block of 32 queries, kv head), over every key the block can
+//    see -- no split across workgroups, so no partials leave the CU.  Its
+//    waves are G query heads x kGroups key groups: group k takes the 32-key
+//    tiles t = k, k + kGroups, ... (interleaved, so the causal diagonal costs
+//    every group the same), and the G waves of a group share each K/V tile
+//    staged in LDS.  At the end the groups merge log-sum-exp style through
+//    LDS.
+//  * Tiles are double-buffered in LDS and staged two deep in registers: while
+//    tile i is multiplied, tile i+1 goes from registers to the other LDS
+//    buffer and tile i+2's 16-byte global loads are in flight.  Page ids come
+//    from a lane window (two per tile), so no load waits on a table load.
+//  * Workgroup i runs on XCD i % 8; the kv head is i % Hkv, so for Hkv = 8
+//    each XCD serves one head and its K/V stay in that XCD's L2.
 //  * Scores are computed transposed, S^T = K . Q^T: the MFMA A operand is a
 //    K row (16 B from LDS), the B operand is the lane's query row (held in
 //    registers for the whole kernel), and in the 32x32 result each lane owns
@@ -22,100 +32,68 @@
 //    K = 16 steps once converted to fp16 (the key order inside a step is a
 //    permutation shared by both operands, which a contraction allows).  V is
 //    stored transposed in LDS (Vt[d][key]) so the A operand is two 8-byte reads.
-//  * K/V rows are gathered page by page through the block table with 16-byte
-//    loads; keys past the split, past the causal limit or in an invalid page
-//    are zero-filled and masked.
-//  * Long key ranges are split over workgroups (split-K) so a 512-token chunk
-//    still fills the CUs; partial (m, l, O) go to the workspace and the last
-//    workgroup of a (query block, kv head) merges them, as in paged decode.
+//  * K/V rows are gathered page by page through the block table; keys at or
+//    past the end of the sequence or in an invalid page are zero-filled and
+//    masked.
 #include "ifn_common.hpp"
 
 namespace ifn {
 
 constexpr int kPBlock = 16;  // tokens per page compiled in
-constexpr int kBK = 64;      // keys per LDS tile
+constexpr int kPT = 32;      // keys per tile (one 32x32 MFMA tile)
 
 template <int D, int G>
 struct PrefillCfg {
-  static constexpr int kWaves = G > 4 ? G : 4;
-  static constexpr int kQB = kWaves / G;  // 32-query sub-blocks per workgroup
-  static constexpr int kBQ = 32 * kQB;    // queries per workgroup
+  static constexpr int kGroups = G >= 8 ? 1 : (G >= 4 ? 2 : 4);  // key groups per workgroup
+  static constexpr int kWaves = G * kGroups;
   static constexpr int kThreads = kWaves * kWave;
-  static constexpr int kKS = D + 8;       // K row stride in LDS (halves)
-  static constexpr int kVS = kBK + 4;     // Vt row stride in LDS (halves)
+  static constexpr int kGroupThreads = G * kWave;
+  static constexpr int kKS = D + 8;    // K tile row stride (halves)
+  static constexpr int kVS = kPT + 4;  // Vt row stride (halves)
+  static constexpr int kBufHalves = kPT * kKS + D * kVS;  // one (group, buffer): K tile + Vt tile
+  static constexpr int kTileBytes = 2 * kGroups * kBufHalves * 2;
+  static constexpr int kDT = D / 32;
+  // merge area: (m, l) of every wave, then the accumulators of groups 1.. (lane-contiguous)
+  static constexpr int kMergeBytes = kWaves * 32 * 2 * 4 + (kGroups - 1) * G * kDT * 16 * kWave * 4;
+  static constexpr int kLdsBytes = kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes;
+  static constexpr int kKItems = kPT * (D / 8);        // 16-byte K chunks per tile
+  static constexpr int kVItems = (kPT / 4) * (D / 8);  // 4 keys x 8 dims per V item
+  static constexpr int kKPer = (kKItems + kGroupThreads - 1) / kGroupThreads;
+  static constexpr int kVPer = (kVItems + kGroupThreads - 1) / kGroupThreads;
 };
-
-struct PrefillWorkspace {
-  uint32_t* count;  // [num_qblocks][num_kv_heads] tickets, zero between calls
-  float* ml;        // [num_q_heads][t_pad][max_splits][2]
-  float* o;         // [num_q_heads][t_pad][max_splits][D]
-};
-
-static inline size_t p_align256(size_t x) { return (x + 255) & ~size_t(255); }
-
-struct PrefillPlan {
-  int bq, n_qb, t_pad, split_keys, max_splits;
-  size_t off_ml, off_o, bytes;
-};
-
-static inline int prefill_bq(int g) { return 32 * ((g > 4 ? g : 4) / g); }
-
-static PrefillPlan plan_prefill(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d) {
-  PrefillPlan p;
-  const int g = hq / hkv;
-  p.bq = prefill_bq(g);
-  p.n_qb = int(ceil_div(T, p.bq));
-  p.t_pad = p.n_qb * p.bq;
-  const int64_t max_keys = int64_t(query_start) + T;
-  // enough splits that (query blocks x kv heads x splits) reaches ~512 workgroups
-  const int64_t units = int64_t(p.n_qb) * hkv;
-  const int64_t want = ceil_div(512, units);
-  int64_t sk = ceil_div(ceil_div(max_keys, want), kBK) * kBK;
-  if (sk < 2 * kBK) sk = 2 * kBK;
-  p.split_keys = int(sk);
-  p.max_splits = int(ceil_div(max_keys, sk));
-  size_t off = kTicketBytes;  // shape-independent ticket area first
-  p.off_ml = off;
-  off = p_align256(off + size_t(hq) * p.t_pad * p.max_splits * 2 * sizeof(float));
-  p.off_o = off;
-  off = p_align256(off + size_t(hq) * p.t_pad * p.max_splits * d * sizeof(float));
-  p.bytes = off;
-  return p;
-}
 
 template <int D, int G>
 __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
-    int64_t num_pages, const int32_t* __restrict__ table, int32_t max_pages, int32_t query_start,
-    int32_t T, int32_t num_kv_heads, float scale_log2, int32_t split_keys, int32_t max_splits,
-    int32_t t_pad, PrefillWorkspace ws) {
+    int64_t num_pages, const int32_t* __restrict__ table, int32_t query_start, int32_t T,
+    int32_t num_kv_heads, int32_t n_qb, float scale_log2) {
   using C = PrefillCfg<D, G>;
-  constexpr int kDT = D / 32;  // 32-row output tiles along head_dim
+  constexpr int kDT = C::kDT;
   constexpr int kKSteps = D / 16;
-  const int split = blockIdx.x;
-  const int qb = blockIdx.y;
-  const int kvh = blockIdx.z;
+  constexpr int kChunks = D / 8;
+  // Workgroup i runs on XCD i % 8: kv head = i % Hkv keeps each head's K/V in one XCD's L2
+  // (for Hkv = 8), and query blocks go longest key range first.
+  const int kvh = int(blockIdx.x) % num_kv_heads;
+  const int qb = n_qb - 1 - int(blockIdx.x) / num_kv_heads;
   const int tid = threadIdx.x;
-  const int wave = tid / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
   const int g = wave % G;
-  const int qsub = wave / G;
+  const int grp = wave / G;
+  const int gt = tid - grp * C::kGroupThreads;  // thread index inside the key group
   const int hq = num_kv_heads * G;
   const int head = kvh * G + g;
   const int total = query_start + T;
-  const int q0 = qb * C::kBQ;
-  const int wg_key_end = min(total, query_start + q0 + C::kBQ);
-  const int nsplits = int(ceil_div(wg_key_end, split_keys));
-  if (split >= nsplits) return;
-  const int k_begin = split * split_keys;
-  const int k_end = min(k_begin + split_keys, wg_key_end);
+  const int q0 = qb * 32;
+  const int key_end = min(total, query_start + q0 + 32);  // keys some query of the block sees
+  const int n_tiles = int(ceil_div(key_end, kPT));
+  const int iters = int(ceil_div(n_tiles, C::kGroups));
 
-  const int col = lane % 32;  // this lane's query column / K row within a 32-tile
+  const int col = lane % 32;  // this lane's query column / K row within a tile
   const int half = lane / 32;
-  const int my_q = q0 + qsub * 32 + col;
+  const int my_q = q0 + col;
   const int my_pos = query_start + my_q;
   const bool q_ok = my_q < T;
-  const int wave_key_end = min(total, query_start + q0 + qsub * 32 + 32);
 
   f16x8 qreg[kKSteps];
 #pragma unroll
@@ -126,90 +104,117 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
       qreg[s] = f16x8{};
   }
 
-  __shared__ __attribute__((aligned(16))) f16 Ks[kBK][C::kKS];
-  __shared__ __attribute__((aligned(16))) f16 Vt[D][C::kVS];
+  __shared__ __attribute__((aligned(16))) unsigned char smem[C::kLdsBytes];
+  auto k_tile = [&](int buf) {
+    return reinterpret_cast<f16*>(smem) + (buf * C::kGroups + grp) * C::kBufHalves;
+  };
+  auto v_tile = [&](int buf) { return k_tile(buf) + kPT * C::kKS; };
+
+  const int64_t tok_stride = int64_t(num_kv_heads) * D;
+  const int64_t v_off = num_pages * kPBlock * tok_stride;
+  const f16* head_pool = pool + int64_t(kvh) * D;
+  // Page ids: a tile of 32 keys spans exactly two pages.  Lane l of every wave of the group
+  // holds page 2*tile + (l & 1) of the group's (l / 2)-th upcoming tile, 32 tiles per window,
+  // so a tile's two ids are uniform v_readlane reads -- no dependent table load per tile.
+  const int seq_pages = int(ceil_div(total, kPBlock));
+  int pid = -1, pid_w = -1;
+  auto tile_pages = [&](int i, int& pa, int& pb) __attribute__((always_inline)) {  // pages of the group's tile of iteration i
+    if ((i >> 5) != pid_w) {
+      pid_w = i >> 5;
+      const int pg = 2 * (grp + C::kGroups * (32 * pid_w + lane / 2)) + (lane & 1);
+      pid = pg < seq_pages ? table[pg] : -1;
+    }
+    pa = __builtin_amdgcn_readlane(pid, 2 * (i & 31));
+    pb = __builtin_amdgcn_readlane(pid, 2 * (i & 31) + 1);
+  };
+
+  struct Stage {
+    u32x4 k[C::kKPer];
+    u32x4 v[C::kVPer][4];
+  };
+  auto load_tile = [&](int i, Stage& st) __attribute__((always_inline)) {  // global -> registers: this thread's share of the tile
+    const int t = i * C::kGroups + grp;
+    const int kt = t * kPT;
+    int pa, pb;
+    tile_pages(i, pa, pb);
+    auto row_ptr = [&](int j) -> const f16* {  // row j of the tile, or nullptr (zero row)
+      const int page = j < kPBlock ? pa : pb;
+      if (kt + j >= total || page < 0 || int64_t(page) >= num_pages) return nullptr;
+      return head_pool + (int64_t(page) * kPBlock + j % kPBlock) * tok_stride;
+    };
+    // Branch-free: a masked row loads from the head's first row (always valid) and is zeroed.
+    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int it = 0; it < C::kKPer; ++it) {
+      const int idx = min(gt + it * C::kGroupThreads, C::kKItems - 1);
+      const f16* r = row_ptr(idx / kChunks);
+      const u32x4 x = ld16((r != nullptr ? r : head_pool) + (idx % kChunks) * 8);
+      st.k[it] = r != nullptr ? x : zero;
+    }
+#pragma unroll
+    for (int it = 0; it < C::kVPer; ++it) {
+      const int idx = min(gt + it * C::kGroupThreads, C::kVItems - 1);
+#pragma unroll
+      for (int rr = 0; rr < 4; ++rr) {
+        const f16* r = row_ptr(4 * (idx / kChunks) + rr);
+        const u32x4 x = ld16((r != nullptr ? r : head_pool) + v_off + (idx % kChunks) * 8);
+        st.v[it][rr] = r != nullptr ? x : zero;
+      }
+    }
+  };
+  auto store_tile = [&](int buf, const Stage& st) __attribute__((always_inline)) {  // registers -> LDS (V transposed)
+    f16* ks = k_tile(buf);
+    f16* vt = v_tile(buf);
+#pragma unroll
+    for (int it = 0; it < C::kKPer; ++it) {
+      const int idx = gt + it * C::kGroupThreads;
+      if (idx < C::kKItems)
+        *reinterpret_cast<u32x4*>(ks + (idx / kChunks) * C::kKS + (idx % kChunks) * 8) = st.k[it];
+    }
+#pragma unroll
+    for (int it = 0; it < C::kVPer; ++it) {
+      const int idx = gt + it * C::kGroupThreads;
+      if (idx < C::kVItems) {
+        const int kq = idx / kChunks, c = idx % kChunks;
+        // dim e of the 4 keys -> one 8-byte Vt write; halves picked from 32-bit words by value
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int w = e / 2;
+          const uint32_t a0 = st.v[it][0][w], a1 = st.v[it][1][w], a2 = st.v[it][2][w], a3 = st.v[it][3][w];
+          const u32x2 col4 = (e & 1) == 0
+                                 ? u32x2{(a0 & 0xFFFFu) | (a1 << 16), (a2 & 0xFFFFu) | (a3 << 16)}
+                                 : u32x2{(a0 >> 16) | (a1 & 0xFFFF0000u), (a2 >> 16) | (a3 & 0xFFFF0000u)};
+          *reinterpret_cast<u32x2*>(vt + (c * 8 + e) * C::kVS + 4 * kq) = col4;
+        }
+      }
+    }
+  };
 
   float m = kNegBig, lsum = 0.f;
   f32x16 acc[kDT];
 #pragma unroll
   for (int dt = 0; dt < kDT; ++dt) acc[dt] = f32x16{};
 
-  const int64_t tok_stride = int64_t(num_kv_heads) * D;
-  const int64_t v_off = num_pages * kPBlock * tok_stride;
-  const f16* head_pool = pool + int64_t(kvh) * D;
-
-  for (int kt = k_begin; kt < k_end; kt += kBK) {
-    __syncthreads();  // the previous tile has been consumed by every wave
-    // K tile: Ks[j][:] = K[kt + j], zero beyond k_end or in an invalid page.
-    constexpr int kChunks = D / 8;
-    constexpr int kKItems = kBK * kChunks;
+  auto compute_tile = [&](int t, int buf) __attribute__((always_inline)) {
+    const int kt = t * kPT;
+    const f16* ks = k_tile(buf);
+    const f16* vt = v_tile(buf);
+    f32x16 st = f32x16{};
 #pragma unroll
-    for (int it = 0; it < int(ceil_div(kKItems, C::kThreads)); ++it) {
-      const int idx = tid + it * C::kThreads;
-      if (kKItems % C::kThreads != 0 && idx >= kKItems) break;
-      const int j = idx / kChunks;
-      const int c = idx % kChunks;
-      const int key = kt + j;
-      u32x4 v = u32x4{0u, 0u, 0u, 0u};
-      if (key < k_end) {
-        const int page = table[key / kPBlock];
-        if (page >= 0 && int64_t(page) < num_pages)
-          v = ld16(head_pool + (int64_t(page) * kPBlock + key % kPBlock) * tok_stride + c * 8);
-      }
-      *reinterpret_cast<u32x4*>(&Ks[j][c * 8]) = v;
-    }
-    // V tile, transposed: each item is 4 keys x 8 dims -> 8 rows of Vt with 4 keys each.
-    constexpr int kVItems = (kBK / 4) * kChunks;
-#pragma unroll
-    for (int it = 0; it < int(ceil_div(kVItems, C::kThreads)); ++it) {
-      const int idx = tid + it * C::kThreads;
-      if (kVItems % C::kThreads != 0 && idx >= kVItems) break;
-      const int kq = idx / kChunks;
-      const int c = idx % kChunks;
-      f16x8 rows[4];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int key = kt + 4 * kq + r;
-        u32x4 v = u32x4{0u, 0u, 0u, 0u};
-        if (key < k_end) {
-          const int page = table[key / kPBlock];
-          if (page >= 0 && int64_t(page) < num_pages)
-            v = ld16(head_pool + v_off + (int64_t(page) * kPBlock + key % kPBlock) * tok_stride + c * 8);
-        }
-        rows[r] = as_h8(v);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        f16x4 col4 = f16x4{rows[0][e], rows[1][e], rows[2][e], rows[3][e]};
-        *reinterpret_cast<f16x4*>(&Vt[c * 8 + e][4 * kq]) = col4;
-      }
-    }
-    __syncthreads();
-    if (kt >= wave_key_end) continue;  // every key of this tile is after this wave's queries
-
-    // S^T = K . Q^T for keys kt..kt+63 (two 32-key tiles).
-    f32x16 st[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      st[t] = f32x16{};
-#pragma unroll
-      for (int s = 0; s < kKSteps; ++s) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(&Ks[32 * t + col][16 * s + 8 * half]);
-        st[t] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[s], st[t], 0, 0, 0);
-      }
+    for (int s = 0; s < kKSteps; ++s) {
+      const f16x8 a = *reinterpret_cast<const f16x8*>(ks + col * C::kKS + 16 * s + 8 * half);
+      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[s], st, 0, 0, 0);
     }
     // scale, causal mask (key_pos <= query_pos), online softmax per query column
     float mx = -INFINITY;
 #pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int key = kt + 32 * t + 8 * (r / 4) + 4 * half + (r % 4);
-        float v = st[t][r] * scale_log2;
-        if (key > my_pos || key >= k_end) v = -INFINITY;
-        st[t][r] = v;
-        mx = fmaxf(mx, v);
-      }
+    for (int r = 0; r < 16; ++r) {
+      const int key = kt + 8 * (r / 4) + 4 * half + (r % 4);
+      float v = st[r] * scale_log2;
+      if (key > my_pos || key >= total) v = -INFINITY;
+      st[r] = v;
+      mx = fmaxf(mx, v);
+    }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
     const float mn = fmaxf(m, mx);
     const float alpha = exp2_fast(m - mn);
@@ -217,87 +222,115 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     lsum *= alpha;
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt) acc[dt] *= alpha;
-    f16x8 pb[4];
+    float pv[16];
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float p = exp2_fast(st[u / 2][8 * (u % 2) + e] - mn);
-        lsum += p;
-        pb[u][e] = f16(p);
-      }
+    for (int r = 0; r < 16; ++r) {
+      pv[r] = exp2_fast(st[r] - mn);
+      lsum += pv[r];
+    }
+    // built by value: element-wise writes into a local vector array end up in scratch
+    const f16x8 pb[2] = {
+        f16x8{f16(pv[0]), f16(pv[1]), f16(pv[2]), f16(pv[3]), f16(pv[4]), f16(pv[5]), f16(pv[6]), f16(pv[7])},
+        f16x8{f16(pv[8]), f16(pv[9]), f16(pv[10]), f16(pv[11]), f16(pv[12]), f16(pv[13]), f16(pv[14]),
+              f16(pv[15])}};
     // O^T += V^T . P^T
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int kb = 32 * (u / 2) + 16 * (u % 2);
-        const f16x4 lo = *reinterpret_cast<const f16x4*>(&Vt[32 * dt + col][kb + 4 * half]);
-        const f16x4 hi = *reinterpret_cast<const f16x4*>(&Vt[32 * dt + col][kb + 8 + 4 * half]);
+      for (int u = 0; u < 2; ++u) {
+        const int kb = 16 * u;
+        const f16x4 lo = *reinterpret_cast<const f16x4*>(vt + (32 * dt + col) * C::kVS + kb + 4 * half);
+        const f16x4 hi = *reinterpret_cast<const f16x4*>(vt + (32 * dt + col) * C::kVS + kb + 8 + 4 * half);
         const f16x8 a = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[u], acc[dt], 0, 0, 0);
       }
+  };
+
+  // Sweep: iteration i multiplies the group's tile i*kGroups + grp from LDS buffer i&1; tile i+1
+  // waits in registers and tile i+2's loads are in flight.  Tile i lives in register stage i&1,
+  // so the loop is unrolled by two.  Every iteration ends with one workgroup barrier.
+  auto has = [&](int i) __attribute__((always_inline)) { return i < iters && i * C::kGroups + grp < n_tiles; };
+  Stage s0, s1;
+  if (has(0)) load_tile(0, s0);
+  if (has(1)) load_tile(1, s1);
+  if (has(0)) store_tile(0, s0);
+  __syncthreads();
+  auto step = [&](int i, Stage& next, Stage& free_stage) __attribute__((always_inline)) {
+    if (has(i + 2)) load_tile(i + 2, free_stage);
+    if (has(i)) compute_tile(i * C::kGroups + grp, i & 1);
+    if (has(i + 1)) store_tile((i + 1) & 1, next);
+    __syncthreads();
+  };
+  for (int i = 0; i < iters; i += 2) {
+    step(i, s1, s0);
+    if (i + 1 < iters) step(i + 1, s0, s1);
   }
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
-  if (nsplits == 1) {
-    if (q_ok) {
-      const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-      f16* orow = out + (int64_t(my_q) * hq + head) * D;
+  if constexpr (C::kGroups > 1) {
+    // Log-sum-exp merge of the key groups through LDS: groups 1.. publish, group 0 combines.
+    float* mlb = reinterpret_cast<float*>(smem);                 // [wave][32][2]
+    float* accb = mlb + C::kWaves * 32 * 2;                       // [(grp-1)*G + g][dt][r][lane]
+    if (half == 0) {
+      mlb[(wave * 32 + col) * 2 + 0] = m;
+      mlb[(wave * 32 + col) * 2 + 1] = ltot;
+    }
+    if (grp > 0) {
 #pragma unroll
       for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
-        for (int a4 = 0; a4 < 4; ++a4) {
-          const int d0 = 32 * dt + 8 * a4 + 4 * half;
-          *reinterpret_cast<f16x4*>(orow + d0) =
-              f16x4{f16(acc[dt][4 * a4] * inv), f16(acc[dt][4 * a4 + 1] * inv),
-                    f16(acc[dt][4 * a4 + 2] * inv), f16(acc[dt][4 * a4 + 3] * inv)};
-        }
+        for (int r = 0; r < 16; ++r)
+          accb[((((grp - 1) * G + g) * kDT + dt) * 16 + r) * kWave + lane] = acc[dt][r];
     }
-    return;
-  }
-
-  // split-K partials: unnormalised O plus (m, l), then the last workgroup merges
-  {
-    const int64_t slot = (int64_t(head) * t_pad + my_q) * max_splits + split;
+    __syncthreads();
+    if (grp != 0) return;
+    float mxg = m;
+#pragma unroll
+    for (int k = 1; k < C::kGroups; ++k) mxg = fmaxf(mxg, mlb[((k * G + g) * 32 + col) * 2]);
+    const float w0 = exp2_fast(m - mxg);
+    float L = w0 * ltot;
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt) acc[dt] *= w0;
+#pragma unroll
+    for (int k = 1; k < C::kGroups; ++k) {
+      const float wk = exp2_fast(mlb[((k * G + g) * 32 + col) * 2] - mxg);
+      L = fmaf(wk, mlb[((k * G + g) * 32 + col) * 2 + 1], L);
+#pragma unroll
+      for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r)
+          acc[dt][r] = fmaf(wk, accb[((((k - 1) * G + g) * kDT + dt) * 16 + r) * kWave + lane], acc[dt][r]);
+    }
+    if (!q_ok) return;
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    f16* orow = out + (int64_t(my_q) * hq + head) * D;
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4)
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d0 = 32 * dt + 8 * a4 + 4 * half;
+        *reinterpret_cast<f16x4*>(orow + d0) =
+            f16x4{f16(acc[dt][4 * a4] * inv), f16(acc[dt][4 * a4 + 1] * inv),
+                  f16(acc[dt][4 * a4 + 2] * inv), f16(acc[dt][4 * a4 + 3] * inv)};
+      }
+  } else {
+    if (!q_ok) return;
+    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
+    f16* orow = out + (int64_t(my_q) * hq + head) * D;
 #pragma unroll
-        for (int c = 0; c < 4; ++c)
-          st_dev(ws.o + slot * D + 32 * dt + 8 * a4 + 4 * half + c, acc[dt][4 * a4 + c]);
-    if (half == 0) {
-      st_dev(ws.ml + slot * 2 + 0, m);
-      st_dev(ws.ml + slot * 2 + 1, ltot);
-    }
+    for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d0 = 32 * dt + 8 * a4 + 4 * half;
+        *reinterpret_cast<f16x4*>(orow + d0) =
+            f16x4{f16(acc[dt][4 * a4] * inv), f16(acc[dt][4 * a4 + 1] * inv),
+                  f16(acc[dt][4 * a4 + 2] * inv), f16(acc[dt][4 * a4 + 3] * inv)};
+      }
   }
-  __shared__ uint32_t s_ticket;
-  uint32_t* counter = ws.count + int64_t(qb) * num_kv_heads + kvh;
-  if (!arrive_last(counter, uint32_t(nsplits - 1), &s_ticket)) return;
-  for (int idx = tid; idx < G * C::kBQ * D; idx += C::kThreads) {
-    const int gg = idx / (C::kBQ * D);
-    const int rem = idx % (C::kBQ * D);
-    const int qq = q0 + rem / D;
-    const int d = rem % D;
-    if (qq >= T) continue;
-    const int hh = kvh * G + gg;
-    const int64_t base = (int64_t(hh) * t_pad + qq) * max_splits;
-    float mx = kNegBig;
-    for (int s = 0; s < nsplits; ++s) mx = fmaxf(mx, ld_dev(ws.ml + (base + s) * 2));
-    float L = 0.f, O = 0.f;
-    for (int s = 0; s < nsplits; ++s) {
-      const float wt = exp2_fast(ld_dev(ws.ml + (base + s) * 2) - mx);
-      L = fmaf(wt, ld_dev(ws.ml + (base + s) * 2 + 1), L);
-      O = fmaf(wt, ld_dev(ws.o + (base + s) * D + d), O);
-    }
-    out[(int64_t(qq) * hq + hh) * D + d] = f16(L > 0.f ? O / L : 0.f);
-  }
-  if (tid == 0) reset_ticket(counter);
 }
 
 typedef void (*PrefillKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t,
-                              int32_t, int32_t, float, int32_t, int32_t, int32_t, PrefillWorkspace);
+                              int32_t, int32_t, float);
 
 static PrefillKernel pick_prefill(int d, int g, int* threads) {
 #define IFN_PREFILL_CASE(DD, GG)                          \
@@ -313,13 +346,15 @@ static PrefillKernel pick_prefill(int d, int g, int* threads) {
 
 }  // namespace ifn
 
+// The kernel keeps every partial result on chip, so it needs no workspace; the size
+// reported is a token 256 bytes so that callers sizing a buffer from it stay valid.
 extern "C" size_t ifn_paged_prefill_workspace_bytes(int32_t num_q_tokens, int32_t query_start,
                                                     int32_t num_q_heads, int32_t num_kv_heads,
                                                     int32_t head_dim, int32_t block_size) {
   if (num_q_tokens < 1 || query_start < 0 || num_q_heads < 1 || num_kv_heads < 1 ||
       head_dim < 1 || block_size < 1 || num_q_heads % num_kv_heads != 0)
     return 0;
-  return ifn::plan_prefill(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim).bytes;
+  return 256;
 }
 
 extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_pool_layer,
@@ -329,6 +364,8 @@ extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_po
                                  float scale, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   using namespace ifn;
+  (void)workspace;
+  (void)workspace_bytes;
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_table == nullptr)
     return IFN_ERR_INVALID_ARGUMENT;
   if (num_pages < 1 || max_pages < 1 || query_start < 0 || num_q_tokens < 0 || num_q_heads < 1 ||
@@ -344,22 +381,12 @@ extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_po
   if (num_q_tokens == 0) return IFN_OK;
   if (int64_t(query_start) + num_q_tokens > int64_t(max_pages) * kPBlock)
     return IFN_ERR_INVALID_ARGUMENT;  // keys past the end of the block table
-  const PrefillPlan p = plan_prefill(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim);
-  if (int64_t(p.n_qb) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
-  if (p.max_splits > 1) {
-    if (workspace == nullptr || workspace_bytes < p.bytes) return IFN_ERR_WORKSPACE;
-    IFN_CHECK_ALIGN16(workspace);
-  }
-  PrefillWorkspace ws;
-  uint8_t* wsb = static_cast<uint8_t*>(workspace);
-  ws.count = reinterpret_cast<uint32_t*>(wsb);
-  ws.ml = reinterpret_cast<float*>(wsb + p.off_ml);
-  ws.o = reinterpret_cast<float*>(wsb + p.off_o);
+  const int64_t n_qb = ceil_div(num_q_tokens, 32);
+  if (n_qb * num_kv_heads > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
-  dim3 grid{unsigned(p.max_splits), unsigned(p.n_qb), unsigned(num_kv_heads)};
-  k<<<grid, unsigned(threads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+  k<<<dim3(unsigned(n_qb * num_kv_heads)), unsigned(threads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
-      static_cast<const f16*>(kv_pool_layer), num_pages, block_table, max_pages, query_start,
-      num_q_tokens, num_kv_heads, scale * kLog2e, p.split_keys, p.max_splits, p.t_pad, ws);
+      static_cast<const f16*>(kv_pool_layer), num_pages, block_table, query_start, num_q_tokens,
+      num_kv_heads, int(n_qb), scale * kLog2e);
   return ifn_launch_status();
 }
