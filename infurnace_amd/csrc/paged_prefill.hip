@@ -122,60 +122,89 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     if ((i >> 5) != pid_w) {
       pid_w = i >> 5;
       const int pg = 2 * (grp + C::kGroups * (32 * pid_w + lane / 2)) + (lane & 1);
-      pid = pg < seq_pages ? table[pg] : -1;
+      const int id = table[min(pg, seq_pages - 1)];
+      pid = pg < seq_pages ? id : -1;
+      // Complete the window load here: otherwise the wait for it lands on the v_readlane
+      // below, on every iteration, and drains the tile prefetch each time.
+      asm volatile("" ::"v"(pid));
     }
     pa = __builtin_amdgcn_readlane(pid, 2 * (i & 31));
     pb = __builtin_amdgcn_readlane(pid, 2 * (i & 31) + 1);
   };
 
+  // Per-thread constants of the tile copy: which page half, the element offset inside the page
+  // and the LDS offset of each item (the same for every tile).
+  int k_goff[C::kKPer], k_loff[C::kKPer], v_goff[C::kVPer], v_loff[C::kVPer], v_key[C::kVPer];
+  bool k_hi[C::kKPer], v_hi[C::kVPer];
+#pragma unroll
+  for (int it = 0; it < C::kKPer; ++it) {
+    const int idx = min(gt + it * C::kGroupThreads, C::kKItems - 1);
+    const int j = idx / kChunks, c = idx % kChunks;
+    k_hi[it] = j >= kPBlock;
+    k_goff[it] = (j % kPBlock) * int(tok_stride) + c * 8;
+    k_loff[it] = j * C::kKS + c * 8;
+  }
+#pragma unroll
+  for (int it = 0; it < C::kVPer; ++it) {
+    const int idx = min(gt + it * C::kGroupThreads, C::kVItems - 1);
+    const int kq = idx / kChunks, c = idx % kChunks;
+    v_key[it] = 4 * kq;
+    v_hi[it] = 4 * kq >= kPBlock;
+    v_goff[it] = ((4 * kq) % kPBlock) * int(tok_stride) + c * 8;
+    v_loff[it] = c * 8 * C::kVS + 4 * kq;
+  }
+  const int64_t page_elems = int64_t(kPBlock) * tok_stride;
+
+  // Tile flags (uniform): bit 0/1 = first/second page valid, bit 2 = every key of the tile is
+  // visible to every query of the block (no mask, no zero fill).
+  auto tile_flags = [&](int i, int pa, int pb) __attribute__((always_inline)) -> int {
+    const int kt = (i * C::kGroups + grp) * kPT;
+    const int oka = pa >= 0 && int64_t(pa) < num_pages, okb = pb >= 0 && int64_t(pb) < num_pages;
+    const int full = oka && okb && kt + kPT <= total && kt + kPT - 1 <= query_start + q0;
+    return oka | (okb << 1) | (full << 2);
+  };
+
   struct Stage {
     u32x4 k[C::kKPer];
     u32x4 v[C::kVPer][4];
+    int flags;
   };
-  auto load_tile = [&](int i, Stage& st) __attribute__((always_inline)) {  // global -> registers: this thread's share of the tile
-    const int t = i * C::kGroups + grp;
-    const int kt = t * kPT;
+  // Global -> registers: this thread's share of the tile.  Every address is a real row (an
+  // invalid page reads page 0); masked keys are dealt with in store_tile / compute_tile.
+  auto load_tile = [&](int i, Stage& st) __attribute__((always_inline)) {
     int pa, pb;
     tile_pages(i, pa, pb);
-    auto row_ptr = [&](int j) -> const f16* {  // row j of the tile, or nullptr (zero row)
-      const int page = j < kPBlock ? pa : pb;
-      if (kt + j >= total || page < 0 || int64_t(page) >= num_pages) return nullptr;
-      return head_pool + (int64_t(page) * kPBlock + j % kPBlock) * tok_stride;
-    };
-    // Branch-free: a masked row loads from the head's first row (always valid) and is zeroed.
-    const u32x4 zero = u32x4{0u, 0u, 0u, 0u};
+    st.flags = tile_flags(i, pa, pb);
+    const f16* base_a = head_pool + int64_t((st.flags & 1) ? pa : 0) * page_elems;
+    const f16* base_b = head_pool + int64_t((st.flags & 2) ? pb : 0) * page_elems;
 #pragma unroll
-    for (int it = 0; it < C::kKPer; ++it) {
-      const int idx = min(gt + it * C::kGroupThreads, C::kKItems - 1);
-      const f16* r = row_ptr(idx / kChunks);
-      const u32x4 x = ld16((r != nullptr ? r : head_pool) + (idx % kChunks) * 8);
-      st.k[it] = r != nullptr ? x : zero;
-    }
+    for (int it = 0; it < C::kKPer; ++it) st.k[it] = ld16((k_hi[it] ? base_b : base_a) + k_goff[it]);
 #pragma unroll
-    for (int it = 0; it < C::kVPer; ++it) {
-      const int idx = min(gt + it * C::kGroupThreads, C::kVItems - 1);
+    for (int it = 0; it < C::kVPer; ++it)
 #pragma unroll
-      for (int rr = 0; rr < 4; ++rr) {
-        const f16* r = row_ptr(4 * (idx / kChunks) + rr);
-        const u32x4 x = ld16((r != nullptr ? r : head_pool) + v_off + (idx % kChunks) * 8);
-        st.v[it][rr] = r != nullptr ? x : zero;
-      }
-    }
+      for (int rr = 0; rr < 4; ++rr)
+        st.v[it][rr] = ld16((v_hi[it] ? base_b : base_a) + v_off + v_goff[it] + rr * tok_stride);
   };
-  auto store_tile = [&](int buf, const Stage& st) __attribute__((always_inline)) {  // registers -> LDS (V transposed)
+  auto store_tile = [&](int i, int buf, Stage& st) __attribute__((always_inline)) {  // registers -> LDS
     f16* ks = k_tile(buf);
     f16* vt = v_tile(buf);
+    if (!(st.flags & 4)) {  // zero V rows of keys past the end or in an invalid page (K is masked)
+      const int kt = (i * C::kGroups + grp) * kPT;
 #pragma unroll
-    for (int it = 0; it < C::kKPer; ++it) {
-      const int idx = gt + it * C::kGroupThreads;
-      if (idx < C::kKItems)
-        *reinterpret_cast<u32x4*>(ks + (idx / kChunks) * C::kKS + (idx % kChunks) * 8) = st.k[it];
+      for (int it = 0; it < C::kVPer; ++it)
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          const int key = v_key[it] + rr;
+          const bool ok = ((st.flags >> (key >= kPBlock ? 1 : 0)) & 1) && kt + key < total;
+          st.v[it][rr] = ok ? st.v[it][rr] : u32x4{0u, 0u, 0u, 0u};
+        }
     }
 #pragma unroll
+    for (int it = 0; it < C::kKPer; ++it)
+      if (gt + it * C::kGroupThreads < C::kKItems) *reinterpret_cast<u32x4*>(ks + k_loff[it]) = st.k[it];
+#pragma unroll
     for (int it = 0; it < C::kVPer; ++it) {
-      const int idx = gt + it * C::kGroupThreads;
-      if (idx < C::kVItems) {
-        const int kq = idx / kChunks, c = idx % kChunks;
+      if (gt + it * C::kGroupThreads < C::kVItems) {
         // dim e of the 4 keys -> one 8-byte Vt write; halves picked from 32-bit words by value
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -184,7 +213,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
           const u32x2 col4 = (e & 1) == 0
                                  ? u32x2{(a0 & 0xFFFFu) | (a1 << 16), (a2 & 0xFFFFu) | (a3 << 16)}
                                  : u32x2{(a0 >> 16) | (a1 & 0xFFFF0000u), (a2 >> 16) | (a3 & 0xFFFF0000u)};
-          *reinterpret_cast<u32x2*>(vt + (c * 8 + e) * C::kVS + 4 * kq) = col4;
+          *reinterpret_cast<u32x2*>(vt + v_loff[it] + e * C::kVS) = col4;
         }
       }
     }
@@ -195,8 +224,8 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 #pragma unroll
   for (int dt = 0; dt < kDT; ++dt) acc[dt] = f32x16{};
 
-  auto compute_tile = [&](int t, int buf) __attribute__((always_inline)) {
-    const int kt = t * kPT;
+  auto compute_tile = [&](int i, int buf, int flags) __attribute__((always_inline)) {
+    const int kt = (i * C::kGroups + grp) * kPT;
     const f16* ks = k_tile(buf);
     const f16* vt = v_tile(buf);
     f32x16 st = f32x16{};
@@ -205,27 +234,32 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
       const f16x8 a = *reinterpret_cast<const f16x8*>(ks + col * C::kKS + 16 * s + 8 * half);
       st = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[s], st, 0, 0, 0);
     }
-    // scale, causal mask (key_pos <= query_pos), online softmax per query column
-    float mx = -INFINITY;
+    // causal mask (key_pos <= query_pos), end of sequence and invalid pages -- only on tiles
+    // that are not entirely visible; raw scores, the scale is folded into the exponent below
+    if (!(flags & 4)) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = kt + 8 * (r / 4) + 4 * half + (r % 4);
-      float v = st[r] * scale_log2;
-      if (key > my_pos || key >= total) v = -INFINITY;
-      st[r] = v;
-      mx = fmaxf(mx, v);
+      for (int r = 0; r < 16; ++r) {
+        const int kk = 8 * (r / 4) + 4 * half + (r % 4);
+        const bool ok = ((flags >> (kk >= kPBlock ? 1 : 0)) & 1) && kt + kk <= my_pos && kt + kk < total;
+        st[r] = ok ? st[r] : -INFINITY;
+      }
     }
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m, mx);
-    const float alpha = exp2_fast(m - mn);
-    m = mn;
-    lsum *= alpha;
+    float mx = st[0];
 #pragma unroll
-    for (int dt = 0; dt < kDT; ++dt) acc[dt] *= alpha;
+    for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[r]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mn = fmaxf(m, mx * scale_log2);
+    if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {  // some running max moved: rescale
+      const float alpha = exp2_fast(m - mn);
+      lsum *= alpha;
+#pragma unroll
+      for (int dt = 0; dt < kDT; ++dt) acc[dt] *= alpha;
+    }
+    m = mn;
     float pv[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      pv[r] = exp2_fast(st[r] - mn);
+      pv[r] = exp2_fast(fmaf(st[r], scale_log2, -mn));
       lsum += pv[r];
     }
     // built by value: element-wise writes into a local vector array end up in scratch
@@ -251,14 +285,22 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   // so the loop is unrolled by two.  Every iteration ends with one workgroup barrier.
   auto has = [&](int i) __attribute__((always_inline)) { return i < iters && i * C::kGroups + grp < n_tiles; };
   Stage s0, s1;
-  if (has(0)) load_tile(0, s0);
-  if (has(1)) load_tile(1, s1);
-  if (has(0)) store_tile(0, s0);
+  s0.flags = s1.flags = 0;
+  // Loads are unconditional (tiles past the end read page 0 and are never used): with a fixed
+  // number of loads per iteration, waiting for tile i+1 never waits for tile i+2.
+  load_tile(0, s0);
+  load_tile(1, s1);
+#pragma unroll
+  for (int st = 0; st < kKSteps; ++st) asm volatile("" ::"v"(qreg[st]));  // query loads done before the loop
+  if (has(0)) store_tile(0, 0, s0);
   __syncthreads();
+  int cur_flags = s0.flags;
   auto step = [&](int i, Stage& next, Stage& free_stage) __attribute__((always_inline)) {
-    if (has(i + 2)) load_tile(i + 2, free_stage);
-    if (has(i)) compute_tile(i * C::kGroups + grp, i & 1);
-    if (has(i + 1)) store_tile((i + 1) & 1, next);
+    const int fl = cur_flags;
+    load_tile(i + 2, free_stage);
+    if (has(i)) compute_tile(i, i & 1, fl);
+    if (has(i + 1)) store_tile(i + 1, (i + 1) & 1, next);
+    cur_flags = next.flags;
     __syncthreads();
   };
   for (int i = 0; i < iters; i += 2) {

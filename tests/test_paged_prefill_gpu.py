@@ -95,3 +95,41 @@ def test_workspace_reuse_and_bad_pages(dev):
     c = paged_attention(Q, P, to_dev(bad, dev), None, None, query_start=1536)
     torch.cuda.synchronize()
     assert torch.isfinite(c.float()).all()
+
+
+def _masked_reference(q, pool, table, start, skip_pages):
+    """float64 causal attention over keys [0, start + i], leaving out every key of the logical pages in
+    skip_pages (the documented meaning of a page id outside [0, num_pages): it contributes no keys)."""
+    T, hq, d = q.shape
+    hkv = pool.shape[3]
+    g = hq // hkv
+    total = start + T
+    keys = [k for k in range(total) if k // 16 not in skip_pages]
+    kk = np.stack([pool[0, table[k // 16], k % 16] for k in keys]).astype(np.float64)  # [n, hkv, d]
+    vv = np.stack([pool[1, table[k // 16], k % 16] for k in keys]).astype(np.float64)
+    kpos = np.asarray(keys)
+    out = np.zeros((T, hq, d))
+    for i in range(T):
+        vis = kpos <= start + i
+        for h in range(hq):
+            s = kk[vis, h // g] @ q[i, h].astype(np.float64) / np.sqrt(d)
+            p = np.exp(s - s.max())
+            out[i, h] = (p[:, None] * vv[vis, h // g]).sum(0) / p.sum()
+    return out
+
+
+def test_invalid_page_contributes_no_keys(dev):
+    say("prefill invalid page id -> its keys are skipped")
+    rng = np.random.default_rng(31)
+    start, T = 40, 30
+    pool, table = _seq(rng, start + T, 16, 8, 128)
+    q = rng.standard_normal((T, 16, 128), dtype=np.float32).astype(np.float16)
+    bad = table.copy()
+    bad[2] = pool.shape[1] + 3  # logical page 2 = keys 32..47
+    out = paged_attention(to_dev(q, dev), to_dev(pool, dev), to_dev(bad, dev), None, None, query_start=start)
+    ref = _masked_reference(q, pool, table, start, {2})
+    assert_attn_close(out, ref.astype(np.float32), "invalid page 2")
+    # negative ids too
+    bad[2] = -1
+    out = paged_attention(to_dev(q, dev), to_dev(pool, dev), to_dev(bad, dev), None, None, query_start=start)
+    assert_attn_close(out, ref.astype(np.float32), "page id -1")
