@@ -47,13 +47,6 @@ constexpr int kMaxBatch = kRowInts - 1;
 constexpr int kMaxWaves = 1024 * kWavesPerBlock;  // waves of a launch are capped at this
 constexpr int kXcds = 8;            // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 
-// Register-ring depth: as deep as 256 VGPRs (two waves per SIMD) allow.
-template <int D, int G>
-struct DecodeStages {
-  static constexpr int kChunks = G * (D / 64);  // accumulator chunks per lane
-  static constexpr int value = kChunks <= 2 ? 4 : (kChunks <= 4 ? 3 : 2);
-};
-
 struct DecodeWorkspace {
   uint32_t* count;  // [batch * num_kv_heads] tickets, zero between calls
   float* ml;        // [slot][G][2]  (max in log2 units, sum); slot = segment + wave
@@ -201,7 +194,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, int32_t batch,
     int32_t num_kv_heads, int32_t max_len, float scale_log2, DecodeWorkspace ws) {
   constexpr int NC = D / 64;  // 16-byte chunks per lane per token row
-  constexpr int S = DecodeStages<D, G>::value;
+  constexpr int S = 2;  // register-ring stages (measured: deeper rings were no faster)
   __shared__ int s_off[kRowInts];  // s_off[b] = pages of rows < b; s_off[batch] = total
   __shared__ int s_len[kRowInts];  // keys of row b (0 for inactive rows)
   __shared__ int s_wsum[kWavesPerBlock];
@@ -290,34 +283,83 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
 
   auto run_range = [&](int64_t r, int64_t u_lo, int64_t u_hi) {
     int pend_n = 0, pend_seg0 = 0, pend_seg1 = 0, pend_first0 = 0, pend_first1 = 0, pend_np0 = 0, pend_np1 = 0;
-    for (int64_t u = u_lo; u < u_hi;) {  // one piece per iteration (uniform loop)
-      // unit u -> (row b, kv head, first page): last row whose first unit is <= u
-      int lo = 0, hi = batch - 1;
+    struct Piece {
+      int b, kvh, seg, page0, np, len;
+      int64_t seg_start, seg_end;
+    };
+    auto locate = [&](int64_t u) -> Piece {  // unit u -> the piece of this range that starts at u
+      int lo = 0, hi = batch - 1;              // last row whose first unit is <= u
       while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
         if (int64_t(s_off[mid]) * num_kv_heads <= u) lo = mid; else hi = mid - 1;
       }
-      const int b = __builtin_amdgcn_readfirstlane(lo);
-      const int pages_b = s_off[b + 1] - s_off[b];
-      const int64_t row_start = int64_t(s_off[b]) * num_kv_heads;
-      const int kvh = int((u - row_start) / pages_b);
-      const int64_t seg_start = row_start + int64_t(kvh) * pages_b;
-      const int64_t seg_end = seg_start + pages_b;
-      const int page0 = int(u - seg_start);
-      const int np = int(min(u_hi, seg_end) - u);  // pages of this piece
-      const int seg = b * num_kv_heads + kvh;
-      const int len = s_len[b];
-      u += np;
-
-      // query of the GQA group and the piece's page ids (64 per lane window)
-      const f16* qs = q + int64_t(seg) * G * D;  // rows (b, kvh*G + g)
+      Piece P;
+      P.b = __builtin_amdgcn_readfirstlane(lo);
+      const int pages_b = s_off[P.b + 1] - s_off[P.b];
+      const int64_t row_start = int64_t(s_off[P.b]) * num_kv_heads;
+      P.kvh = int((u - row_start) / pages_b);
+      P.seg_start = row_start + int64_t(P.kvh) * pages_b;
+      P.seg_end = P.seg_start + pages_b;
+      P.page0 = int(u - P.seg_start);
+      P.np = int(min(u_hi, P.seg_end) - u);
+      P.seg = P.b * num_kv_heads + P.kvh;
+      P.len = s_len[P.b];
+      return P;
+    };
+    // Query rows of a piece and its first two 64-page windows of ids.  The loads are
+    // unconditional (indices clamped into the piece): a fixed number of outstanding loads
+    // lets every later wait count exactly.
+    auto fetch_q = [&](const Piece& P, f16x8 (&qr)[G][NC]) {
+      const f16* qs = q + int64_t(P.seg) * G * D;  // rows (b, kvh*G + g)
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int ch = 0; ch < NC; ++ch) qv[g][ch] = as_h8(ld16(qs + g * D + (col + 8 * ch) * 8));
-      const int32_t* bt = block_tables + int64_t(b) * max_pages + page0;
-      int ids0 = lane < np ? bt[lane] : 0;
-      int ids1 = lane + kWave < np ? bt[lane + kWave] : 0;
+        for (int ch = 0; ch < NC; ++ch) qr[g][ch] = as_h8(ld16(qs + g * D + (col + 8 * ch) * 8));
+    };
+    auto fetch_ids = [&](const Piece& P, int& i0, int& i1) {
+      const int32_t* bt = block_tables + int64_t(P.b) * max_pages + P.page0;
+      i0 = bt[min(lane, P.np - 1)];
+      i1 = bt[min(lane + kWave, P.np - 1)];
+    };
+    auto head_of = [&](const Piece& P) {
+      return pool + int64_t(P.kvh) * D + int64_t(row) * tok_stride + col * 8;
+    };
+    auto issue = [&](const f16* hb, int phys, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool& ok) {
+      ok = phys >= 0 && int64_t(phys) < num_pages;
+      const f16* base = hb + int64_t(ok ? phys : 0) * page_elems;
+#pragma unroll
+      for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+        for (int ch = 0; ch < NC; ++ch) {
+          kr[tt][ch] = ld16(base + tt * 8 * tok_stride + ch * 64);
+          vr[tt][ch] = ld16(base + v_off + tt * 8 * tok_stride + ch * 64);
+        }
+    };
+
+    // The next piece is located, and its query and page ids requested, when the current
+    // piece starts; its first page is requested before the current piece's row merge and
+    // stores.  A piece therefore starts with its data in flight instead of paying a chain of
+    // dependent loads.
+    // With few accumulator chunks the next query goes to a second register set while the
+    // current piece streams; otherwise (register budget) it is loaded into the live set once the
+    // last page has been consumed, and arrives during the row merge.
+    constexpr bool kPrefetchQ = G * NC <= 4;
+    Piece cur = locate(u_lo);
+    int ids0, ids1, nid0, nid1;
+    f16x8 qn[kPrefetchQ ? G : 1][NC];
+    fetch_q(cur, qv);
+    fetch_ids(cur, ids0, ids1);
+    issue(head_of(cur), __builtin_amdgcn_readlane(ids0, 0), kb[0], vb[0], okb[0]);
+    for (int64_t u = u_lo;;) {  // one piece per iteration (uniform loop)
+      const int np = cur.np, page0 = cur.page0, len = cur.len, seg = cur.seg;
+      const int64_t seg_start = cur.seg_start, seg_end = cur.seg_end;
+      const bool has_next = u + np < u_hi;
+      const Piece nxt = has_next ? locate(u + np) : cur;
+      if constexpr (kPrefetchQ) fetch_q(nxt, qn);
+      fetch_ids(nxt, nid0, nid1);
+      const int32_t* bt = block_tables + int64_t(cur.b) * max_pages + page0;
+      const f16* head_base = head_of(cur);
+      const f16* head_next = head_of(nxt);
       int cur_w = 0;
       auto page_id = [&](int k) -> int {
         const int j = k & (kWave - 1);
@@ -327,22 +369,15 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
         if ((k >> 6) != cur_w) {
           ids0 = ids1;
           cur_w = k >> 6;
-          const int nxt = kWave * (cur_w + 1) + lane;
-          ids1 = nxt < np ? bt[nxt] : 0;
+          ids1 = bt[min(kWave * (cur_w + 1) + lane, np - 1)];
         }
       };
-      const f16* head_base = pool + int64_t(kvh) * D + int64_t(row) * tok_stride + col * 8;
+      // page k of the piece; k == np is the next piece's first page
       auto load_page = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool& ok) {
-        const int phys = page_id(k < np ? k : np - 1);  // past the end: re-read the last page (L2 hit)
-        ok = phys >= 0 && int64_t(phys) < num_pages;
-        const f16* base = head_base + int64_t(ok ? phys : 0) * page_elems;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-          for (int ch = 0; ch < NC; ++ch) {
-            kr[tt][ch] = ld16(base + tt * 8 * tok_stride + ch * 64);
-            vr[tt][ch] = ld16(base + v_off + tt * 8 * tok_stride + ch * 64);
-          }
+        if (k < np)
+          issue(head_base, page_id(k), kr, vr, ok);
+        else if (has_next)
+          issue(head_next, __builtin_amdgcn_readlane(nid0, 0), kr, vr, ok);
       };
       auto consume = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool ok) {
         const int p = page0 + k;
@@ -391,26 +426,28 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
 #pragma unroll
           for (int e = 0; e < 8; ++e) acc[g][ch][e] = 0.f;
       }
-      // S-stage register ring over the piece: page k+S-1 is requested while page k is
-      // consumed; the scheduling barriers keep the loads ahead of the arithmetic.
-#pragma unroll
-      for (int j = 0; j < S - 1; ++j) load_page(j, kb[j], vb[j], okb[j]);
+      // Two-stage register ring: page k+1 is requested while page k is consumed (page k lives
+      // in slot k & 1; page 0 is already in flight).  The scheduling barriers keep the loads
+      // ahead of the arithmetic.
       int k = 0;
-      for (; k + S <= np; k += S) {
-#pragma unroll
-        for (int j = 0; j < S; ++j) {
-          shift(k + j);
-          load_page(k + j + S - 1, kb[(j + S - 1) % S], vb[(j + S - 1) % S], okb[(j + S - 1) % S]);
-          __builtin_amdgcn_sched_barrier(0);
-          consume(k + j, kb[j], vb[j], okb[j]);
-        }
+      for (; k + 2 <= np; k += 2) {
+        shift(k);
+        load_page(k + 1, kb[1], vb[1], okb[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        consume(k, kb[0], vb[0], okb[0]);
+        shift(k + 1);
+        load_page(k + 2, kb[0], vb[0], okb[0]);  // k + 2 == np: the next piece's first page
+        __builtin_amdgcn_sched_barrier(0);
+        consume(k + 1, kb[1], vb[1], okb[1]);
       }
-#pragma unroll
-      for (int j = 0; j < S - 1; ++j)  // tail: fewer than S pages left, all requested
-        if (k + j < np) {
-          shift(k + j);
-          consume(k + j, kb[j], vb[j], okb[j]);
-        }
+      if (k < np) {  // odd page count: the last page sits in slot 0
+        shift(k);
+        consume(k, kb[0], vb[0], okb[0]);
+        if (has_next) issue(head_next, __builtin_amdgcn_readlane(nid0, 0), kb[0], vb[0], okb[0]);
+      }
+      if constexpr (!kPrefetchQ) {
+        if (has_next) fetch_q(nxt, qv);
+      }
 
       // Merge the 8 lane rows: (m, l) by butterflies; O by a reduce-scatter after which lane
       // 8*row + col holds element e = row of its column, i.e. output dim (col + 8*ch)*8 + row.
@@ -466,6 +503,17 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
           pend_seg1 = seg; pend_first1 = int(w_first); pend_np1 = np_seg;
         }
         pend_n = pend_n + 1;
+      }
+      if (!has_next) break;
+      u += np;
+      cur = nxt;
+      ids0 = nid0;
+      ids1 = nid1;
+      if constexpr (kPrefetchQ) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int ch = 0; ch < NC; ++ch) qv[g][ch] = qn[g][ch];
       }
     }
     if (pend_n == 0) return;
