@@ -179,6 +179,61 @@ def run_prefill(lib, hip, dev, g, stream) -> dict:
             "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
 
 
+def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> dict:
+    """Decode leg for a second or third workload (configs 4 and 5): `layers` distinct layer pools,
+    store_kv (one token per row) then decode per layer; HIP events around every decode launch.
+    For a table with shared pages the roofline counts each physical page once (`unique`); the
+    logical K/V a launch attends is reported beside it."""
+    import torch
+    B, hq, hkv, d, P = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.num_pages
+    pool = torch.empty((layers, 2, P, 16, hkv, d), dtype=torch.float16, device=dev)
+    for layer in range(layers):
+        pool[layer].normal_(generator=g)
+    q = torch.randn((layers, B, hq, d), generator=g, device=dev, dtype=torch.float16)
+    nk = torch.randn((layers, B, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty((B, hq, d), dtype=torch.float16, device=dev)
+    bt = torch.from_numpy(w.block_tables).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    slots = torch.from_numpy(w.append_slots).to(dev)
+    max_len = int(w.seq_lens.max())
+    ws_bytes = lib.ifn_paged_decode_workspace_bytes(B, hq, hkv, d, 16, max_len)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    lb = pool[0].numel() * 2
+    scale = 1.0 / np.sqrt(d)
+
+    def one(layer, evs=None, j=0):
+        rc = lib.ifn_store_kv(pool.data_ptr() + layer * lb, P, slots.data_ptr(), None, nk[layer].data_ptr(),
+                              nk[layer].data_ptr(), B, hkv, d, 16, stream)
+        if evs is not None:
+            hip.hip.hipEventRecord(evs[2 * j], stream)
+        rc |= lib.ifn_paged_decode(out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P, bt.data_ptr(),
+                                   w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, ws.data_ptr(),
+                                   ws_bytes, stream)
+        if evs is not None:
+            hip.hip.hipEventRecord(evs[2 * j + 1], stream)
+        if rc:
+            raise RuntimeError(f"{w.name}: launch failed: {rc}")
+
+    for layer in range(layers):
+        one(layer)
+    torch.cuda.synchronize()
+    n = layers * reps
+    evs = hip.create(2 * n)
+    for r in range(reps):
+        for layer in range(layers):
+            one(layer, evs, r * layers + layer)
+    torch.cuda.synchronize()
+    us = float(np.mean([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(n)])) * 1e3
+    hip.destroy(evs)
+    del pool
+    uniq = w.decode_bytes(unique=True)
+    logical = w.decode_bytes()
+    gbps = uniq / (us / 1e6) / 1e9
+    return {"workload": w.name, "layers_timed": layers, "reps": reps, "decode_us_per_layer": round(us, 2),
+            "bytes_per_layer": uniq, "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
+            "logical_bytes_per_layer": logical, "effective_GB/s": round(logical / (us / 1e6) / 1e9, 1)}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -187,6 +242,7 @@ def main() -> int:
     ap.add_argument("--cpu-seconds", type=float, default=12.0)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-prefill", action="store_true", help="skip the config-3 chunked-prefill leg")
+    ap.add_argument("--no-extra", action="store_true", help="skip the config-4 and config-5 decode legs")
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 counter passes: no CPU baseline, no prefill leg, plus one "
                          "1 GiB elementwise copy (torch.neg) whose FETCH/WRITE counters calibrate HBM bytes")
@@ -194,6 +250,7 @@ def main() -> int:
     if args.profile_pass:
         args.no_cpu_baseline = True
         args.no_prefill = True
+        args.no_extra = True
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (asked for --gpus {args.gpus}); the hot path shards by sequence "
               "with no exchange, so N GPUs run N independent copies of this benchmark.", file=sys.stderr)
@@ -306,6 +363,20 @@ def main() -> int:
     if not args.no_prefill:
         prefill = run_prefill(lib, hip, dev, g, stream)
 
+    extra = {}
+    if not args.no_extra:
+        cpu_pool = pool[0].cpu() if not args.no_cpu_baseline else None  # the CPU leg reads layer 0
+        del pool
+        torch.cuda.empty_cache()
+        print("[bench] config 4 (8.6 GB per layer) ...", file=sys.stderr, flush=True)
+        extra["config4"] = run_decode_config(lib, hip, dev, g, stream, workloads.config4(), layers=1, reps=10)
+        torch.cuda.empty_cache()
+        print("[bench] config 5 (Qwen3-8B shapes, shared prefix) ...", file=sys.stderr, flush=True)
+        extra["config5"] = run_decode_config(lib, hip, dev, g, stream, workloads.config5(), layers=36, reps=3)
+        torch.cuda.empty_cache()
+    else:
+        cpu_pool = pool[0]
+
     if args.profile_pass:
         src = torch.empty(1 << 29, dtype=torch.float16, device=dev).normal_(generator=g)
         dst = torch.empty_like(src)
@@ -316,7 +387,7 @@ def main() -> int:
     cpu = None
     if not args.no_cpu_baseline:
         print("[bench] CPU baseline ...", file=sys.stderr, flush=True)
-        cpu = run_cpu_baseline(w, pool[0], q[0], args.cpu_seconds)
+        cpu = run_cpu_baseline(w, cpu_pool, q[0], args.cpu_seconds)
 
     result = {
         "metric": METRIC,
@@ -344,6 +415,8 @@ def main() -> int:
                            "us": round(a_ms * 1e3, 2), "bytes": a_bytes, "GB/s": round(a_gbps, 2),
                            "frac": round(a_gbps / HBM_PEAK_GBPS, 4)},
         "prefill": prefill,
+        "config4": extra.get("config4"),
+        "config5": extra.get("config5"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)
