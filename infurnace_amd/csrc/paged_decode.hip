@@ -68,21 +68,6 @@ static inline size_t decode_ws_layout(int32_t batch, int32_t hkv, int32_t g, int
   return off;
 }
 
-// Number of CUs of the current device (queried once per device; 0 when there is none).
-static int device_cu_count() {
-  static std::atomic<int> cache[64];
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  if (dev >= 0 && dev < 64) {
-    const int c = cache[dev].load(std::memory_order_relaxed);
-    if (c > 0) return c;
-  }
-  int n = 0;
-  if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
-  if (dev >= 0 && dev < 64) cache[dev].store(n, std::memory_order_relaxed);
-  return n;
-}
-
 // Workgroups of a decode launch: one per CU (capped so waves <= kMaxWaves).
 static int decode_blocks() {
   int cus = device_cu_count();

@@ -40,6 +40,42 @@
 namespace ifn {
 
 constexpr int kPBlock = 16;  // tokens per page compiled in
+constexpr int kMaxSplit = 4;  // workgroups per (query block, kv head) at most
+
+struct PrefillWorkspace {
+  uint32_t* count;  // [query block][kv head][G] tickets, zero between calls
+  float* ml;        // [pair][split][64 lanes][2]   (m in log2 units, l)
+  float* o;         // [pair][split][D/32][16][64 lanes] unnormalised outputs
+};
+
+struct PrefillPlan {
+  int64_t n_qb;
+  int nsplit;
+  size_t off_ml, off_o, bytes;
+};
+
+// Key split: enough workgroups to cover the CUs when (query blocks x kv heads) alone does not,
+// provided every split still gets at least two tiles per key group.
+static PrefillPlan plan_prefill(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
+  PrefillPlan p;
+  const int g = hq / hkv;
+  const int groups = g >= 8 ? 1 : (g >= 4 ? 2 : 4);
+  p.n_qb = (int64_t(T) + 31) / 32;
+  const int64_t units = p.n_qb * hkv;
+  const int64_t max_tiles = (int64_t(query_start) + T + 31) / 32;
+  int ns = 1;
+  while (ns < kMaxSplit && units * ns * 2 <= cus && max_tiles >= int64_t(2 * ns) * 2 * groups) ns *= 2;
+  if (units * g > kMaxTickets) ns = 1;
+  p.nsplit = ns;
+  const size_t slots = size_t(units) * g * ns;
+  size_t off = kTicketBytes;
+  p.off_ml = off;
+  off = (off + slots * 64 * 2 * sizeof(float) + 255) & ~size_t(255);
+  p.off_o = off;
+  off = (off + slots * size_t(d) / 32 * 16 * 64 * sizeof(float) + 255) & ~size_t(255);
+  p.bytes = ns > 1 ? off : 256;
+  return p;
+}
 constexpr int kPT = 32;      // keys per tile (one 32x32 MFMA tile)
 
 template <int D, int G>
@@ -66,15 +102,18 @@ template <int D, int G>
 __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
     int64_t num_pages, const int32_t* __restrict__ table, int32_t query_start, int32_t T,
-    int32_t num_kv_heads, int32_t n_qb, float scale_log2) {
+    int32_t num_kv_heads, int32_t n_qb, int32_t nsplit, float scale_log2, PrefillWorkspace ws) {
   using C = PrefillCfg<D, G>;
   constexpr int kDT = C::kDT;
   constexpr int kKSteps = D / 16;
   constexpr int kChunks = D / 8;
   // Workgroup i runs on XCD i % 8: kv head = i % Hkv keeps each head's K/V in one XCD's L2
   // (for Hkv = 8), and query blocks go longest key range first.
+  // The nsplit workgroups of one (query block, kv head) take interleaved key tiles and merge
+  // through the workspace at the end.
   const int kvh = int(blockIdx.x) % num_kv_heads;
-  const int qb = n_qb - 1 - int(blockIdx.x) / num_kv_heads;
+  const int split = (int(blockIdx.x) / num_kv_heads) % nsplit;
+  const int qb = n_qb - 1 - int(blockIdx.x) / (num_kv_heads * nsplit);
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
@@ -87,7 +126,10 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   const int q0 = qb * 32;
   const int key_end = min(total, query_start + q0 + 32);  // keys some query of the block sees
   const int n_tiles = int(ceil_div(key_end, kPT));
-  const int iters = int(ceil_div(n_tiles, C::kGroups));
+  // tile of iteration i for this wave's key group: (i * nsplit + split) * kGroups + grp
+  auto tile_of = [&](int i) { return (i * nsplit + split) * C::kGroups + grp; };
+  const int first = split * C::kGroups;  // first tile of this workgroup (group 0)
+  const int iters = n_tiles > first ? int(ceil_div(n_tiles - first, C::kGroups * nsplit)) : 0;
 
   const int col = lane % 32;  // this lane's query column / K row within a tile
   const int half = lane / 32;
@@ -121,7 +163,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   auto tile_pages = [&](int i, int& pa, int& pb) __attribute__((always_inline)) {  // pages of the group's tile of iteration i
     if ((i >> 5) != pid_w) {
       pid_w = i >> 5;
-      const int pg = 2 * (grp + C::kGroups * (32 * pid_w + lane / 2)) + (lane & 1);
+      const int pg = 2 * tile_of(32 * pid_w + lane / 2) + (lane & 1);
       const int id = table[min(pg, seq_pages - 1)];
       pid = pg < seq_pages ? id : -1;
       // Complete the window load here: otherwise the wait for it lands on the v_readlane
@@ -158,7 +200,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   // Tile flags (uniform): bit 0/1 = first/second page valid, bit 2 = every key of the tile is
   // visible to every query of the block (no mask, no zero fill).
   auto tile_flags = [&](int i, int pa, int pb) __attribute__((always_inline)) -> int {
-    const int kt = (i * C::kGroups + grp) * kPT;
+    const int kt = tile_of(i) * kPT;
     const int oka = pa >= 0 && int64_t(pa) < num_pages, okb = pb >= 0 && int64_t(pb) < num_pages;
     const int full = oka && okb && kt + kPT <= total && kt + kPT - 1 <= query_start + q0;
     return oka | (okb << 1) | (full << 2);
@@ -189,7 +231,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     f16* ks = k_tile(buf);
     f16* vt = v_tile(buf);
     if (!(st.flags & 4)) {  // zero V rows of keys past the end or in an invalid page (K is masked)
-      const int kt = (i * C::kGroups + grp) * kPT;
+      const int kt = tile_of(i) * kPT;
 #pragma unroll
       for (int it = 0; it < C::kVPer; ++it)
 #pragma unroll
@@ -225,7 +267,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   for (int dt = 0; dt < kDT; ++dt) acc[dt] = f32x16{};
 
   auto compute_tile = [&](int i, int buf, int flags) __attribute__((always_inline)) {
-    const int kt = (i * C::kGroups + grp) * kPT;
+    const int kt = tile_of(i) * kPT;
     const f16* ks = k_tile(buf);
     const f16* vt = v_tile(buf);
     f32x16 st = f32x16{};
@@ -283,7 +325,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   // Sweep: iteration i multiplies the group's tile i*kGroups + grp from LDS buffer i&1; tile i+1
   // waits in registers and tile i+2's loads are in flight.  Tile i lives in register stage i&1,
   // so the loop is unrolled by two.  Every iteration ends with one workgroup barrier.
-  auto has = [&](int i) __attribute__((always_inline)) { return i < iters && i * C::kGroups + grp < n_tiles; };
+  auto has = [&](int i) __attribute__((always_inline)) { return i < iters && tile_of(i) < n_tiles; };
   Stage s0, s1;
   s0.flags = s1.flags = 0;
   // Loads are unconditional (tiles past the end read page 0 and are never used): with a fixed
@@ -309,6 +351,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   }
 
   const float ltot = lsum + __shfl_xor(lsum, 32);
+  float mfin = m, lfin = ltot;
   if constexpr (C::kGroups > 1) {
     // Log-sum-exp merge of the key groups through LDS: groups 1.. publish, group 0 combines.
     float* mlb = reinterpret_cast<float*>(smem);                 // [wave][32][2]
@@ -343,36 +386,74 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
         for (int r = 0; r < 16; ++r)
           acc[dt][r] = fmaf(wk, accb[((((k - 1) * G + g) * kDT + dt) * 16 + r) * kWave + lane], acc[dt][r]);
     }
-    if (!q_ok) return;
-    const float inv = L > 0.f ? 1.f / L : 0.f;
-    f16* orow = out + (int64_t(my_q) * hq + head) * D;
-#pragma unroll
-    for (int dt = 0; dt < kDT; ++dt)
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int d0 = 32 * dt + 8 * a4 + 4 * half;
-        *reinterpret_cast<f16x4*>(orow + d0) =
-            f16x4{f16(acc[dt][4 * a4] * inv), f16(acc[dt][4 * a4 + 1] * inv),
-                  f16(acc[dt][4 * a4 + 2] * inv), f16(acc[dt][4 * a4 + 3] * inv)};
-      }
-  } else {
-    if (!q_ok) return;
-    const float inv = ltot > 0.f ? 1.f / ltot : 0.f;
-    f16* orow = out + (int64_t(my_q) * hq + head) * D;
-#pragma unroll
-    for (int dt = 0; dt < kDT; ++dt)
-#pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4) {
-        const int d0 = 32 * dt + 8 * a4 + 4 * half;
-        *reinterpret_cast<f16x4*>(orow + d0) =
-            f16x4{f16(acc[dt][4 * a4] * inv), f16(acc[dt][4 * a4 + 1] * inv),
-                  f16(acc[dt][4 * a4 + 2] * inv), f16(acc[dt][4 * a4 + 3] * inv)};
-      }
+    mfin = mxg;
+    lfin = L;
   }
+
+  if (nsplit > 1) {
+    // Cross-workgroup merge: publish this split's (m, l, O) for head g with device-coherent
+    // stores (lane-contiguous), wait for them, take the (query block, head) ticket; the last of
+    // the nsplit arrivals combines the others' partials with its own registers.
+    constexpr int kSlotO = kDT * 16 * kWave;  // floats of O per (pair, split)
+    const int64_t pair = (int64_t(qb) * num_kv_heads + kvh) * G + g;
+    const int64_t slot = pair * nsplit + split;
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) st_dev(ws.o + slot * kSlotO + (dt * 16 + r) * kWave + lane, acc[dt][r]);
+    st_dev(ws.ml + (slot * kWave + lane) * 2 + 0, mfin);
+    st_dev(ws.ml + (slot * kWave + lane) * 2 + 1, lfin);
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial is acknowledged
+    uint32_t t = 0;
+    if (lane == 0) t = __hip_atomic_fetch_add(ws.count + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    t = __builtin_amdgcn_readfirstlane(t);
+    if (t != uint32_t(nsplit - 1)) return;
+    // Combine every split's partial -- this wave's own included, read back from memory -- in
+    // split order, so the result does not depend on which workgroup arrived last.
+    float mo[kMaxSplit], lo[kMaxSplit];
+    float mx = kNegBig;
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxSplit; ++s2) {
+      if (s2 < nsplit) {
+        mo[s2] = ld_dev(ws.ml + ((pair * nsplit + s2) * kWave + lane) * 2 + 0);
+        lo[s2] = ld_dev(ws.ml + ((pair * nsplit + s2) * kWave + lane) * 2 + 1);
+        mx = fmaxf(mx, mo[s2]);
+      }
+    }
+    lfin = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt) acc[dt] = f32x16{};
+#pragma unroll
+    for (int s2 = 0; s2 < kMaxSplit; ++s2) {
+      if (s2 < nsplit) {
+        const float wk = exp2_fast(mo[s2] - mx);
+        lfin = fmaf(wk, lo[s2], lfin);
+        const float* so = ws.o + (pair * nsplit + s2) * kSlotO;
+#pragma unroll
+        for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(wk, ld_dev(so + (dt * 16 + r) * kWave + lane), acc[dt][r]);
+      }
+    }
+    if (lane == 0) reset_ticket(ws.count + pair);
+  }
+
+  if (!q_ok) return;
+  const float inv = lfin > 0.f ? 1.f / lfin : 0.f;
+  f16* orow = out + (int64_t(my_q) * hq + head) * D;
+#pragma unroll
+  for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+    for (int a4 = 0; a4 < 4; ++a4) {
+      const int d0 = 32 * dt + 8 * a4 + 4 * half;
+      *reinterpret_cast<f16x4*>(orow + d0) =
+          f16x4{f16(acc[dt][4 * a4] * inv), f16(acc[dt][4 * a4 + 1] * inv),
+                f16(acc[dt][4 * a4 + 2] * inv), f16(acc[dt][4 * a4 + 3] * inv)};
+    }
 }
 
 typedef void (*PrefillKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t,
-                              int32_t, int32_t, float);
+                              int32_t, int32_t, int32_t, float, PrefillWorkspace);
 
 static PrefillKernel pick_prefill(int d, int g, int* threads) {
 #define IFN_PREFILL_CASE(DD, GG)                          \
@@ -388,15 +469,17 @@ static PrefillKernel pick_prefill(int d, int g, int* threads) {
 
 }  // namespace ifn
 
-// The kernel keeps every partial result on chip, so it needs no workspace; the size
-// reported is a token 256 bytes so that callers sizing a buffer from it stay valid.
+// Workspace for the key split (tickets + partials); 256 bytes when the shapes need no split.
+// It depends on the current device's CU count, like the launch itself.
 extern "C" size_t ifn_paged_prefill_workspace_bytes(int32_t num_q_tokens, int32_t query_start,
                                                     int32_t num_q_heads, int32_t num_kv_heads,
                                                     int32_t head_dim, int32_t block_size) {
   if (num_q_tokens < 1 || query_start < 0 || num_q_heads < 1 || num_kv_heads < 1 ||
       head_dim < 1 || block_size < 1 || num_q_heads % num_kv_heads != 0)
     return 0;
-  return 256;
+  int cus = ifn::device_cu_count();
+  if (cus < 1) cus = 256;
+  return ifn::plan_prefill(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim, cus).bytes;
 }
 
 extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_pool_layer,
@@ -406,8 +489,6 @@ extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_po
                                  float scale, void* workspace, size_t workspace_bytes,
                                  void* stream) {
   using namespace ifn;
-  (void)workspace;
-  (void)workspace_bytes;
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_table == nullptr)
     return IFN_ERR_INVALID_ARGUMENT;
   if (num_pages < 1 || max_pages < 1 || query_start < 0 || num_q_tokens < 0 || num_q_heads < 1 ||
@@ -423,12 +504,24 @@ extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_po
   if (num_q_tokens == 0) return IFN_OK;
   if (int64_t(query_start) + num_q_tokens > int64_t(max_pages) * kPBlock)
     return IFN_ERR_INVALID_ARGUMENT;  // keys past the end of the block table
-  const int64_t n_qb = ceil_div(num_q_tokens, 32);
-  if (n_qb * num_kv_heads > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
+  const int cus = device_cu_count();
+  if (cus < 1) return IFN_ERR_HIP;
+  const PrefillPlan p = plan_prefill(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim, cus);
+  if (p.n_qb * num_kv_heads * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
+  PrefillWorkspace ws{nullptr, nullptr, nullptr};
+  if (p.nsplit > 1) {
+    if (workspace == nullptr || workspace_bytes < p.bytes) return IFN_ERR_WORKSPACE;
+    IFN_CHECK_ALIGN16(workspace);
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    ws.count = reinterpret_cast<uint32_t*>(wsb);
+    ws.ml = reinterpret_cast<float*>(wsb + p.off_ml);
+    ws.o = reinterpret_cast<float*>(wsb + p.off_o);
+  }
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
-  k<<<dim3(unsigned(n_qb * num_kv_heads)), unsigned(threads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+  k<<<dim3(unsigned(p.n_qb * num_kv_heads * p.nsplit)), unsigned(threads), 0,
+      reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_table, query_start, num_q_tokens,
-      num_kv_heads, int(n_qb), scale * kLog2e);
+      num_kv_heads, int(p.n_qb), p.nsplit, scale * kLog2e, ws);
   return ifn_launch_status();
 }

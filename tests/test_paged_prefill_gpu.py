@@ -27,7 +27,8 @@ def _seq(rng, total, hq, hkv, d, extra=6):
 
 @pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 128), (64, 8, 128), (16, 8, 64),
                                       (4, 1, 64)])
-@pytest.mark.parametrize("start,T", [(0, 1), (0, 37), (0, 128), (45, 38), (100, 300), (512, 512), (17, 1)])
+@pytest.mark.parametrize("start,T", [(0, 1), (0, 37), (0, 128), (45, 38), (100, 300), (512, 512), (17, 1),
+                                     (3000, 40), (1500, 100)])
 def test_prefill_matches_oracle(dev, hq, hkv, d, start, T):
     say(f"prefill hq={hq} hkv={hkv} d={d} start={start} T={T}")
     rng = np.random.default_rng(start * 1000 + T + hq + d)
