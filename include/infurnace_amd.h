@@ -144,6 +144,53 @@ int ifn_paged_prefill(void* out, const void* query, const void* kv_pool_layer, i
                       int32_t head_dim, int32_t block_size, float scale, void* workspace,
                       size_t workspace_bytes, void* stream);
 
+/*
+ * Pre-append step, fused: for every token t and head, q and k get a per-head
+ * RMSNorm over head_dim (x * rsqrt(mean(x^2) + eps) * weight) and the
+ * half-split rotary embedding at positions[t]; k and v are then cast to fp16
+ * and stored at slot_mapping[t] (tokens with active_mask[t] == 0 or an
+ * out-of-range slot store nothing); q is written to q_out as fp16.
+ * q: fp32 [num_tokens][num_q_heads][head_dim]; k, v: fp32
+ * [num_tokens][num_kv_heads][head_dim]; norm weights fp32 [head_dim];
+ * rope_table fp32 [max_positions][head_dim] = cos(pos * f_i) for i < D/2
+ * followed by sin(pos * f_i), f_i = base^(-2i/D).  A position outside
+ * [0, max_positions) stores nothing and writes a zero q row.  head_dim <= 256.
+ * Replaces: the norm/rope/cast/store sequence of
+ * src/infurnace/executor/tinygrad/model.py:183-196 (decode) and :109-137
+ * (prefill), with _rms_norm :11-13, _precompute_rope :19-23 and _apply_rope
+ * :24-27.
+ */
+int ifn_qk_norm_rope_append(void* q_out, const float* q, const float* k, const float* v,
+                            const float* q_norm_weight, const float* k_norm_weight,
+                            const float* rope_table, int32_t max_positions,
+                            const int32_t* positions, const int32_t* slot_mapping,
+                            const uint8_t* active_mask, void* kv_pool_layer, int64_t num_pages,
+                            int32_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t block_size, float eps, void* stream);
+
+/*
+ * Zero the K and V of each listed page in every layer of the full pool
+ * [num_layers][2][num_pages][block_size][num_kv_heads][head_dim].  Ids outside
+ * [0, num_pages) are skipped.
+ * Replaces: ContiguousKVCache.clear_slot,
+ * src/infurnace/executor/tinygrad/buffers.py:67-81 (a released sequence's
+ * pages return to the freshly allocated state, docs/phase2d.md:10-20).
+ */
+int ifn_zero_pages(void* kv_pool, int32_t num_layers, int64_t num_pages, const int32_t* page_ids,
+                   int32_t num_ids, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                   void* stream);
+
+/*
+ * Copy page src_ids[i] to dst_ids[i] (K and V, every layer).  Destination ids
+ * must be distinct and must not appear among the sources.  Pairs with an id
+ * outside [0, num_pages) are skipped.
+ * Serves: the private copy of a partial tail block when a sequence starts from
+ * a shared prefix (partial blocks stay private, docs/architecture.md:381-391).
+ */
+int ifn_copy_pages(void* kv_pool, int32_t num_layers, int64_t num_pages, const int32_t* src_ids,
+                   const int32_t* dst_ids, int32_t num_ids, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t block_size, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,183 @@
+// Pre-append step and page utilities of the KV-cache path (gfx950).
+//
+// ifn_qk_norm_rope_append fuses what the reference does between the Q/K/V
+// projections and the cache write, per token t and head:
+//   q, k: per-head RMSNorm over head_dim (src/infurnace/executor/tinygrad/model.py:11-13,
+//         applied at :183-184 / :109-110), then half-split rotary embedding with the
+//         [position][cos | sin] table (:19-27, applied at :186-187);
+//   k, v: cast to fp16 and stored at slot_mapping[t] (:190-196 decode, :134-137 prefill);
+//   q:    written as fp16 for paged attention.
+// One wavefront per (token, head) row: lane l owns the rotary pairs (i, i + D/2) for
+// i = l, l + 64, ..., so the RMS reduction is one wave sum and the rotation never leaves
+// the lane.  Every load and store is a contiguous 256-byte (fp32) or 128-byte (fp16) run.
+//
+// ifn_zero_pages / ifn_copy_pages are the paged forms of clear_slot
+// (src/infurnace/executor/tinygrad/buffers.py:67-81): zero, or copy, whole pages in every layer.
+#include "ifn_common.hpp"
+
+namespace ifn {
+
+constexpr int kPrepWaves = 4;
+constexpr int kPrepThreads = kPrepWaves * kWave;
+
+__global__ __launch_bounds__(kPrepThreads) void qk_norm_rope_append_kernel(
+    f16* __restrict__ q_out, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w,
+    const float* __restrict__ rope, int32_t max_pos, const int32_t* __restrict__ positions,
+    const int32_t* __restrict__ slot_mapping, const uint8_t* __restrict__ active, f16* __restrict__ pool,
+    int64_t num_slots, int32_t T, int32_t hq, int32_t hkv, int32_t D, float eps) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t row = int64_t(blockIdx.x) * kPrepWaves + threadIdx.x / kWave;
+  const int rows_per_token = hq + 2 * hkv;
+  if (row >= int64_t(T) * rows_per_token) return;
+  const int t = int(row / rows_per_token);
+  const int r = int(row % rows_per_token);
+  const int kind = r < hq ? 0 : (r < hq + hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v
+  const int h = kind == 0 ? r : (kind == 1 ? r - hq : r - hq - hkv);
+  const int half = D / 2;
+  const float* src = kind == 0 ? q + (int64_t(t) * hq + h) * D
+                               : (kind == 1 ? k : v) + (int64_t(t) * hkv + h) * D;
+  const int pos = positions[t];
+  const bool pos_ok = pos >= 0 && pos < max_pos;
+  const int64_t slot = slot_mapping != nullptr ? slot_mapping[t] : -1;
+  const bool store = kind != 0 && pos_ok && (active == nullptr || active[t] != 0) && slot >= 0 &&
+                     slot < num_slots;
+  constexpr int kMaxPairs = 2;  // head_dim <= 256
+  float x1[kMaxPairs], x2[kMaxPairs];
+#pragma unroll
+  for (int j = 0; j < kMaxPairs; ++j) {
+    const int i = lane + kWave * j;
+    x1[j] = i < half ? src[i] : 0.f;
+    x2[j] = i < half ? src[half + i] : 0.f;
+  }
+  if (kind != 2) {
+    float ss = 0.f;
+#pragma unroll
+    for (int j = 0; j < kMaxPairs; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
+    ss = wave_sum(ss);
+    const float rs = 1.0f / sqrtf(ss / float(D) + eps);
+    const float* w = kind == 0 ? q_norm_w : k_norm_w;
+    const float* cs = rope + int64_t(pos_ok ? pos : 0) * D;
+#pragma unroll
+    for (int j = 0; j < kMaxPairs; ++j) {
+      const int i = lane + kWave * j;
+      if (i < half) {
+        const float a = x1[j] * rs * w[i];
+        const float b = x2[j] * rs * w[half + i];
+        const float c = cs[i], s = cs[half + i];
+        x1[j] = a * c - b * s;
+        x2[j] = b * c + a * s;
+      }
+    }
+  }
+  if (kind == 0) {
+    f16* dst = q_out + (int64_t(t) * hq + h) * D;
+#pragma unroll
+    for (int j = 0; j < kMaxPairs; ++j) {
+      const int i = lane + kWave * j;
+      if (i < half) {
+        dst[i] = pos_ok ? f16(x1[j]) : f16(0.f);
+        dst[half + i] = pos_ok ? f16(x2[j]) : f16(0.f);
+      }
+    }
+  } else if (store) {
+    // pool layer: [2][slot][hkv][D]; V is num_slots rows after K
+    f16* dst = pool + (int64_t(kind - 1) * num_slots + slot) * hkv * D + int64_t(h) * D;
+#pragma unroll
+    for (int j = 0; j < kMaxPairs; ++j) {
+      const int i = lane + kWave * j;
+      if (i < half) {
+        dst[i] = f16(x1[j]);
+        dst[half + i] = f16(x2[j]);
+      }
+    }
+  }
+}
+
+// One thread block per (layer, K|V, listed page): 16-byte stores (and loads) over the page.
+template <bool kCopy>
+__global__ __launch_bounds__(256) void page_op_kernel(uint8_t* __restrict__ pool, int64_t num_pages,
+                                                      int64_t page_bytes, const int32_t* __restrict__ dst_ids,
+                                                      const int32_t* __restrict__ src_ids, int32_t n) {
+  const int64_t item = blockIdx.x;  // ((layer * 2 + kv) * n + i)
+  const int i = int(item % n);
+  const int64_t half_index = item / n;  // layer * 2 + kv
+  const int dst = dst_ids[i];
+  if (dst < 0 || int64_t(dst) >= num_pages) return;
+  uint8_t* base = pool + half_index * num_pages * page_bytes;
+  u32x4* d = reinterpret_cast<u32x4*>(base + int64_t(dst) * page_bytes);
+  const int64_t chunks = page_bytes / 16;
+  if constexpr (kCopy) {
+    const int src = src_ids[i];
+    if (src < 0 || int64_t(src) >= num_pages) return;
+    const u32x4* s = reinterpret_cast<const u32x4*>(base + int64_t(src) * page_bytes);
+    for (int64_t c = threadIdx.x; c < chunks; c += blockDim.x) d[c] = s[c];
+  } else {
+    for (int64_t c = threadIdx.x; c < chunks; c += blockDim.x) d[c] = u32x4{0u, 0u, 0u, 0u};
+  }
+}
+
+static int page_op(bool copy, void* kv_pool, int32_t num_layers, int64_t num_pages, const int32_t* dst_ids,
+                   const int32_t* src_ids, int32_t n, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t block_size, void* stream) {
+  if (kv_pool == nullptr || dst_ids == nullptr || (copy && src_ids == nullptr)) return IFN_ERR_INVALID_ARGUMENT;
+  if (num_layers < 1 || num_pages < 1 || n < 0 || num_kv_heads < 1 || head_dim < 1 || block_size < 1)
+    return IFN_ERR_INVALID_ARGUMENT;
+  const int64_t page_bytes = int64_t(block_size) * num_kv_heads * head_dim * 2;
+  if (page_bytes % 16 != 0) return IFN_ERR_UNSUPPORTED;
+  IFN_CHECK_ALIGN16(kv_pool);
+  if (n == 0) return IFN_OK;
+  const int64_t blocks = int64_t(num_layers) * 2 * n;
+  if (blocks > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  uint8_t* pool = static_cast<uint8_t*>(kv_pool);
+  if (copy)
+    page_op_kernel<true><<<dim3(unsigned(blocks)), dim3(256), 0, s>>>(pool, num_pages, page_bytes, dst_ids, src_ids, n);
+  else
+    page_op_kernel<false><<<dim3(unsigned(blocks)), dim3(256), 0, s>>>(pool, num_pages, page_bytes, dst_ids, nullptr, n);
+  return ifn_launch_status();
+}
+
+}  // namespace ifn
+
+extern "C" int ifn_qk_norm_rope_append(void* q_out, const float* q, const float* k, const float* v,
+                                       const float* q_norm_weight, const float* k_norm_weight,
+                                       const float* rope_table, int32_t max_positions,
+                                       const int32_t* positions, const int32_t* slot_mapping,
+                                       const uint8_t* active_mask, void* kv_pool_layer, int64_t num_pages,
+                                       int32_t num_tokens, int32_t num_q_heads, int32_t num_kv_heads,
+                                       int32_t head_dim, int32_t block_size, float eps, void* stream) {
+  using namespace ifn;
+  if (q_out == nullptr || q == nullptr || k == nullptr || v == nullptr || q_norm_weight == nullptr ||
+      k_norm_weight == nullptr || rope_table == nullptr || positions == nullptr || slot_mapping == nullptr ||
+      kv_pool_layer == nullptr)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (num_tokens < 0 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 2 || head_dim % 2 != 0 ||
+      block_size < 1 || num_pages < 1 || max_positions < 1 || num_q_heads % num_kv_heads != 0 || !(eps >= 0.f))
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (head_dim > 256) return IFN_ERR_UNSUPPORTED;
+  if (num_tokens == 0) return IFN_OK;
+  const int64_t rows = int64_t(num_tokens) * (num_q_heads + 2 * num_kv_heads);
+  const int64_t blocks = (rows + kPrepWaves - 1) / kPrepWaves;
+  if (blocks > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
+  qk_norm_rope_append_kernel<<<dim3(unsigned(blocks)), dim3(kPrepThreads), 0,
+                               reinterpret_cast<hipStream_t>(stream)>>>(
+      static_cast<f16*>(q_out), q, k, v, q_norm_weight, k_norm_weight, rope_table, max_positions, positions,
+      slot_mapping, active_mask, static_cast<f16*>(kv_pool_layer), num_pages * block_size, num_tokens,
+      num_q_heads, num_kv_heads, head_dim, eps);
+  return ifn_launch_status();
+}
+
+extern "C" int ifn_zero_pages(void* kv_pool, int32_t num_layers, int64_t num_pages, const int32_t* page_ids,
+                              int32_t num_ids, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                              void* stream) {
+  return ifn::page_op(false, kv_pool, num_layers, num_pages, page_ids, nullptr, num_ids, num_kv_heads, head_dim,
+                      block_size, stream);
+}
+
+extern "C" int ifn_copy_pages(void* kv_pool, int32_t num_layers, int64_t num_pages, const int32_t* src_ids,
+                              const int32_t* dst_ids, int32_t num_ids, int32_t num_kv_heads, int32_t head_dim,
+                              int32_t block_size, void* stream) {
+  return ifn::page_op(true, kv_pool, num_layers, num_pages, dst_ids, src_ids, num_ids, num_kv_heads, head_dim,
+                      block_size, stream);
+}

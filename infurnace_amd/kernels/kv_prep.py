@@ -1,0 +1,136 @@
+"""Pre-append step and page utilities of the KV-cache path (HIP, gfx950).
+
+``qk_norm_rope_append`` fuses the steps between the Q/K/V projections and the
+cache write in the reference's forward pass
+(src/infurnace/executor/tinygrad/model.py:183-196 for decode, :109-137 for
+prefill): per-head RMSNorm of q and k (``_rms_norm``, :11-13), the half-split
+rotary embedding (``_apply_rope`` :24-27 over the table of ``_precompute_rope``
+:19-23), the fp32 -> fp16 cast, and the slot-mapped store of k and v.  One
+launch replaces a norm, a rope and a store pass over K.
+
+``zero_pages`` is the paged form of ``ContiguousKVCache.clear_slot``
+(src/infurnace/executor/tinygrad/buffers.py:67-81): a released sequence's pages
+return to the freshly allocated (zero) state.  ``copy_pages`` gives a sequence a
+private copy of a block (partial tail blocks are never shared,
+docs/architecture.md:381-391).
+"""
+from __future__ import annotations
+
+import math
+
+import numpy as np
+import torch
+
+from .. import _capi
+from ._common import KVStoreError, check_pool, current_stream, ptr
+
+__all__ = ["qk_norm_rope_append", "rope_table", "zero_pages", "copy_pages"]
+
+
+def rope_table(max_positions: int, head_dim: int, base: float, device=None) -> torch.Tensor:
+    """fp32 [max_positions, head_dim] rows ``[cos(p f_i) | sin(p f_i)]``, f_i = base^(-2i/D), i < D/2.
+
+    The layout of ``_precompute_rope`` (model.py:19-23).  The angles are computed in
+    float64 and rounded once to float32.
+    """
+    if max_positions < 1 or head_dim < 2 or head_dim % 2 or not base > 0:
+        raise ValueError("rope_table needs max_positions >= 1, an even head_dim and base > 0")
+    inv = 1.0 / (base ** (np.arange(0, head_dim, 2, dtype=np.float64) / head_dim))
+    ang = np.arange(max_positions, dtype=np.float64)[:, None] * inv[None, :]
+    table = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+    return torch.from_numpy(table).to(device) if device is not None else torch.from_numpy(table)
+
+
+def _f32(name: str, t, shape: tuple, device) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise KVStoreError(f"{name} must be a torch.Tensor")
+    if t.dtype != torch.float32:
+        raise KVStoreError(f"{name} dtype must be float32, got {t.dtype}")
+    if tuple(t.shape) != shape:
+        raise KVStoreError(f"{name} shape must be {shape}, got {tuple(t.shape)}")
+    if t.device != device or not t.is_contiguous():
+        raise KVStoreError(f"{name} must be a contiguous tensor on {device}")
+    return t
+
+
+def _i32(name: str, t, n: int, device, dtypes=(torch.int32,)) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor) or t.dtype not in dtypes or tuple(t.shape) != (n,):
+        raise KVStoreError(f"{name} must be a {dtypes} tensor of shape ({n},)")
+    if t.device != device or not t.is_contiguous():
+        raise KVStoreError(f"{name} must be a contiguous tensor on {device}")
+    return t
+
+
+def qk_norm_rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_weight: torch.Tensor,
+                        k_norm_weight: torch.Tensor, rope: torch.Tensor, positions: torch.Tensor,
+                        slot_mapping: torch.Tensor, active_mask: torch.Tensor | None, kv_pool: torch.Tensor, *,
+                        layer: int = 0, eps: float = 1e-6, q_out: torch.Tensor | None = None) -> torch.Tensor:
+    """Normalise and rotate q, k; store k and v (fp16) at their slots; return q as fp16.
+
+    q fp32 [T, Hq, D]; k, v fp32 [T, Hkv, D]; norm weights fp32 [D]; ``rope`` from
+    ``rope_table``; positions and slot_mapping int32 [T]; active_mask bool/uint8 [T] or
+    None.  A token whose position is outside the table stores nothing and gets a zero
+    q row.
+    """
+    pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, KVStoreError)
+    dev = pool_layer.device
+    if not isinstance(q, torch.Tensor) or q.ndim != 3:
+        raise KVStoreError("q must be a rank-3 [T, Hq, D] tensor")
+    T, hq = q.shape[0], q.shape[1]
+    if hq % hkv:
+        raise KVStoreError(f"num_q_heads {hq} is not a multiple of num_kv_heads {hkv}")
+    _f32("q", q, (T, hq, d), dev)
+    _f32("k", k, (T, hkv, d), dev)
+    _f32("v", v, (T, hkv, d), dev)
+    _f32("q_norm_weight", q_norm_weight, (d,), dev)
+    _f32("k_norm_weight", k_norm_weight, (d,), dev)
+    if not isinstance(rope, torch.Tensor) or rope.ndim != 2:
+        raise KVStoreError("rope must be the rank-2 table of rope_table()")
+    _f32("rope", rope, (rope.shape[0], d), dev)
+    _i32("positions", positions, T, dev)
+    _i32("slot_mapping", slot_mapping, T, dev)
+    if active_mask is not None:
+        _i32("active_mask", active_mask, T, dev, (torch.bool, torch.uint8))
+    if not (eps >= 0 and math.isfinite(eps)):
+        raise KVStoreError("eps must be a finite non-negative number")
+    if q_out is None:
+        q_out = torch.empty((T, hq, d), dtype=torch.float16, device=dev)
+    elif q_out.dtype != torch.float16 or tuple(q_out.shape) != (T, hq, d) or q_out.device != dev or \
+            not q_out.is_contiguous():
+        raise KVStoreError(f"q_out must be a contiguous float16 [{T}, {hq}, {d}] tensor on {dev}")
+    if T == 0:
+        return q_out
+    _capi.call("ifn_qk_norm_rope_append", ptr(q_out), ptr(q), ptr(k), ptr(v), ptr(q_norm_weight),
+               ptr(k_norm_weight), ptr(rope), rope.shape[0], ptr(positions), ptr(slot_mapping), ptr(active_mask),
+               ptr(pool_layer), P, T, hq, hkv, d, bs, float(eps), current_stream(dev))
+    return q_out
+
+
+def _full_pool(kv_pool) -> tuple:
+    if not isinstance(kv_pool, torch.Tensor) or kv_pool.ndim != 6:
+        raise KVStoreError("kv_pool must be the rank-6 [layers, 2, pages, block_size, Hkv, D] pool")
+    check_pool(kv_pool, 0, KVStoreError)
+    return kv_pool.shape
+
+
+def zero_pages(kv_pool: torch.Tensor, page_ids: torch.Tensor) -> None:
+    """Zero K and V of every listed page in every layer (ids outside the pool are skipped)."""
+    L, _, P, bs, hkv, d = _full_pool(kv_pool)
+    ids = _i32("page_ids", page_ids, page_ids.numel() if isinstance(page_ids, torch.Tensor) else -1,
+               kv_pool.device)
+    _capi.call("ifn_zero_pages", ptr(kv_pool), L, P, ptr(ids), ids.numel(), hkv, d, bs,
+               current_stream(kv_pool.device))
+
+
+def copy_pages(kv_pool: torch.Tensor, src_ids: torch.Tensor, dst_ids: torch.Tensor) -> None:
+    """Copy page src_ids[i] to dst_ids[i] in every layer.  Destinations must be distinct and
+    disjoint from the sources (checked here on the host)."""
+    L, _, P, bs, hkv, d = _full_pool(kv_pool)
+    n = src_ids.numel() if isinstance(src_ids, torch.Tensor) else -1
+    src = _i32("src_ids", src_ids, n, kv_pool.device)
+    dst = _i32("dst_ids", dst_ids, n, kv_pool.device)
+    s, t = src.cpu().tolist(), dst.cpu().tolist()
+    if len(set(t)) != len(t) or set(t) & set(s):
+        raise KVStoreError("copy_pages destinations must be distinct and not among the sources")
+    _capi.call("ifn_copy_pages", ptr(kv_pool), L, P, ptr(src), ptr(dst), n, hkv, d, bs,
+               current_stream(kv_pool.device))

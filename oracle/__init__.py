@@ -42,6 +42,9 @@ def lib() -> ctypes.CDLL:
         L.orc_store_kv.argtypes = [p, i64, p, p, p, p, i32, i32, i32, i32]
         L.orc_paged_attention.argtypes = [p, p, p, i64, p, i32, p, p, i32, i32, i32, i32, i32, i32, f32]
         L.orc_paged_attention.restype = ctypes.c_int
+        L.orc_qk_norm_rope_append.argtypes = [p, p, i64, p, p, p, p, p, p, i32, p, p, p, i32, i32, i32, i32, i32,
+                                              f32]
+        L.orc_qk_norm_rope_append.restype = ctypes.c_int
         _lib = L
     return _lib
 
@@ -122,3 +125,26 @@ def paged_attention(q, pool_layer, block_tables, seq_lens, active_mask=None, sca
     if rc != 0:
         raise ValueError(f"oracle rejected inputs (code {rc})")
     return o[:, 0] if decode else o
+
+
+def qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope_table, positions, slot_mapping,
+                        active_mask, pool_layer: np.ndarray, eps: float = 1e-6) -> np.ndarray:
+    """Pre-append step: returns q (fp16 [T, Hq, D]) after RMSNorm + rotary; stores k (normed,
+    rotated) and v (cast) into ``pool_layer`` [2, P, bs, Hkv, D] fp16 in place."""
+    if pool_layer.dtype != np.float16 or not pool_layer.flags.c_contiguous or pool_layer.ndim != 5:
+        raise TypeError("pool_layer must be a C-contiguous [2,P,bs,Hkv,D] float16 array")
+    _, P, bs, hkv, d = pool_layer.shape
+    qf, kf, vf = _c(q, np.float32), _c(k, np.float32), _c(v, np.float32)
+    T, hq, _ = qf.shape
+    qw, kw = _c(q_norm_weight, np.float32), _c(k_norm_weight, np.float32)
+    rope = _c(rope_table, np.float32)
+    pos = _c(positions, np.int32)
+    sm = _c(slot_mapping, np.int32)
+    am = None if active_mask is None else _c(np.asarray(active_mask).astype(np.uint8), np.uint8)
+    out = np.zeros((T, hq, d), np.float16)
+    rc = lib().orc_qk_norm_rope_append(_ptr(out), _ptr(pool_layer), P, _ptr(qf), _ptr(kf), _ptr(vf), _ptr(qw),
+                                       _ptr(kw), _ptr(rope), rope.shape[0], _ptr(pos), _ptr(sm), _ptr(am), T, hq,
+                                       hkv, d, bs, float(eps))
+    if rc != 0:
+        raise ValueError(f"orc_qk_norm_rope_append failed: {rc}")
+    return out

@@ -220,3 +220,64 @@ int orc_paged_attention(uint16_t* out, const uint16_t* q, const uint16_t* pool_l
   free(qf);
   return rc;
 }
+
+/* ---------------- pre-append step: q/k RMSNorm + rotary, k/v cast + store ----------------
+ *
+ * Follows src/infurnace/executor/tinygrad/model.py: _rms_norm (:11-13)
+ * x * rsqrt(mean(x^2) + eps) then * weight; _apply_rope (:24-27) on the table of
+ * _precompute_rope (:19-23), whose row is [cos(pos f_i) | sin(pos f_i)], i < D/2;
+ * decode order :183-196 (q/k norm, rope, cast k/v to the cache dtype, store at
+ * the slot).  v is only cast.  fp32 arithmetic, sums in ascending dim order,
+ * one fp16 round at the end.  A token whose position lies outside
+ * [0, max_pos) stores nothing and gets a zero q row; inactive tokens and
+ * out-of-range slots store nothing.
+ *
+ * Pinned by (tests/test_oracle.py): a float64 numpy restatement of the two
+ * formulas (within one fp16 rounding), the rotation invariants (each pair's
+ * norm is preserved; position 0 is the identity; two rotations compose), and
+ * v rows equal to the plain fp16 cast bit for bit.
+ */
+static void orc_norm_rope_row(const float* x, const float* w, const float* cs, int32_t D, float eps, float* y) {
+  float ss = 0.f;
+  for (int32_t i = 0; i < D; ++i) ss += x[i] * x[i];
+  const float rs = 1.0f / sqrtf(ss / (float)D + eps);
+  const int32_t half = D / 2;
+  for (int32_t i = 0; i < half; ++i) {
+    const float a = x[i] * rs * w[i];
+    const float b = x[half + i] * rs * w[half + i];
+    y[i] = a * cs[i] - b * cs[half + i];
+    y[half + i] = b * cs[i] + a * cs[half + i];
+  }
+}
+
+int orc_qk_norm_rope_append(uint16_t* q_out, uint16_t* pool_layer, int64_t num_pages, const float* q,
+                            const float* k, const float* v, const float* q_norm_w, const float* k_norm_w,
+                            const float* rope, int32_t max_pos, const int32_t* positions,
+                            const int32_t* slot_mapping, const uint8_t* active, int32_t T, int32_t Hq,
+                            int32_t Hkv, int32_t D, int32_t block_size, float eps) {
+  if (D < 2 || D % 2 != 0 || Hq % Hkv != 0) return -1;
+  float* y = (float*)malloc(sizeof(float) * (size_t)D);
+  if (y == NULL) return -3;
+  const int64_t num_slots = num_pages * block_size;
+  for (int32_t t = 0; t < T; ++t) {
+    const int32_t pos = positions[t];
+    const int pos_ok = pos >= 0 && pos < max_pos;
+    const float* cs = rope + (int64_t)(pos_ok ? pos : 0) * D;
+    for (int32_t h = 0; h < Hq; ++h) {
+      uint16_t* dst = q_out + ((int64_t)t * Hq + h) * D;
+      orc_norm_rope_row(q + ((int64_t)t * Hq + h) * D, q_norm_w, cs, D, eps, y);
+      for (int32_t i = 0; i < D; ++i) dst[i] = pos_ok ? orc_float_to_half(y[i]) : 0;
+    }
+    const int64_t slot = slot_mapping[t];
+    if (!pos_ok || (active != NULL && active[t] == 0) || slot < 0 || slot >= num_slots) continue;
+    for (int32_t h = 0; h < Hkv; ++h) {
+      uint16_t* kd = pool_layer + (slot * Hkv + h) * D;
+      uint16_t* vd = pool_layer + ((num_slots + slot) * Hkv + h) * D;
+      orc_norm_rope_row(k + ((int64_t)t * Hkv + h) * D, k_norm_w, cs, D, eps, y);
+      for (int32_t i = 0; i < D; ++i) kd[i] = orc_float_to_half(y[i]);
+      for (int32_t i = 0; i < D; ++i) vd[i] = orc_float_to_half(v[((int64_t)t * Hkv + h) * D + i]);
+    }
+  }
+  free(y);
+  return 0;
+}

@@ -103,3 +103,30 @@ def test_python_wrappers_reject_host_tensors():
                         torch.ones(1, dtype=torch.int32), None)
     with pytest.raises(KVStoreError):
         store_kv(pool.float(), torch.zeros(1, dtype=torch.int32), None, k, k)
+
+
+def test_prep_and_page_ops_host_validation():
+    L = _capi.lib()
+    base = dict(qo=A, q=A, k=A, v=A, qw=A, kw=A, rope=A, mp=4096, pos=A, sm=A, am=None, pool=A, P=64, T=4,
+                hq=16, hkv=8, d=128, bs=16, eps=1e-6)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return L.ifn_qk_norm_rope_append(a["qo"], a["q"], a["k"], a["v"], a["qw"], a["kw"], a["rope"], a["mp"],
+                                         a["pos"], a["sm"], a["am"], a["pool"], a["P"], a["T"], a["hq"], a["hkv"],
+                                         a["d"], a["bs"], a["eps"], None)
+
+    assert call(q=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(rope=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(hq=12) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(d=127) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(eps=-1.0) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(eps=float("nan")) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(d=512) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(T=0) == _capi.IFN_OK
+    assert L.ifn_zero_pages(None, 2, 64, A, 3, 8, 128, 16, None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert L.ifn_zero_pages(A, 0, 64, A, 3, 8, 128, 16, None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert L.ifn_zero_pages(A + 8, 2, 64, A, 3, 8, 128, 16, None) == _capi.IFN_ERR_ALIGNMENT
+    assert L.ifn_zero_pages(A, 2, 64, A, 0, 8, 128, 16, None) == _capi.IFN_OK
+    assert L.ifn_copy_pages(A, 2, 64, None, A, 3, 8, 128, 16, None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert L.ifn_copy_pages(A, 2, 64, A, A, 0, 8, 128, 16, None) == _capi.IFN_OK

@@ -250,3 +250,97 @@ def test_inactive_rows_untouched_and_bad_tables_rejected():
     bad[0, 0] = pool.shape[1]
     with pytest.raises(ValueError):
         oracle.paged_attention(q, pool, bad, sl)
+
+
+# ---------------- pre-append step: q/k RMSNorm + rotary, k/v cast + store ----------------
+
+def _rope64(max_pos, d, base):
+    inv = 1.0 / (base ** (np.arange(0, d, 2, dtype=np.float64) / d))
+    ang = np.arange(max_pos, dtype=np.float64)[:, None] * inv[None, :]
+    return np.concatenate([np.cos(ang), np.sin(ang)], axis=1)
+
+
+def _prep64(x, w, rope_row, eps):
+    """float64 restatement: x * rsqrt(mean(x^2) + eps) * w, then (x1 c - x2 s, x2 c + x1 s)."""
+    x = x.astype(np.float64)
+    y = x / np.sqrt(np.mean(x * x, axis=-1, keepdims=True) + eps) * w.astype(np.float64)
+    h = x.shape[-1] // 2
+    c, s = rope_row[:h], rope_row[h:]
+    return np.concatenate([y[..., :h] * c - y[..., h:] * s, y[..., h:] * c + y[..., :h] * s], axis=-1)
+
+
+def _prep_case(rng, T=5, hq=4, hkv=2, d=64, P=6, bs=16, max_pos=300):
+    q = rng.standard_normal((T, hq, d)).astype(np.float32) * 3
+    k = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    v = rng.standard_normal((T, hkv, d)).astype(np.float32)
+    qw = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    kw = (1 + 0.1 * rng.standard_normal(d)).astype(np.float32)
+    rope = _rope64(max_pos, d, 1e6).astype(np.float32)
+    pos = rng.integers(0, max_pos, T).astype(np.int32)
+    slots = rng.permutation(P * bs)[:T].astype(np.int32)
+    pool = rng.standard_normal((2, P, bs, hkv, d)).astype(np.float16)
+    return q, k, v, qw, kw, rope, pos, slots, pool
+
+
+def _ulps(a16, b64):
+    """|a - b| in units of the fp16 spacing at b (a correctly rounded fp16 of b is within 0.5)."""
+    b = np.asarray(b64, np.float64)
+    ulp = np.spacing(np.abs(b).astype(np.float16)).astype(np.float64)
+    return np.abs(a16.astype(np.float64) - b) / np.maximum(ulp, 2.0 ** -24)
+
+
+def test_prep_matches_float64_restatement():
+    rng = np.random.default_rng(40)
+    q, k, v, qw, kw, rope, pos, slots, pool = _prep_case(rng)
+    before = pool.copy()
+    qo = oracle.qk_norm_rope_append(q, k, v, qw, kw, rope, pos, slots, None, pool, eps=1e-6)
+    rope64 = rope.astype(np.float64)
+    for t in range(q.shape[0]):
+        ref_q = _prep64(q[t], qw, rope64[pos[t]], 1e-6)
+        assert _ulps(qo[t], ref_q).max() <= 1.0
+        s = slots[t]
+        kk = pool[0, s // 16, s % 16]
+        assert _ulps(kk, _prep64(k[t], kw, rope64[pos[t]], 1e-6)).max() <= 1.0
+        assert np.array_equal(pool[1, s // 16, s % 16].view(np.uint16), v[t].astype(np.float16).view(np.uint16))
+    untouched = np.ones(pool.shape[1] * 16, bool)
+    untouched[slots] = False
+    flat_b, flat_a = before.reshape(2, -1, *before.shape[3:]), pool.reshape(2, -1, *pool.shape[3:])
+    assert np.array_equal(flat_b[:, untouched].view(np.uint16), flat_a[:, untouched].view(np.uint16))
+
+
+def test_prep_rotation_invariants():
+    rng = np.random.default_rng(41)
+    q, k, v, qw, kw, rope, pos, slots, pool = _prep_case(rng, T=3, d=128)
+    ones = np.ones_like(qw)
+    # position 0 is the identity rotation: output = x / rms(x) (weights 1)
+    pos0 = np.zeros_like(pos)
+    q0 = oracle.qk_norm_rope_append(q, k, v, ones, ones, rope, pos0, slots, None, pool.copy(), eps=0.0)
+    rms = np.sqrt(np.mean(q.astype(np.float64) ** 2, axis=-1, keepdims=True))
+    assert _ulps(q0, q / rms).max() <= 1.0
+    # a rotation keeps every (i, i + D/2) pair's norm
+    qp = oracle.qk_norm_rope_append(q, k, v, ones, ones, rope, pos, slots, None, pool.copy(), eps=0.0)
+    h = q.shape[-1] // 2
+    n0 = q0[..., :h].astype(np.float64) ** 2 + q0[..., h:].astype(np.float64) ** 2
+    n1 = qp[..., :h].astype(np.float64) ** 2 + qp[..., h:].astype(np.float64) ** 2
+    assert np.allclose(n0, n1, rtol=4e-3, atol=1e-4)
+    # rotations compose: rotating by a then by b (table rows) equals rotating by a + b
+    tab = _rope64(64, 128, 10000.0)
+    x = rng.standard_normal(128)
+    def rot(x, r):
+        c, s = r[:h], r[h:]
+        return np.concatenate([x[:h] * c - x[h:] * s, x[h:] * c + x[:h] * s])
+    assert np.allclose(rot(rot(x, tab[5]), tab[9]), rot(x, tab[14]), atol=1e-12)
+
+
+def test_prep_skips_inactive_bad_slots_and_positions():
+    rng = np.random.default_rng(42)
+    q, k, v, qw, kw, rope, pos, slots, pool = _prep_case(rng, T=4)
+    slots[1] = pool.shape[1] * 16 + 3      # out of range
+    pos[2] = rope.shape[0]                 # outside the table
+    active = np.array([1, 1, 1, 0], np.uint8)
+    before = pool.copy()
+    qo = oracle.qk_norm_rope_append(q, k, v, qw, kw, rope, pos, slots, active, pool)
+    assert np.all(qo[2] == 0)
+    changed = np.nonzero((before.reshape(2, -1, *before.shape[3:]).view(np.uint16) !=
+                          pool.reshape(2, -1, *pool.shape[3:]).view(np.uint16)).any(axis=(0, 2, 3)))[0]
+    assert set(changed.tolist()) <= {int(slots[0])}
