@@ -179,6 +179,55 @@ def run_prefill(lib, hip, dev, g, stream) -> dict:
             "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
 
 
+def run_pre_append(lib, hip, dev, g, stream) -> dict:
+    """Fused pre-append (q/k RMSNorm + rotary + fp16 cast + slot append) on config-3 chunks:
+    512 tokens per launch, 28 layers with distinct inputs, HIP events around every launch."""
+    import torch
+    from infurnace_amd import workloads
+    from infurnace_amd.kernels import rope_table
+    w = workloads.config3()
+    L, hq, hkv, d, T = w.num_layers, w.num_q_heads, w.num_kv_heads, w.head_dim, w.chunk
+    pool = torch.zeros((L, 2, w.num_pages, 16, hkv, d), dtype=torch.float16, device=dev)
+    q = torch.randn((L, T, hq, d), generator=g, device=dev)
+    k = torch.randn((L, T, hkv, d), generator=g, device=dev)
+    v = torch.randn((L, T, hkv, d), generator=g, device=dev)
+    qw = torch.ones(d, device=dev)
+    rope = rope_table(w.prompt_len, d, 1e6, device=dev)
+    pos = torch.arange(T, dtype=torch.int32, device=dev) + 3 * T
+    slots = torch.from_numpy((w.block_table.astype(np.int64)[(np.arange(T) + 3 * T) // 16] * 16
+                              + (np.arange(T) + 3 * T) % 16).astype(np.int32)).to(dev)
+    q_out = torch.empty((T, hq, d), dtype=torch.float16, device=dev)
+    lb = pool[0].numel() * 2
+
+    def one(layer):
+        rc = lib.ifn_qk_norm_rope_append(q_out.data_ptr(), q[layer].data_ptr(), k[layer].data_ptr(), v[layer].data_ptr(),
+                                         qw.data_ptr(), qw.data_ptr(), rope.data_ptr(), rope.shape[0], pos.data_ptr(),
+                                         slots.data_ptr(), None, pool.data_ptr() + layer * lb, w.num_pages, T, hq, hkv,
+                                         d, 16, 1e-6, stream)
+        if rc:
+            raise RuntimeError(f"pre-append launch failed: {rc}")
+
+    for layer in range(L):
+        one(layer)
+    torch.cuda.synchronize()
+    reps = 5
+    evs = hip.create(2 * L * reps)
+    for r in range(reps):
+        for layer in range(L):
+            hip.hip.hipEventRecord(evs[2 * (r * L + layer)], stream)
+            one(layer)
+            hip.hip.hipEventRecord(evs[2 * (r * L + layer) + 1], stream)
+    torch.cuda.synchronize()
+    us = float(np.mean([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(L * reps)])) * 1e3
+    hip.destroy(evs)
+    rows = T * (hq + 2 * hkv)
+    nbytes = rows * d * 4 + rows * d * 2 + T * d * 4 + 2 * d * 4 + 2 * T * 4  # fp32 in, fp16 out, rope rows
+    gbps = nbytes / (us / 1e6) / 1e9
+    return {"workload": "config-3 chunk: 512 tokens x (16 q + 8 k + 8 v heads) x 128, 28 layers",
+            "us_per_launch": round(us, 2), "bytes": nbytes, "GB/s": round(gbps, 1),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4)}
+
+
 def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> dict:
     """Decode leg for a second or third workload (configs 4 and 5): `layers` distinct layer pools,
     store_kv (one token per row) then decode per layer; HIP events around every decode launch.
@@ -360,8 +409,10 @@ def main() -> int:
     del pool3, k3, v3
 
     prefill = None
+    pre_append = None
     if not args.no_prefill:
         prefill = run_prefill(lib, hip, dev, g, stream)
+        pre_append = run_pre_append(lib, hip, dev, g, stream)
 
     extra = {}
     if not args.no_extra:
@@ -415,6 +466,7 @@ def main() -> int:
                            "us": round(a_ms * 1e3, 2), "bytes": a_bytes, "GB/s": round(a_gbps, 2),
                            "frac": round(a_gbps / HBM_PEAK_GBPS, 4)},
         "prefill": prefill,
+        "pre_append": pre_append,
         "config4": extra.get("config4"),
         "config5": extra.get("config5"),
         "cpu_baseline": cpu,

@@ -64,10 +64,24 @@ class PagedKVCache:
         """Zero the given pages in every layer (slot reuse without stale state, buffers.py:67-81)."""
         if len(ids) == 0:
             return
-        idx = torch.as_tensor(np.asarray(ids, np.int64), device=self.kv.device)
-        if int(idx.min()) < 0 or int(idx.max()) >= self.num_blocks:
+        arr = np.asarray(ids, np.int64)
+        if int(arr.min()) < 0 or int(arr.max()) >= self.num_blocks:
             raise KVCacheError("page id outside the pool")
-        self.kv.index_fill_(2, idx, 0)
+        from ..kernels import zero_pages  # the HIP page kernel (ifn_zero_pages)
+        zero_pages(self.kv, torch.as_tensor(arr.astype(np.int32), device=self.kv.device))
+
+    def copy_pages(self, src: Sequence[int], dst: Sequence[int]) -> None:
+        """Copy page src[i] to dst[i] in every layer (a private copy of a shared partial block)."""
+        if len(src) != len(dst):
+            raise KVCacheError("copy_pages needs as many destinations as sources")
+        if len(src) == 0:
+            return
+        s, d = np.asarray(src, np.int64), np.asarray(dst, np.int64)
+        if min(s.min(), d.min()) < 0 or max(s.max(), d.max()) >= self.num_blocks:
+            raise KVCacheError("page id outside the pool")
+        from ..kernels import copy_pages
+        copy_pages(self.kv, torch.as_tensor(s.astype(np.int32), device=self.kv.device),
+                   torch.as_tensor(d.astype(np.int32), device=self.kv.device))
 
 
 @dataclass

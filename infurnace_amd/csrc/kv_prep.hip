@@ -7,9 +7,10 @@
 //         [position][cos | sin] table (:19-27, applied at :186-187);
 //   k, v: cast to fp16 and stored at slot_mapping[t] (:190-196 decode, :134-137 prefill);
 //   q:    written as fp16 for paged attention.
-// One wavefront per (token, head) row: lane l owns the rotary pairs (i, i + D/2) for
-// i = l, l + 64, ..., so the RMS reduction is one wave sum and the rotation never leaves
-// the lane.  Every load and store is a contiguous 256-byte (fp32) or 128-byte (fp16) run.
+// One workgroup per token; a wavefront handles a (token, head) row at a time, lane l owning
+// the rotary pairs (i, i + D/2) for i = l, l + 64, ..., so the RMS reduction is one wave sum
+// and the rotation never leaves the lane.  Every load and store is a contiguous 256-byte
+// (fp32) or 128-byte (fp16) run.
 //
 // ifn_zero_pages / ifn_copy_pages are the paged forms of clear_slot
 // (src/infurnace/executor/tinygrad/buffers.py:67-81): zero, or copy, whole pages in every layer.
@@ -17,78 +18,93 @@
 
 namespace ifn {
 
-constexpr int kPrepWaves = 4;
+constexpr int kPrepWaves = 8;
 constexpr int kPrepThreads = kPrepWaves * kWave;
+constexpr int kPrepRows = 4;   // rows a wave loads before it computes (loads in flight together)
 
+// One workgroup per token.  The token's rows (Hq q heads, then Hkv k heads, then Hkv v heads)
+// go to the 8 waves in batches of kPrepRows; a wave loads its batch, then normalises,
+// rotates and stores it.  The rotary row and both norm weights are loaded once per wave.
+template <int kMaxPairs>  // rotary pairs per lane: ceil(head_dim / 128)
 __global__ __launch_bounds__(kPrepThreads) void qk_norm_rope_append_kernel(
     f16* __restrict__ q_out, const float* __restrict__ q, const float* __restrict__ k,
     const float* __restrict__ v, const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w,
     const float* __restrict__ rope, int32_t max_pos, const int32_t* __restrict__ positions,
     const int32_t* __restrict__ slot_mapping, const uint8_t* __restrict__ active, f16* __restrict__ pool,
-    int64_t num_slots, int32_t T, int32_t hq, int32_t hkv, int32_t D, float eps) {
+    int64_t num_slots, int32_t hq, int32_t hkv, int32_t D, float eps) {
   const int lane = threadIdx.x % kWave;
-  const int64_t row = int64_t(blockIdx.x) * kPrepWaves + threadIdx.x / kWave;
-  const int rows_per_token = hq + 2 * hkv;
-  if (row >= int64_t(T) * rows_per_token) return;
-  const int t = int(row / rows_per_token);
-  const int r = int(row % rows_per_token);
-  const int kind = r < hq ? 0 : (r < hq + hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v
-  const int h = kind == 0 ? r : (kind == 1 ? r - hq : r - hq - hkv);
+  const int wave = threadIdx.x / kWave;
+  const int t = blockIdx.x;
+  const int rows = hq + 2 * hkv;
   const int half = D / 2;
-  const float* src = kind == 0 ? q + (int64_t(t) * hq + h) * D
-                               : (kind == 1 ? k : v) + (int64_t(t) * hkv + h) * D;
   const int pos = positions[t];
   const bool pos_ok = pos >= 0 && pos < max_pos;
-  const int64_t slot = slot_mapping != nullptr ? slot_mapping[t] : -1;
-  const bool store = kind != 0 && pos_ok && (active == nullptr || active[t] != 0) && slot >= 0 &&
-                     slot < num_slots;
-  constexpr int kMaxPairs = 2;  // head_dim <= 256
-  float x1[kMaxPairs], x2[kMaxPairs];
+  const int64_t slot = slot_mapping[t];
+  const bool store = pos_ok && (active == nullptr || active[t] != 0) && slot >= 0 && slot < num_slots;
+  const float* cs = rope + int64_t(pos_ok ? pos : 0) * D;
+  float c[kMaxPairs], sn[kMaxPairs], wq1[kMaxPairs], wq2[kMaxPairs], wk1[kMaxPairs], wk2[kMaxPairs];
 #pragma unroll
   for (int j = 0; j < kMaxPairs; ++j) {
-    const int i = lane + kWave * j;
-    x1[j] = i < half ? src[i] : 0.f;
-    x2[j] = i < half ? src[half + i] : 0.f;
+    const int i = min(lane + kWave * j, half - 1);
+    c[j] = cs[i];
+    sn[j] = cs[half + i];
+    wq1[j] = q_norm_w[i];
+    wq2[j] = q_norm_w[half + i];
+    wk1[j] = k_norm_w[i];
+    wk2[j] = k_norm_w[half + i];
   }
-  if (kind != 2) {
-    float ss = 0.f;
+  for (int r0 = wave * kPrepRows; r0 < rows; r0 += kPrepWaves * kPrepRows) {
+    float x1[kPrepRows][kMaxPairs], x2[kPrepRows][kMaxPairs];
 #pragma unroll
-    for (int j = 0; j < kMaxPairs; ++j) ss += x1[j] * x1[j] + x2[j] * x2[j];
-    ss = wave_sum(ss);
-    const float rs = 1.0f / sqrtf(ss / float(D) + eps);
-    const float* w = kind == 0 ? q_norm_w : k_norm_w;
-    const float* cs = rope + int64_t(pos_ok ? pos : 0) * D;
+    for (int rr = 0; rr < kPrepRows; ++rr) {
+      const int r = min(r0 + rr, rows - 1);  // a short last batch re-reads a valid row
+      const float* src = r < hq ? q + (int64_t(t) * hq + r) * D
+                                : (r < hq + hkv ? k + (int64_t(t) * hkv + (r - hq)) * D
+                                                : v + (int64_t(t) * hkv + (r - hq - hkv)) * D);
 #pragma unroll
-    for (int j = 0; j < kMaxPairs; ++j) {
-      const int i = lane + kWave * j;
-      if (i < half) {
-        const float a = x1[j] * rs * w[i];
-        const float b = x2[j] * rs * w[half + i];
-        const float c = cs[i], s = cs[half + i];
-        x1[j] = a * c - b * s;
-        x2[j] = b * c + a * s;
+      for (int j = 0; j < kMaxPairs; ++j) {
+        const int i = min(lane + kWave * j, half - 1);
+        x1[rr][j] = src[i];
+        x2[rr][j] = src[half + i];
       }
     }
-  }
-  if (kind == 0) {
-    f16* dst = q_out + (int64_t(t) * hq + h) * D;
 #pragma unroll
-    for (int j = 0; j < kMaxPairs; ++j) {
-      const int i = lane + kWave * j;
-      if (i < half) {
-        dst[i] = pos_ok ? f16(x1[j]) : f16(0.f);
-        dst[half + i] = pos_ok ? f16(x2[j]) : f16(0.f);
+    for (int rr = 0; rr < kPrepRows; ++rr) {
+      const int r = r0 + rr;
+      if (r >= rows) break;
+      const int kind = r < hq ? 0 : (r < hq + hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v
+      if (kind != 2) {
+        float ss = 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxPairs; ++j)
+          if (lane + kWave * j < half) ss += x1[rr][j] * x1[rr][j] + x2[rr][j] * x2[rr][j];
+        ss = wave_sum(ss);
+        const float rs = 1.0f / sqrtf(ss / float(D) + eps);
+#pragma unroll
+        for (int j = 0; j < kMaxPairs; ++j) {
+          const float a = x1[rr][j] * rs * (kind == 0 ? wq1[j] : wk1[j]);
+          const float b = x2[rr][j] * rs * (kind == 0 ? wq2[j] : wk2[j]);
+          x1[rr][j] = a * c[j] - b * sn[j];
+          x2[rr][j] = b * c[j] + a * sn[j];
+        }
       }
-    }
-  } else if (store) {
-    // pool layer: [2][slot][hkv][D]; V is num_slots rows after K
-    f16* dst = pool + (int64_t(kind - 1) * num_slots + slot) * hkv * D + int64_t(h) * D;
+      f16* dst;
+      if (kind == 0) {
+        dst = q_out + (int64_t(t) * hq + r) * D;
+      } else {
+        if (!store) continue;
+        const int h = kind == 1 ? r - hq : r - hq - hkv;
+        // pool layer: [2][slot][hkv][D]; V is num_slots rows after K
+        dst = pool + (int64_t(kind - 1) * num_slots + slot) * hkv * D + int64_t(h) * D;
+      }
 #pragma unroll
-    for (int j = 0; j < kMaxPairs; ++j) {
-      const int i = lane + kWave * j;
-      if (i < half) {
-        dst[i] = f16(x1[j]);
-        dst[half + i] = f16(x2[j]);
+      for (int j = 0; j < kMaxPairs; ++j) {
+        const int i = lane + kWave * j;
+        if (i < half) {
+          const bool zero = kind == 0 && !pos_ok;
+          dst[i] = zero ? f16(0.f) : f16(x1[rr][j]);
+          dst[half + i] = zero ? f16(0.f) : f16(x2[rr][j]);
+        }
       }
     }
   }
@@ -157,14 +173,11 @@ extern "C" int ifn_qk_norm_rope_append(void* q_out, const float* q, const float*
     return IFN_ERR_INVALID_ARGUMENT;
   if (head_dim > 256) return IFN_ERR_UNSUPPORTED;
   if (num_tokens == 0) return IFN_OK;
-  const int64_t rows = int64_t(num_tokens) * (num_q_heads + 2 * num_kv_heads);
-  const int64_t blocks = (rows + kPrepWaves - 1) / kPrepWaves;
-  if (blocks > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
-  qk_norm_rope_append_kernel<<<dim3(unsigned(blocks)), dim3(kPrepThreads), 0,
-                               reinterpret_cast<hipStream_t>(stream)>>>(
+  auto kernel = head_dim <= 128 ? qk_norm_rope_append_kernel<1> : qk_norm_rope_append_kernel<2>;
+  kernel<<<dim3(unsigned(num_tokens)), dim3(kPrepThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(q_out), q, k, v, q_norm_weight, k_norm_weight, rope_table, max_positions, positions,
-      slot_mapping, active_mask, static_cast<f16*>(kv_pool_layer), num_pages * block_size, num_tokens,
-      num_q_heads, num_kv_heads, head_dim, eps);
+      slot_mapping, active_mask, static_cast<f16*>(kv_pool_layer), num_pages * block_size, num_q_heads,
+      num_kv_heads, head_dim, eps);
   return ifn_launch_status();
 }
 

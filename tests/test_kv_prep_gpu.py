@@ -103,3 +103,18 @@ def test_zero_and_copy_pages_bit_exact(dev):
     assert np.array_equal(P.cpu().numpy().view(np.uint16), exp.view(np.uint16))
     with pytest.raises(ValueError):
         copy_pages(P, to_dev(np.array([1, 2], np.int32), dev), to_dev(np.array([2, 4], np.int32), dev))
+
+
+def test_paged_cache_clear_and_copy_use_the_page_kernels(dev):
+    say("PagedKVCache.clear_pages / copy_pages")
+    from infurnace_amd.cache import PagedKVCache
+    cache = PagedKVCache(2, 10, 8, 128, device=dev, zero=False)
+    g = torch.Generator(device=dev).manual_seed(3)
+    cache.kv.normal_(generator=g)
+    before = cache.kv.clone()
+    cache.copy_pages([1, 4], [6, 8])
+    cache.clear_pages([1, 3])
+    exp = before.clone()
+    exp[:, :, [6, 8]] = before[:, :, [1, 4]]
+    exp[:, :, [1, 3]] = 0
+    assert torch.equal(cache.kv.view(torch.int16), exp.view(torch.int16))
