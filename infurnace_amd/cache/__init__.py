@@ -6,6 +6,8 @@ docs/roadmap.md:325-337 and docs/architecture.md:225-240, 255-257.
 from .block_pool import (OWNERS, BlockPool, BlockPoolError, PoolExhausted, build_block_table, slot_mapping,
                          slot_mapping_for_positions)
 from .kv_manager import KVCacheError, KVManager, PagedKVCache
+from .prefix_cache import PrefixCache, PrefixCacheError
 
 __all__ = ["BlockPool", "BlockPoolError", "PoolExhausted", "OWNERS", "build_block_table", "slot_mapping",
-           "slot_mapping_for_positions", "KVManager", "PagedKVCache", "KVCacheError"]
+           "slot_mapping_for_positions", "KVManager", "PagedKVCache", "KVCacheError", "PrefixCache",
+           "PrefixCacheError"]
