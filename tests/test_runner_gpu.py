@@ -1,0 +1,122 @@
+"""PagedKVRunner: the KV side of a Runner (src/infurnace/executor/runner.py:5-45) driven the way
+the engine drives it -- chunked prefill, batched decode plans with padding rows, clear_slot and
+slot reuse -- against the oracle on a contiguous per-slot cache.  Tolerance atol 2e-3 / rtol
+1e-2 (fp16 outputs, fp32 accumulation)."""
+from dataclasses import dataclass
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import assert_attn_close, say, to_dev
+from infurnace_amd.runner import PagedKVRunner, RunnerError
+
+pytestmark = pytest.mark.gpu
+
+L, HQ, HKV, D = 2, 16, 8, 128
+
+
+@dataclass(frozen=True)
+class Plan:  # the fields of DecodePlan (src/infurnace/scheduler/plan.py:16-28) the runner reads
+    slots: tuple
+    positions: tuple
+    active_mask: tuple
+    block_tables: tuple = ()
+
+
+class Reference:
+    """Contiguous fp16 K/V per (slot, layer), attention by the oracle over an identity table."""
+
+    def __init__(self):
+        self.k, self.v = {}, {}
+
+    def clear(self, slot):
+        for l in range(L):
+            self.k.pop((slot, l), None)
+            self.v.pop((slot, l), None)
+
+    def append(self, slot, layer, k, v):
+        key = (slot, layer)
+        self.k[key] = np.concatenate([self.k.get(key, np.zeros((0, HKV, D), np.float16)), k])
+        self.v[key] = np.concatenate([self.v.get(key, np.zeros((0, HKV, D), np.float16)), v])
+
+    def attend(self, slot, layer, q, start):
+        kk, vv = self.k[(slot, layer)], self.v[(slot, layer)]
+        n = kk.shape[0]
+        pages = -(-n // 16)
+        pool = np.zeros((2, pages, 16, HKV, D), np.float16)
+        pool[0].reshape(-1, HKV, D)[:n] = kk
+        pool[1].reshape(-1, HKV, D)[:n] = vv
+        table = np.arange(pages, dtype=np.int32)
+        if start is None:  # decode: one query [Hq, D] at position n - 1
+            return oracle.paged_attention(q[None], pool, table[None], np.asarray([n], np.int32))[0]
+        # prefill: the T causal queries [T, Hq, D] end at position n - 1
+        return oracle.paged_attention(q[None], pool, table[None], np.asarray([n], np.int32))[0]
+
+
+def _qkv(rng, T):
+    f = lambda *s: rng.standard_normal(s, dtype=np.float32).astype(np.float16)
+    return f(T, HQ, D), f(T, HKV, D), f(T, HKV, D)
+
+
+def test_engine_sequence_of_prefills_decodes_and_slot_reuse(dev):
+    say("runner: chunked prefill, batched decode with padding, clear_slot, reuse")
+    rng = np.random.default_rng(9)
+    run = PagedKVRunner(L, num_slots=3, max_context=256, num_kv_heads=HKV, head_dim=D, num_blocks=64, device=dev)
+    ref = Reference()
+
+    def prefill(slot, start, T):
+        step = run.begin_prefill(slot, start, T)
+        for l in range(L):
+            q, k, v = _qkv(rng, T)
+            out = step.store_attend(l, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))
+            ref.append(slot, l, k, v)
+            assert_attn_close(out, ref.attend(slot, l, q, start), f"prefill slot {slot} start {start} layer {l}")
+
+    def decode(rows):  # rows: list of (slot, active)
+        plan = Plan(tuple(s for s, _ in rows), tuple(run.length(s) if a else 0 for s, a in rows),
+                    tuple(a for _, a in rows))
+        filled = run.fill_block_tables(plan)
+        step = run.begin_decode(plan)
+        for l in range(L):
+            q, k, v = _qkv(rng, len(rows))
+            sentinel = torch.full((len(rows), HQ, D), 3.0, dtype=torch.float16, device=dev)
+            out = step.store_attend(l, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev), out=sentinel)
+            for i, (s, a) in enumerate(rows):
+                if not a:
+                    assert torch.all(out[i] == 3.0), "a padding row was written"
+                    continue
+                ref.append(s, l, k[i:i + 1], v[i:i + 1])
+                assert_attn_close(out[i:i + 1], ref.attend(s, l, q[i], None)[None], f"decode slot {s} layer {l}")
+        return filled
+
+    prefill(0, 0, 32)
+    prefill(0, 32, 8)          # second chunk of the same prompt
+    prefill(1, 0, 20)
+    for _ in range(5):
+        filled = decode([(0, True), (1, True), (2, False)])
+    assert list(filled[0][:3]) == run.mgr.blocks(0)[:3]
+    freed = run.clear_slot(0, zero=True)
+    assert freed and all(torch.all(run.cache.kv[:, :, p] == 0) for p in freed)
+    ref.clear(0)
+    prefill(0, 0, 10)          # the slot is reused from position 0
+    for _ in range(3):
+        decode([(1, True), (0, True)])
+    run.pool.check_invariants()
+
+
+def test_runner_rejects_out_of_order_work(dev):
+    say("runner error paths")
+    run = PagedKVRunner(1, num_slots=2, max_context=64, num_kv_heads=HKV, head_dim=D, num_blocks=8, device=dev)
+    run.begin_prefill(0, 0, 16)
+    with pytest.raises(RunnerError):
+        run.begin_prefill(0, 8, 4)                     # chunk does not start at the stored length
+    with pytest.raises(RunnerError):
+        run.begin_decode(Plan((0,), (15,), (True,)))  # position must be the stored length (16)
+    with pytest.raises(RunnerError):
+        run.begin_decode(Plan((1,), (0,), (True,)))   # slot 1 was never prefilled
+    with pytest.raises(RunnerError):
+        run.begin_prefill(1, 0, 65)                    # past max_context
+    with pytest.raises(RunnerError):
+        run.begin_prefill(3, 0, 1)                     # slot out of range
