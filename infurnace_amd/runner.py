@@ -32,7 +32,7 @@ from typing import Sequence
 import numpy as np
 import torch
 
-from .cache import BlockPool, KVCacheError, KVManager, PagedKVCache
+from .cache import BlockPool, KVCacheError, KVManager, PagedKVCache, PrefixCache
 from .kernels import paged_attention, qk_norm_rope_append, store_kv
 
 __all__ = ["PagedKVRunner", "RunnerError"]
@@ -83,7 +83,8 @@ class PagedKVRunner:
     """Paged KV state for ``num_slots`` concurrent sequences of up to ``max_context`` tokens."""
 
     def __init__(self, num_layers: int, num_slots: int, max_context: int, num_kv_heads: int, head_dim: int,
-                 num_blocks: int, device: str | torch.device = "cuda", block_size: int = 16):
+                 num_blocks: int, device: str | torch.device = "cuda", block_size: int = 16,
+                 prefix_namespace=None, prefix_capacity_blocks: int | None = None):
         if num_slots < 1 or max_context < 1:
             raise RunnerError("num_slots and max_context must be positive")
         self._num_slots, self._max_context = num_slots, max_context
@@ -93,6 +94,10 @@ class PagedKVRunner:
         self.cache = PagedKVCache(num_layers, num_blocks, num_kv_heads, head_dim, block_size, self.device)
         self.pool = BlockPool(num_blocks, block_size)
         self.mgr = KVManager(self.pool, max_pages_per_seq=self.max_pages)
+        # prefix cache (docs/roadmap.md:442-470) when a namespace -- checkpoint and KV-affecting
+        # settings -- is given; PrefillPlan.prefix_token_ids / prefix_cache_hit (plan.py:14-15)
+        self.prefix = (PrefixCache(self.pool, prefix_namespace, prefix_capacity_blocks)
+                       if prefix_namespace is not None else None)
 
     # Runner contract (runner.py:11-21)
     @property
@@ -147,6 +152,31 @@ class PagedKVRunner:
         pos = np.arange(start_position, start_position + num_tokens, dtype=np.int32)
         return _Step(self, self._dev(slots.astype(np.int32)), self._dev(self._table([slot])[0]), None, None,
                      self._dev(pos), start_position, start_position + num_tokens)
+
+    def attach_prefix(self, slot: int, token_ids: Sequence[int]) -> int:
+        """Start an empty slot from the longest cached prefix of ``token_ids`` (complete blocks).
+
+        Returns the number of tokens whose K/V the slot now shares; prefill resumes there
+        (``begin_prefill(slot, n, ...)``).  At least one token is always left to prefill, so
+        the last prompt token's logits are produced.
+        """
+        self._check_slot(slot)
+        if self.prefix is None:
+            raise RunnerError("this runner has no prefix cache (prefix_namespace was not given)")
+        if slot in self.mgr:
+            raise RunnerError(f"slot {slot} is not empty")
+        pages, n = self.prefix.lookup(list(token_ids)[:max(0, len(token_ids) - 1)])
+        self.mgr.add_sequence(slot, prefix_blocks=pages, prefix_len=n)
+        return n
+
+    def publish_prefix(self, slot: int, token_ids: Sequence[int]) -> int:
+        """Publish the complete blocks of the slot's first ``len(token_ids)`` tokens."""
+        self._check_slot(slot)
+        if self.prefix is None:
+            raise RunnerError("this runner has no prefix cache (prefix_namespace was not given)")
+        if len(token_ids) > self.length(slot):
+            raise RunnerError(f"slot {slot} holds {self.length(slot)} tokens, not {len(token_ids)}")
+        return self.prefix.insert(list(token_ids), self.mgr.blocks(slot))
 
     # -- decode -----------------------------------------------------------------------------
 

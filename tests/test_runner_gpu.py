@@ -120,3 +120,31 @@ def test_runner_rejects_out_of_order_work(dev):
         run.begin_prefill(1, 0, 65)                    # past max_context
     with pytest.raises(RunnerError):
         run.begin_prefill(3, 0, 1)                     # slot out of range
+
+
+def test_prefix_cache_hit_shares_pages_and_matches_full_prefill(dev):
+    say("runner: prefix-cache hit")
+    rng = np.random.default_rng(21)
+    run = PagedKVRunner(1, num_slots=2, max_context=256, num_kv_heads=HKV, head_dim=D, num_blocks=32, device=dev,
+                        prefix_namespace=("toy", "fp16"))
+    prompt = list(range(1000, 1048))                 # 48 tokens = 3 complete blocks
+    q, k, v = _qkv(rng, 48)
+    step = run.begin_prefill(0, 0, 48)
+    step.store_attend(0, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))
+    assert run.publish_prefix(0, prompt) == 3
+    # a second prompt extends the first: its first 48 tokens (3 pages) are shared
+    n = run.attach_prefix(1, prompt + [7, 8, 9, 10, 11])
+    assert n == 48 and run.mgr.blocks(1)[:3] == run.mgr.blocks(0)[:3]
+    q2, k2, v2 = _qkv(rng, 5)
+    step = run.begin_prefill(1, 48, 5)
+    out = step.store_attend(0, to_dev(q2, dev), to_dev(k2, dev), to_dev(v2, dev))
+    ref = Reference()
+    ref.append(1, 0, np.concatenate([k, k2]), np.concatenate([v, v2]))
+    assert_attn_close(out, ref.attend(1, 0, q2, 48), "suffix prefill over shared prefix pages")
+    # the shared pages outlive both slots while the cache holds them
+    shared = run.mgr.blocks(0)[:3]
+    run.clear_slot(0)
+    run.clear_slot(1)
+    assert all(not run.pool.is_free(p) for p in shared)
+    assert sorted(run.prefix.evict(3)) == sorted(shared)
+    run.pool.check_invariants()
