@@ -121,6 +121,35 @@ int ifn_paged_decode(void* out, const void* query, const void* kv_pool_layer, in
                      int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/* Workspace bytes ifn_paged_decode_shared_prefix needs for these shapes. */
+size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num_q_heads,
+                                                      int32_t num_kv_heads, int32_t head_dim,
+                                                      int32_t block_size, int32_t shared_pages);
+
+/*
+ * ifn_paged_decode for a batch whose rows share leading pages (a prefix-cache
+ * hit): prefix_pages[0 .. shared_pages) are pages that every row of at least
+ * shared_pages * block_size keys holds, in that order, at the start of its
+ * block table.  The shared pages are read once for all rows (an MFMA pass of
+ * every row's query over them), then each row streams only its own pages and
+ * merges the two partial softmax states.  Same arguments, output and rules as
+ * ifn_paged_decode otherwise; rows shorter than the prefix are attended in
+ * full through their own table.  shared_pages == 0 is ifn_paged_decode.
+ * The precondition is not checked: a row whose leading table entries differ
+ * from prefix_pages is attended as if it held prefix_pages.
+ * Replaces: paged_attention (decode) over block tables with identical leading
+ * ids -- the prefix cache's shared blocks, docs/roadmap.md:442-470,
+ * docs/architecture.md:381-391 -- whose placeholder is
+ * src/infurnace/kernels/paged_attention.py (0 B).
+ */
+int ifn_paged_decode_shared_prefix(void* out, const void* query, const void* kv_pool_layer,
+                                   int64_t num_pages, const int32_t* prefix_pages, int32_t shared_pages,
+                                   const int32_t* block_tables, int32_t max_pages_per_seq,
+                                   const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                                   int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                   int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
+                                   size_t workspace_bytes, void* stream);
+
 /* Workspace bytes ifn_paged_prefill needs for these shapes. */
 size_t ifn_paged_prefill_workspace_bytes(int32_t num_q_tokens, int32_t query_start,
                                          int32_t num_q_heads, int32_t num_kv_heads,

@@ -128,6 +128,17 @@ inline int device_cu_count() {
   return n;
 }
 
+// Shared-prefix pass (paged_prefill.hip) of the shared-prefix decode entry point: each of
+// `batch` query rows attends keys [0, key_len) of the pages prefix_pages[0 ..] with no mask, and
+// its unnormalised (m, l, O) goes to px_ml / px_o in the decode kernel's partial layout.  The key
+// split needs tickets (zero between calls) and split_ml / split_o of the sizes reported by
+// prefix_pass_sizes (0 when the plan has no split).
+void prefix_pass_sizes(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus,
+                       size_t* split_ml_bytes, size_t* split_o_bytes);
+int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
+                int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, uint32_t* tickets,
+                float* split_ml, float* split_o, float* px_ml, float* px_o, int cus, hipStream_t stream);
+
 }  // namespace ifn
 
 // Host-side helpers shared by the entry points.

@@ -53,6 +53,18 @@ struct DecodeWorkspace {
   float* o;         // [slot][G][head_dim] unnormalised outputs
 };
 
+// Shared-prefix (cascade) mode: the first `pages` pages of every row at least pages * block_size
+// keys long hold a prefix whose attention was computed once for all rows (paged prefill in
+// shared-prefix mode) into partial states ml[(seg * G + g) * 2 + {0,1}], o[(seg * G + g) * D + dim],
+// seg = row * Hkv + kv head.  For those rows the kernel streams only the pages after the prefix
+// and merges every segment with its prefix partial; shorter rows are attended in full.
+// pages == 0: ordinary decode.
+struct DecodePrefix {
+  const float* ml;
+  const float* o;
+  int32_t pages;
+};
+
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Workspace: [tickets: kTicketBytes][ml][o].  A launch of n waves publishes into at most
@@ -104,7 +116,13 @@ __device__ __forceinline__ float row_reduce_scatter(const float (&x)[8], int row
 // common case (npieces <= batch) costs a single round trip to device-coherent memory.
 template <int D, int G>
 __device__ __forceinline__ void merge_pieces(f16* __restrict__ o, const DecodeWorkspace& ws, int64_t base,
-                                             int npieces, int lane) {
+                                             int ndecode, int lane, const float* xml = nullptr,
+                                             const float* xo = nullptr) {
+  // pieces 0 .. ndecode-1 are workspace slots base + i; piece ndecode (when xml is given) is the
+  // segment's shared-prefix partial at xml / xo
+  const int npieces = ndecode + (xml != nullptr ? 1 : 0);
+  auto ml_of = [&](int i) { return i < ndecode ? ws.ml + (base + i) * G * 2 : xml; };
+  auto o_of = [&](int i) { return i < ndecode ? ws.o + (base + i) * G * D : xo; };
   constexpr int NC = D / kWave;
   constexpr int kPB = 64 / (G * NC) < 2 ? 2 : (64 / (G * NC) > 16 ? 16 : 64 / (G * NC));
   float mx[G], L[G], O[G][NC];
@@ -118,21 +136,21 @@ __device__ __forceinline__ void merge_pieces(f16* __restrict__ o, const DecodeWo
   for (int c0 = 0; c0 < npieces; c0 += kWave) {
     const int cnt = min(kWave, npieces - c0);
     const bool have = lane < cnt;
-    const int64_t my_slot = base + c0 + (have ? lane : cnt - 1);
+    const float* my_ml = ml_of(c0 + (have ? lane : cnt - 1));
     float mp[G], lp[G], v[kPB][G][NC];
 #pragma unroll
     for (int g = 0; g < G; ++g) {
-      mp[g] = ld_dev(ws.ml + (my_slot * G + g) * 2);
-      lp[g] = ld_dev(ws.ml + (my_slot * G + g) * 2 + 1);
+      mp[g] = ld_dev(my_ml + g * 2);
+      lp[g] = ld_dev(my_ml + g * 2 + 1);
     }
     auto load_batch = [&](int c1) {
 #pragma unroll
       for (int uu = 0; uu < kPB; ++uu) {
-        const int64_t sl = base + c0 + min(c1 + uu, cnt - 1);
+        const float* po = o_of(c0 + min(c1 + uu, cnt - 1));
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int j = 0; j < NC; ++j) v[uu][g][j] = ld_dev(ws.o + (sl * G + g) * D + lane + kWave * j);
+          for (int j = 0; j < NC; ++j) v[uu][g][j] = ld_dev(po + g * D + lane + kWave * j);
       }
     };
     load_batch(0);
@@ -177,7 +195,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
     int64_t num_pages, const int32_t* __restrict__ block_tables, int32_t max_pages,
     const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, int32_t batch,
-    int32_t num_kv_heads, int32_t max_len, float scale_log2, DecodeWorkspace ws) {
+    int32_t num_kv_heads, int32_t max_len, float scale_log2, DecodeWorkspace ws, DecodePrefix px) {
   constexpr int NC = D / 64;  // 16-byte chunks per lane per token row
   constexpr int S = 2;  // register-ring stages (measured: deeper rings were no faster)
   __shared__ int s_off[kRowInts];  // s_off[b] = pages of rows < b; s_off[batch] = total
@@ -189,6 +207,8 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   const int lane = tid % kWave;
   const int hq = num_kv_heads * G;
   const int cap = min(max_pages * kBlock, max_len);
+  const int prefix_keys = px.pages * kBlock;  // rows with at least this many keys use the prefix
+  auto uses_prefix = [&](int len) { return px.pages > 0 && len >= prefix_keys; };
   auto row_len = [&](int b) -> int {  // keys of row b; inactive rows have none
     const int sl = seq_lens[b];                       // both loads issue before either is used
     const int act = active != nullptr ? int(active[b]) : 1;
@@ -204,6 +224,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       const int len = row_len(i);
       s_len[i] = len;
       pages = len > 0 ? (len + kBlock - 1) / kBlock : 0;
+      if (uses_prefix(len)) pages -= px.pages;  // cascade: only the pages after the prefix
     }
     int x = pages;
 #pragma unroll
@@ -231,8 +252,16 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   if (blockIdx.x == 0) {
     for (int b = wave; b < batch; b += kWavesPerBlock) {
       const bool live = active == nullptr || active[b] != 0;
-      if (live && s_len[b] <= 0) {
-        for (int i = lane; i < hq * D; i += kWave) out[int64_t(b) * hq * D + i] = f16(0.f);
+      if (live && s_off[b + 1] == s_off[b]) {  // no pages to stream
+        for (int i = lane; i < hq * D; i += kWave) {
+          float val = 0.f;
+          if (uses_prefix(s_len[b])) {  // everything it sees is the shared prefix
+            const int64_t ps = int64_t(b) * hq + i / D;  // (row * Hkv + kv head) * G + g
+            const float lp = px.ml[ps * 2 + 1];
+            val = lp > 0.f ? px.o[ps * D + i % D] / lp : 0.f;
+          }
+          out[int64_t(b) * hq * D + i] = f16(val);
+        }
       }
     }
   }
@@ -269,7 +298,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   auto run_range = [&](int64_t r, int64_t u_lo, int64_t u_hi) {
     int pend_n = 0, pend_seg0 = 0, pend_seg1 = 0, pend_first0 = 0, pend_first1 = 0, pend_np0 = 0, pend_np1 = 0;
     struct Piece {
-      int b, kvh, seg, page0, np, len;
+      int b, kvh, seg, page0, np, len, poff;  // poff: table entries skipped (shared prefix)
       int64_t seg_start, seg_end;
     };
     auto locate = [&](int64_t u) -> Piece {  // unit u -> the piece of this range that starts at u
@@ -289,6 +318,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       P.np = int(min(u_hi, P.seg_end) - u);
       P.seg = P.b * num_kv_heads + P.kvh;
       P.len = s_len[P.b];
+      P.poff = uses_prefix(P.len) ? px.pages : 0;
       return P;
     };
     // Query rows of a piece and its first two 64-page windows of ids.  The loads are
@@ -302,7 +332,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
         for (int ch = 0; ch < NC; ++ch) qr[g][ch] = as_h8(ld16(qs + g * D + (col + 8 * ch) * 8));
     };
     auto fetch_ids = [&](const Piece& P, int& i0, int& i1) {
-      const int32_t* bt = block_tables + int64_t(P.b) * max_pages + P.page0;
+      const int32_t* bt = block_tables + int64_t(P.b) * max_pages + P.poff + P.page0;
       i0 = bt[min(lane, P.np - 1)];
       i1 = bt[min(lane + kWave, P.np - 1)];
     };
@@ -336,13 +366,13 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     fetch_ids(cur, ids0, ids1);
     issue(head_of(cur), __builtin_amdgcn_readlane(ids0, 0), kb[0], vb[0], okb[0]);
     for (int64_t u = u_lo;;) {  // one piece per iteration (uniform loop)
-      const int np = cur.np, page0 = cur.page0, len = cur.len, seg = cur.seg;
+      const int np = cur.np, page0 = cur.page0, len = cur.len, seg = cur.seg, poff = cur.poff;
       const int64_t seg_start = cur.seg_start, seg_end = cur.seg_end;
       const bool has_next = u + np < u_hi;
       const Piece nxt = has_next ? locate(u + np) : cur;
       if constexpr (kPrefetchQ) fetch_q(nxt, qn);
       fetch_ids(nxt, nid0, nid1);
-      const int32_t* bt = block_tables + int64_t(cur.b) * max_pages + page0;
+      const int32_t* bt = block_tables + int64_t(cur.b) * max_pages + poff + page0;
       const f16* head_base = head_of(cur);
       const f16* head_next = head_of(nxt);
       int cur_w = 0;
@@ -365,7 +395,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
           issue(head_next, __builtin_amdgcn_readlane(nid0, 0), kr, vr, ok);
       };
       auto consume = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool ok) {
-        const int p = page0 + k;
+        const int p = poff + page0 + k;  // page of the row
         bool valid[2];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) valid[tt] = ok && (p * kBlock + row + 8 * tt) < len;
@@ -460,6 +490,19 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       const int64_t w_first = range_of(seg_start);
       const int np_seg = int(range_of(seg_end - 1) - w_first + 1);
       if (np_seg == 1) {  // this wave held the whole segment: write the output
+        if (poff > 0) {  // cascade: merge with the segment's prefix partial first
+#pragma unroll
+          for (int g = 0; g < G; ++g) {
+            const float* pml = px.ml + (int64_t(seg) * G + g) * 2;
+            const float mp = pml[0], lp = pml[1];
+            const float mx = fmaxf(m[g], mp);
+            const float wa = exp2_fast(m[g] - mx), wb = exp2_fast(mp - mx);
+            l[g] = wa * l[g] + wb * lp;
+#pragma unroll
+            for (int ch = 0; ch < NC; ++ch)
+              o_red[g][ch] = wa * o_red[g][ch] + wb * px.o[(int64_t(seg) * G + g) * D + (col + 8 * ch) * 8 + row];
+          }
+        }
         f16* o = out + int64_t(seg) * G * D;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -514,8 +557,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       const int npieces = i == 0 ? pend_np0 : pend_np1;
       if (ti != uint32_t(npieces - 1)) continue;
       // Merge pieces slot = seg + w for w = first .. first + npieces - 1 (log-sum-exp weights).
+      const bool with_prefix = uses_prefix(s_len[seg / num_kv_heads]);
       merge_pieces<D, G>(out + int64_t(seg) * G * D, ws, int64_t(seg) + (i == 0 ? pend_first0 : pend_first1),
-                         npieces, lane);
+                         npieces, lane, with_prefix ? px.ml + int64_t(seg) * G * 2 : nullptr,
+                         with_prefix ? px.o + int64_t(seg) * G * D : nullptr);
       if (lane == 0) reset_ticket(ws.count + seg);
     }
   };
@@ -525,7 +570,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
 
 typedef void (*DecodeKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t,
                              const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, float,
-                             DecodeWorkspace);
+                             DecodeWorkspace, DecodePrefix);
 
 static DecodeKernel pick_decode(int d, int g) {
 #define IFN_DECODE_CASE(DD, GG) \
@@ -588,6 +633,109 @@ extern "C" int ifn_paged_decode(void* out, const void* query, const void* kv_poo
   k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
-      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws);
+      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws, DecodePrefix{nullptr, nullptr, 0});
+  return ifn_launch_status();
+}
+
+namespace ifn {
+
+// Workspace of the shared-prefix entry: [tickets][decode partials][prefix pass key-split
+// partials][per-segment prefix partials].  The tickets are the same kTicketBytes at offset 0 as
+// in every other entry point, so one zeroed workspace serves all of them in any order: each
+// kernel returns every ticket it takes to zero before it ends, and the prefix pass finishes
+// before the decode kernel starts (same stream), so the two take turns on the same array.
+struct SharedLayout {
+  size_t dec_ml, dec_o, split_ml, split_o, px_ml, px_o, bytes;
+};
+
+static SharedLayout shared_layout(int32_t batch, int32_t hkv, int32_t g, int32_t d, int64_t waves,
+                                  int32_t key_len, int cus) {
+  SharedLayout L;
+  size_t off_ml, off_o;
+  const size_t dec = decode_ws_layout(batch, hkv, g, d, waves, &off_ml, &off_o);
+  size_t sml = 0, so = 0;
+  prefix_pass_sizes(batch, hkv * g, hkv, d, key_len, cus, &sml, &so);
+  const size_t segs = size_t(batch) * hkv * g;
+  L.dec_ml = off_ml;
+  L.dec_o = off_o;
+  L.split_ml = dec;
+  L.split_o = align256(L.split_ml + sml);
+  L.px_ml = align256(L.split_o + so);
+  L.px_o = align256(L.px_ml + segs * 2 * sizeof(float));
+  L.bytes = align256(L.px_o + segs * d * sizeof(float));
+  return L;
+}
+
+}  // namespace ifn
+
+extern "C" size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num_q_heads,
+                                                                 int32_t num_kv_heads, int32_t head_dim,
+                                                                 int32_t block_size, int32_t shared_pages) {
+  if (batch < 1 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 || block_size < 1 || shared_pages < 0 ||
+      num_q_heads % num_kv_heads != 0)
+    return 0;
+  int cus = ifn::device_cu_count();
+  if (cus < 1) cus = 256;
+  return ifn::shared_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
+                            int64_t(ifn::decode_blocks()) * ifn::kWavesPerBlock, shared_pages * block_size, cus)
+      .bytes;
+}
+
+extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, const void* kv_pool_layer,
+                                              int64_t num_pages, const int32_t* prefix_pages, int32_t shared_pages,
+                                              const int32_t* block_tables, int32_t max_pages_per_seq,
+                                              const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                                              int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                              int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
+                                              size_t workspace_bytes, void* stream) {
+  using namespace ifn;
+  if (shared_pages == 0)
+    return ifn_paged_decode(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                            active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
+                            workspace, workspace_bytes, stream);
+  if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_tables == nullptr ||
+      seq_lens == nullptr || prefix_pages == nullptr)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || num_pages < 1 || max_pages_per_seq < 1 || num_q_heads < 1 || num_kv_heads < 1 ||
+      head_dim < 1 || max_seq_len < 0 || num_q_heads % num_kv_heads != 0 || shared_pages < 0 ||
+      shared_pages > max_pages_per_seq)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
+  if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
+  const int g = num_q_heads / num_kv_heads;
+  DecodeKernel k = pick_decode(head_dim, g);
+  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
+  IFN_CHECK_ALIGN16(out);
+  IFN_CHECK_ALIGN16(query);
+  IFN_CHECK_ALIGN16(kv_pool_layer);
+  if (batch == 0) return IFN_OK;
+  const int cus = device_cu_count();
+  if (cus < 1) return IFN_ERR_HIP;
+  const int blocks = decode_blocks();
+  const int32_t key_len = shared_pages * kBlock;
+  const SharedLayout L = shared_layout(batch, num_kv_heads, g, head_dim, int64_t(blocks) * kWavesPerBlock,
+                                      key_len, cus);
+  if (workspace == nullptr || workspace_bytes < L.bytes) return IFN_ERR_WORKSPACE;
+  IFN_CHECK_ALIGN16(workspace);
+  if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
+  uint8_t* wsb = static_cast<uint8_t*>(workspace);
+  float* px_ml = reinterpret_cast<float*>(wsb + L.px_ml);
+  float* px_o = reinterpret_cast<float*>(wsb + L.px_o);
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  // 1. every row's queries against the shared pages, once
+  int rc = prefix_pass(static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
+                       prefix_pages, key_len, batch, num_q_heads, num_kv_heads, head_dim, scale * kLog2e,
+                       reinterpret_cast<uint32_t*>(wsb), reinterpret_cast<float*>(wsb + L.split_ml),
+                       reinterpret_cast<float*>(wsb + L.split_o), px_ml, px_o, cus, s);
+  if (rc != IFN_OK) return rc;
+  // 2. the private pages, merged with the prefix partials
+  DecodeWorkspace ws;
+  ws.count = reinterpret_cast<uint32_t*>(wsb);
+  ws.ml = reinterpret_cast<float*>(wsb + L.dec_ml);
+  ws.o = reinterpret_cast<float*>(wsb + L.dec_o);
+  k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, s>>>(
+      static_cast<f16*>(out), static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
+      block_tables, max_pages_per_seq, seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws,
+      DecodePrefix{px_ml, px_o, shared_pages});
   return ifn_launch_status();
 }

@@ -40,7 +40,7 @@
 namespace ifn {
 
 constexpr int kPBlock = 16;  // tokens per page compiled in
-constexpr int kMaxSplit = 4;  // workgroups per (query block, kv head) at most
+constexpr int kMaxSplit = 16;  // workgroups per (query block, kv head) at most
 
 struct PrefillWorkspace {
   uint32_t* count;  // [query block][kv head][G] tickets, zero between calls
@@ -48,32 +48,43 @@ struct PrefillWorkspace {
   float* o;         // [pair][split][D/32][16][64 lanes] unnormalised outputs
 };
 
+// Shared-prefix mode: every query row sees keys [0, key_len) (no causal mask) and the result is
+// written unnormalised, as (m, l, O) in the split-KV partial layout of paged decode --
+// ml[(seg * G + g) * 2 + {0,1}], o[(seg * G + g) * D + dim] with seg = row * Hkv + kv head --
+// for the decode kernel to merge.  key_len == 0 is ordinary causal prefill.
+struct PrefixOut {
+  float* ml;
+  float* o;
+  int32_t key_len;
+};
+
 struct PrefillPlan {
   int64_t n_qb;
   int nsplit;
+  size_t ml_bytes, o_bytes;  // key-split partial arrays
   size_t off_ml, off_o, bytes;
 };
 
 // Key split: enough workgroups to cover the CUs when (query blocks x kv heads) alone does not,
 // provided every split still gets at least two tiles per key group.
-static PrefillPlan plan_prefill(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
+static PrefillPlan plan_prefill(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus,
+                                int32_t key_len = 0) {
   PrefillPlan p;
   const int g = hq / hkv;
   const int groups = g >= 8 ? 1 : (g >= 4 ? 2 : 4);
   p.n_qb = (int64_t(T) + 31) / 32;
   const int64_t units = p.n_qb * hkv;
-  const int64_t max_tiles = (int64_t(query_start) + T + 31) / 32;
+  const int64_t max_tiles = ((key_len > 0 ? int64_t(key_len) : int64_t(query_start) + T) + 31) / 32;
   int ns = 1;
   while (ns < kMaxSplit && units * ns * 2 <= cus && max_tiles >= int64_t(2 * ns) * 2 * groups) ns *= 2;
   if (units * g > kMaxTickets) ns = 1;
   p.nsplit = ns;
   const size_t slots = size_t(units) * g * ns;
-  size_t off = kTicketBytes;
-  p.off_ml = off;
-  off = (off + slots * 64 * 2 * sizeof(float) + 255) & ~size_t(255);
-  p.off_o = off;
-  off = (off + slots * size_t(d) / 32 * 16 * 64 * sizeof(float) + 255) & ~size_t(255);
-  p.bytes = ns > 1 ? off : 256;
+  p.ml_bytes = (slots * 64 * 2 * sizeof(float) + 255) & ~size_t(255);
+  p.o_bytes = (slots * size_t(d) / 32 * 16 * 64 * sizeof(float) + 255) & ~size_t(255);
+  p.off_ml = kTicketBytes;
+  p.off_o = p.off_ml + p.ml_bytes;
+  p.bytes = ns > 1 ? p.off_o + p.o_bytes : 256;
   return p;
 }
 constexpr int kPT = 32;      // keys per tile (one 32x32 MFMA tile)
@@ -102,7 +113,7 @@ template <int D, int G>
 __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
     int64_t num_pages, const int32_t* __restrict__ table, int32_t query_start, int32_t T,
-    int32_t num_kv_heads, int32_t n_qb, int32_t nsplit, float scale_log2, PrefillWorkspace ws) {
+    int32_t num_kv_heads, int32_t n_qb, int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefixOut px) {
   using C = PrefillCfg<D, G>;
   constexpr int kDT = C::kDT;
   constexpr int kKSteps = D / 16;
@@ -122,9 +133,12 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   const int gt = tid - grp * C::kGroupThreads;  // thread index inside the key group
   const int hq = num_kv_heads * G;
   const int head = kvh * G + g;
-  const int total = query_start + T;
+  const bool prefix_mode = px.key_len > 0;
+  const int total = prefix_mode ? px.key_len : query_start + T;  // keys that exist
   const int q0 = qb * 32;
-  const int key_end = min(total, query_start + q0 + 32);  // keys some query of the block sees
+  // keys some query of the block sees, and the position of the block's first query
+  const int key_end = prefix_mode ? total : min(total, query_start + q0 + 32);
+  const int min_pos = prefix_mode ? total - 1 : query_start + q0;
   const int n_tiles = int(ceil_div(key_end, kPT));
   // tile of iteration i for this wave's key group: (i * nsplit + split) * kGroups + grp
   auto tile_of = [&](int i) { return (i * nsplit + split) * C::kGroups + grp; };
@@ -134,7 +148,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   const int col = lane % 32;  // this lane's query column / K row within a tile
   const int half = lane / 32;
   const int my_q = q0 + col;
-  const int my_pos = query_start + my_q;
+  const int my_pos = prefix_mode ? total - 1 : query_start + my_q;
   const bool q_ok = my_q < T;
 
   f16x8 qreg[kKSteps];
@@ -202,7 +216,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   auto tile_flags = [&](int i, int pa, int pb) __attribute__((always_inline)) -> int {
     const int kt = tile_of(i) * kPT;
     const int oka = pa >= 0 && int64_t(pa) < num_pages, okb = pb >= 0 && int64_t(pb) < num_pages;
-    const int full = oka && okb && kt + kPT <= total && kt + kPT - 1 <= query_start + q0;
+    const int full = oka && okb && kt + kPT <= total && kt + kPT - 1 <= min_pos;
     return oka | (okb << 1) | (full << 2);
   };
 
@@ -435,10 +449,23 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
           for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(wk, ld_dev(so + (dt * 16 + r) * kWave + lane), acc[dt][r]);
       }
     }
+    mfin = mx;  // acc and lfin are now relative to the maximum over all splits
     if (lane == 0) reset_ticket(ws.count + pair);
   }
 
   if (!q_ok) return;
+  if (prefix_mode) {  // unnormalised partial for the decode merge (row my_q, kv head kvh, head g)
+    const int64_t pslot = (int64_t(my_q) * num_kv_heads + kvh) * G + g;
+    if (half == 0) {
+      px.ml[pslot * 2 + 0] = mfin;
+      px.ml[pslot * 2 + 1] = lfin;
+    }
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) px.o[pslot * D + 32 * dt + 8 * (r / 4) + 4 * half + (r % 4)] = acc[dt][r];
+    return;
+  }
   const float inv = lfin > 0.f ? 1.f / lfin : 0.f;
   f16* orow = out + (int64_t(my_q) * hq + head) * D;
 #pragma unroll
@@ -453,7 +480,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 }
 
 typedef void (*PrefillKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t,
-                              int32_t, int32_t, int32_t, float, PrefillWorkspace);
+                              int32_t, int32_t, int32_t, float, PrefillWorkspace, PrefixOut);
 
 static PrefillKernel pick_prefill(int d, int g, int* threads) {
 #define IFN_PREFILL_CASE(DD, GG)                          \
@@ -465,6 +492,28 @@ static PrefillKernel pick_prefill(int d, int g, int* threads) {
   IFN_PREFILL_CASE(128, 1) IFN_PREFILL_CASE(128, 2) IFN_PREFILL_CASE(128, 4) IFN_PREFILL_CASE(128, 8)
 #undef IFN_PREFILL_CASE
   return nullptr;
+}
+
+void prefix_pass_sizes(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus,
+                       size_t* split_ml_bytes, size_t* split_o_bytes) {
+  const PrefillPlan p = plan_prefill(batch, 0, hq, hkv, d, cus, key_len);
+  *split_ml_bytes = p.nsplit > 1 ? p.ml_bytes : 0;
+  *split_o_bytes = p.nsplit > 1 ? p.o_bytes : 0;
+}
+
+int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
+                int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, uint32_t* tickets,
+                float* split_ml, float* split_o, float* px_ml, float* px_o, int cus, hipStream_t stream) {
+  int threads = 0;
+  PrefillKernel k = pick_prefill(d, hq / hkv, &threads);
+  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
+  const PrefillPlan p = plan_prefill(batch, 0, hq, hkv, d, cus, key_len);
+  if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
+  const PrefillWorkspace ws{tickets, split_ml, split_o};
+  k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), unsigned(threads), 0, stream>>>(
+      nullptr, q, pool, num_pages, prefix_pages, 0, batch, hkv, int(p.n_qb), p.nsplit, scale_log2, ws,
+      PrefixOut{px_ml, px_o, key_len});
+  return ifn_launch_status();
 }
 
 }  // namespace ifn
@@ -522,6 +571,6 @@ extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_po
       reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_table, query_start, num_q_tokens,
-      num_kv_heads, int(p.n_qb), p.nsplit, scale * kLog2e, ws);
+      num_kv_heads, int(p.n_qb), p.nsplit, scale * kLog2e, ws, PrefixOut{nullptr, nullptr, 0});
   return ifn_launch_status();
 }

@@ -64,14 +64,18 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
                     sequence_lengths: torch.Tensor | None, active_mask: torch.Tensor | None = None, *,
                     layer: int = 0, scale: float | None = None, query_start: int | None = None,
                     out: torch.Tensor | None = None, block_size: int = 16,
-                    max_seq_len: int | None = None) -> torch.Tensor:
+                    max_seq_len: int | None = None, shared_prefix_pages: torch.Tensor | None = None) -> torch.Tensor:
     """Paged GQA attention; returns ``out`` (allocated when None).
 
     Decode (``query_start is None``): ``query`` [B, Hq, D] fp16,
     ``block_tables`` int32 [B, max_pages], ``sequence_lengths`` int32 [B] on the
     device, ``active_mask`` bool/uint8 [B] or None.  ``max_seq_len`` is an
     optional host-side upper bound of ``sequence_lengths`` (default
-    max_pages * block_size) that sizes the launch.
+    max_pages * block_size) that sizes the launch.  ``shared_prefix_pages``
+    (int32 [S] on the device) declares that every row of at least
+    S * block_size keys starts its table with these S pages (a prefix-cache
+    hit); they are then read once for the whole batch instead of once per row.
+    The declaration is trusted, not checked.
 
     Prefill (``query_start`` given): ``query`` [T, Hq, D] of one sequence,
     ``block_tables`` int32 [max_pages] or [1, max_pages]; ``sequence_lengths`` is
@@ -117,6 +121,19 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
         if msl < 0:
             raise PagedAttentionError("max_seq_len must be non-negative")
         if n == 0:
+            return out
+        if shared_prefix_pages is not None:
+            if not isinstance(shared_prefix_pages, torch.Tensor) or shared_prefix_pages.ndim != 1:
+                raise PagedAttentionError("shared_prefix_pages must be a rank-1 int32 tensor")
+            sp = shared_prefix_pages.shape[0]
+            _check("shared_prefix_pages", shared_prefix_pages, (sp,), (torch.int32,), dev)
+            if sp > max_pages:
+                raise PagedAttentionError(f"{sp} shared pages exceed the table's {max_pages} columns")
+            nbytes = lib.ifn_paged_decode_shared_prefix_workspace_bytes(n, hq, hkv, d, bs, sp)
+            ws = workspace_for(dev, stream, nbytes)
+            _capi.call("ifn_paged_decode_shared_prefix", ptr(out), ptr(query), ptr(pool_layer), P,
+                       ptr(shared_prefix_pages), sp, ptr(block_tables), max_pages, ptr(sequence_lengths),
+                       ptr(active_mask), n, hq, hkv, d, bs, msl, float(scale), ptr(ws), ws.numel(), stream)
             return out
         nbytes = lib.ifn_paged_decode_workspace_bytes(n, hq, hkv, d, bs, msl)
         ws = workspace_for(dev, stream, nbytes)

@@ -1,0 +1,158 @@
+"""Shared-prefix decode (ifn_paged_decode_shared_prefix) on the GPU vs the oracle.
+
+The prefix cache (docs/roadmap.md:442-470) makes rows share their leading pages;
+config 5 of the benchmark is 64 rows over one 4096-token prefix.  The shared
+entry point reads those pages once for the batch, then merges each row's own
+pages in.  Its result is the ordinary paged decode of the same tables, so the
+checks are the decode oracle (atol 2e-3 / rtol 1e-2 in fp16) plus agreement
+with ifn_paged_decode on the same inputs.
+"""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import assert_attn_close, oracle_decode, randn16, say, to_dev
+from infurnace_amd import workloads
+from infurnace_amd.kernels import paged_attention
+
+pytestmark = pytest.mark.gpu
+
+
+def _shared(rng, n_shared, suffix_lens, hq, hkv, d, short_rows=()):
+    """Tables whose first n_shared pages are the same ids; rows in short_rows get their own
+    tables and lengths below the prefix."""
+    B = len(suffix_lens)
+    lens = np.asarray([n_shared * 16 + s for s in suffix_lens], np.int32)
+    for b, L in short_rows:
+        lens[b] = L
+    pages = [-(-int(L) // 16) for L in lens]
+    P = n_shared + sum(pages) + 7
+    perm = rng.permutation(P).astype(np.int32)
+    prefix = perm[:n_shared]
+    table = np.zeros((B, max(max(pages), n_shared, 1)), np.int32)
+    off = n_shared
+    short = {b for b, _ in short_rows}
+    for b in range(B):
+        if b in short:
+            table[b, :pages[b]] = perm[off:off + pages[b]]
+            off += pages[b]
+        else:
+            own = pages[b] - n_shared
+            table[b, :n_shared] = prefix
+            table[b, n_shared:pages[b]] = perm[off:off + own]
+            off += own
+    pool = rng.standard_normal((2, P, 16, hkv, d), dtype=np.float32).astype(np.float16)
+    q = rng.standard_normal((B, hq, d), dtype=np.float32).astype(np.float16)
+    return pool, table, lens, q, prefix.copy()
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 128), (64, 8, 128), (16, 8, 64),
+                                      (4, 1, 64)])
+@pytest.mark.parametrize("n_shared", [1, 3, 8, 40])
+def test_matches_oracle_and_plain_decode(dev, hq, hkv, d, n_shared):
+    say(f"shared-prefix hq={hq} hkv={hkv} d={d} shared={n_shared}")
+    rng = np.random.default_rng(hq * 7 + hkv * 3 + d + n_shared)
+    suffix = [0, 1, 15, 16, 17, 100, 333, 1000]  # 0: the row is exactly the prefix
+    pool, table, lens, q, prefix = _shared(rng, n_shared, suffix, hq, hkv, d)
+    args = (to_dev(q, dev), to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev), None)
+    out = paged_attention(*args, shared_prefix_pages=to_dev(prefix, dev))
+    ref = oracle.paged_attention(q, pool, table, lens)
+    assert_attn_close(out, ref, f"hq={hq} hkv={hkv} d={d} shared={n_shared}")
+    plain = paged_attention(*args)
+    assert_attn_close(out, plain.cpu().numpy(), "vs ifn_paged_decode")
+
+
+def test_short_rows_inactive_rows_and_padding(dev):
+    """Rows shorter than the prefix use their own tables; inactive rows are not written."""
+    say("shared-prefix short/inactive rows")
+    rng = np.random.default_rng(21)
+    suffix = [5, 200, 0, 64, 77, 1, 300, 31, 9]
+    pool, table, lens, q, prefix = _shared(rng, 12, suffix, 16, 8, 128, short_rows=[(1, 40), (4, 191), (7, 0)])
+    active = np.ones(len(suffix), np.uint8)
+    active[[3, 6]] = 0
+    q_d = to_dev(q, dev)
+    out = torch.full_like(q_d, 7.0)
+    paged_attention(q_d, to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev), to_dev(active, dev), out=out,
+                    shared_prefix_pages=to_dev(prefix, dev))
+    live = [i for i in range(len(suffix)) if active[i] and lens[i] > 0]
+    ref = oracle.paged_attention(q[live], pool, table[live], lens[live])
+    assert_attn_close(out[live], ref, "live rows")
+    assert bool((out[[3, 6]] == 7.0).all()), "inactive rows were written"
+    assert bool((out[7] == 0).all()), "an active row with no keys must be zero"
+
+
+def test_deterministic_and_workspace_reuse(dev):
+    """Repeated calls are bit-identical; one workspace serves changing shapes."""
+    say("shared-prefix determinism + workspace reuse")
+    rng = np.random.default_rng(22)
+    outs = []
+    for n_shared, suffix in ((64, [10, 500, 3]), (5, [1000, 0, 16, 70, 2]), (64, [10, 500, 3])):
+        pool, table, lens, q, prefix = _shared(np.random.default_rng(n_shared), n_shared, suffix, 32, 8, 128)
+        args = (to_dev(q, dev), to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev), None)
+        o1 = paged_attention(*args, shared_prefix_pages=to_dev(prefix, dev))
+        o2 = paged_attention(*args, shared_prefix_pages=to_dev(prefix, dev))
+        assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+        assert_attn_close(o1, oracle.paged_attention(q, pool, table, lens), f"shared={n_shared}")
+        outs.append(o1)
+    assert torch.equal(outs[0].view(torch.int16), outs[2].view(torch.int16))
+
+
+def test_config5_full_size_with_churn(dev):
+    """Config 5 (64 rows, 4096-token prefix + 512 own tokens, G=4) with suffix page churn."""
+    say("shared-prefix config5 churn")
+    w = workloads.config5()
+    g = torch.Generator(device=dev).manual_seed(505)
+    pool = randn16((2, w.num_pages, 16, 8, 128), g, dev)
+    table = w.block_tables.copy()
+    prefix = to_dev(table[0, :w.shared_prefix_pages].copy(), dev)
+    free_ids = list(w.extra["free_ids"])
+    for step, churn in enumerate(w.extra["churn"][:2]):
+        old = [int(table[r, c]) for r, c in churn]
+        new = free_ids[:len(old)]
+        free_ids = free_ids[len(old):] + old
+        for (r, c), pid in zip(churn, new):
+            table[r, c] = pid
+        idx = torch.as_tensor(new, dtype=torch.long, device=dev)
+        pool[:, idx] = randn16((2, len(new), 16, 8, 128), g, dev)
+        q = randn16((w.batch, 32, 128), g, dev)
+        tdev, ldev = to_dev(table, dev), to_dev(w.seq_lens, dev)
+        out = paged_attention(q, pool, tdev, ldev, None, shared_prefix_pages=prefix)
+        rows = [0, 17, 31, 63]
+        assert_attn_close(out[rows], oracle_decode(pool, table, w.seq_lens, q, rows=rows), f"config5 step {step}")
+        plain = paged_attention(q, pool, tdev, ldev, None)
+        assert_attn_close(out, plain.cpu().numpy(), f"config5 step {step} vs ifn_paged_decode")
+
+
+def test_large_batch_many_splits(dev):
+    """200 rows over a 2000-token prefix: several query blocks and key splits in the prefix pass."""
+    say("shared-prefix B=200 prefix 2000")
+    rng = np.random.default_rng(23)
+    suffix = list(rng.integers(0, 300, size=200))
+    pool, table, lens, q, prefix = _shared(rng, 125, suffix, 16, 8, 128)
+    args = (to_dev(q, dev), to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev), None)
+    out = paged_attention(*args, shared_prefix_pages=to_dev(prefix, dev))
+    rows = [0, 1, 63, 64, 127, 128, 199]
+    ref = oracle.paged_attention(q[rows], pool, table[rows], lens[rows])
+    assert_attn_close(out[rows], ref, "B=200")
+    assert_attn_close(out, paged_attention(*args).cpu().numpy(), "B=200 vs ifn_paged_decode")
+
+
+def test_workspace_shared_with_other_entry_points(dev):
+    """Shared-prefix, plain decode and prefill calls alternate on one workspace (fixed ticket area)."""
+    say("shared-prefix workspace alternation")
+    rng = np.random.default_rng(24)
+    for rep in range(2):
+        for n_shared, suffix, hq in ((40, [3, 900, 64, 0], 16), (200, list(rng.integers(0, 500, 33)), 32)):
+            pool, table, lens, q, prefix = _shared(rng, n_shared, suffix, hq, 8, 128)
+            args = (to_dev(q, dev), to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev), None)
+            ref = oracle.paged_attention(q, pool, table, lens)
+            assert_attn_close(paged_attention(*args, shared_prefix_pages=to_dev(prefix, dev)), ref,
+                              f"rep {rep} shared={n_shared}")
+            assert_attn_close(paged_attention(*args), ref, f"rep {rep} plain")
+            t = 200
+            qp = rng.standard_normal((t, hq, 128), dtype=np.float32).astype(np.float16)
+            o2 = paged_attention(to_dev(qp, dev), args[1], to_dev(table[1], dev), None, None,
+                                 query_start=int(lens[1]) - t)
+            ref2 = oracle.paged_attention(qp[None], pool, table[1:2], lens[1:2])[0]
+            assert_attn_close(o2, ref2, f"rep {rep} prefill")
