@@ -232,7 +232,9 @@ def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> di
     """Decode leg for a second or third workload (configs 4 and 5): `layers` distinct layer pools,
     store_kv (one token per row) then decode per layer; HIP events around every decode launch.
     For a table with shared pages the roofline counts each physical page once (`unique`); the
-    logical K/V a launch attends is reported beside it."""
+    logical K/V a launch attends is reported beside it.  Such a workload is timed through the
+    shared-prefix entry point (prefix pass + decode over private pages, both inside the events) and
+    through the plain decode entry point."""
     import torch
     B, hq, hkv, d, P = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.num_pages
     pool = torch.empty((layers, 2, P, 16, hkv, d), dtype=torch.float16, device=dev)
@@ -245,42 +247,61 @@ def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> di
     sl = torch.from_numpy(w.seq_lens).to(dev)
     slots = torch.from_numpy(w.append_slots).to(dev)
     max_len = int(w.seq_lens.max())
-    ws_bytes = lib.ifn_paged_decode_workspace_bytes(B, hq, hkv, d, 16, max_len)
+    sp = int(w.shared_prefix_pages or 0)
+    prefix = torch.from_numpy(np.ascontiguousarray(w.block_tables[0, :sp])).to(dev) if sp else None
+    ws_bytes = max(lib.ifn_paged_decode_workspace_bytes(B, hq, hkv, d, 16, max_len),
+                   lib.ifn_paged_decode_shared_prefix_workspace_bytes(B, hq, hkv, d, 16, sp) if sp else 0)
     ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
     lb = pool[0].numel() * 2
     scale = 1.0 / np.sqrt(d)
 
-    def one(layer, evs=None, j=0):
+    def one(layer, shared, evs=None, j=0):
         rc = lib.ifn_store_kv(pool.data_ptr() + layer * lb, P, slots.data_ptr(), None, nk[layer].data_ptr(),
                               nk[layer].data_ptr(), B, hkv, d, 16, stream)
         if evs is not None:
             hip.hip.hipEventRecord(evs[2 * j], stream)
-        rc |= lib.ifn_paged_decode(out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P, bt.data_ptr(),
-                                   w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, ws.data_ptr(),
-                                   ws_bytes, stream)
+        if shared:
+            rc |= lib.ifn_paged_decode_shared_prefix(
+                out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P, prefix.data_ptr(), sp,
+                bt.data_ptr(), w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, ws.data_ptr(),
+                ws_bytes, stream)
+        else:
+            rc |= lib.ifn_paged_decode(out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P,
+                                       bt.data_ptr(), w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len,
+                                       scale, ws.data_ptr(), ws_bytes, stream)
         if evs is not None:
             hip.hip.hipEventRecord(evs[2 * j + 1], stream)
         if rc:
             raise RuntimeError(f"{w.name}: launch failed: {rc}")
 
-    for layer in range(layers):
-        one(layer)
-    torch.cuda.synchronize()
-    n = layers * reps
-    evs = hip.create(2 * n)
-    for r in range(reps):
+    def timed(shared: bool) -> float:
         for layer in range(layers):
-            one(layer, evs, r * layers + layer)
-    torch.cuda.synchronize()
-    us = float(np.mean([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(n)])) * 1e3
-    hip.destroy(evs)
+            one(layer, shared)
+        torch.cuda.synchronize()
+        n = layers * reps
+        evs = hip.create(2 * n)
+        for r in range(reps):
+            for layer in range(layers):
+                one(layer, shared, evs, r * layers + layer)
+        torch.cuda.synchronize()
+        us = float(np.mean([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(n)])) * 1e3
+        hip.destroy(evs)
+        return us
+
+    us = timed(bool(sp))
+    us_plain = timed(False) if sp else us
     del pool
     uniq = w.decode_bytes(unique=True)
     logical = w.decode_bytes()
     gbps = uniq / (us / 1e6) / 1e9
-    return {"workload": w.name, "layers_timed": layers, "reps": reps, "decode_us_per_layer": round(us, 2),
-            "bytes_per_layer": uniq, "GB/s": round(gbps, 1), "frac": round(gbps / HBM_PEAK_GBPS, 4),
-            "logical_bytes_per_layer": logical, "effective_GB/s": round(logical / (us / 1e6) / 1e9, 1)}
+    res = {"workload": w.name, "layers_timed": layers, "reps": reps,
+           "entry": "ifn_paged_decode_shared_prefix" if sp else "ifn_paged_decode",
+           "decode_us_per_layer": round(us, 2), "bytes_per_layer": uniq, "GB/s": round(gbps, 1),
+           "frac": round(gbps / HBM_PEAK_GBPS, 4), "logical_bytes_per_layer": logical,
+           "effective_GB/s": round(logical / (us / 1e6) / 1e9, 1)}
+    if sp:
+        res["plain_decode_us_per_layer"] = round(us_plain, 2)
+    return res
 
 
 def main() -> int:

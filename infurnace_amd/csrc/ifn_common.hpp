@@ -15,6 +15,7 @@ typedef f16 f16x2 __attribute__((ext_vector_type(2)));
 typedef f16 f16x4 __attribute__((ext_vector_type(4)));
 typedef f16 f16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -129,15 +130,14 @@ inline int device_cu_count() {
 }
 
 // Shared-prefix pass (paged_prefill.hip) of the shared-prefix decode entry point: each of
-// `batch` query rows attends keys [0, key_len) of the pages prefix_pages[0 ..] with no mask, and
-// its unnormalised (m, l, O) goes to px_ml / px_o in the decode kernel's partial layout.  The key
-// split needs tickets (zero between calls) and split_ml / split_o of the sizes reported by
-// prefix_pass_sizes (0 when the plan has no split).
-void prefix_pass_sizes(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus,
-                       size_t* split_ml_bytes, size_t* split_o_bytes);
+// `batch` query rows attends keys [0, key_len) of the pages prefix_pages[0 ..] with no mask.  The
+// keys are split prefix_pass_splits() ways; each split's unnormalised state (m, l, O) goes to
+// px_ml[((seg * stride + split) * G + g) * 2 + {0,1}] / px_o[((seg * stride + split) * G + g) * D + dim],
+// seg = row * Hkv + kv head, stride >= the split count.
+int prefix_pass_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus);
 int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
-                int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, uint32_t* tickets,
-                float* split_ml, float* split_o, float* px_ml, float* px_o, int cus, hipStream_t stream);
+                int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
+                int32_t stride, int cus, hipStream_t stream);
 
 }  // namespace ifn
 

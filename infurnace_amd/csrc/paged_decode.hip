@@ -54,15 +54,17 @@ struct DecodeWorkspace {
 };
 
 // Shared-prefix (cascade) mode: the first `pages` pages of every row at least pages * block_size
-// keys long hold a prefix whose attention was computed once for all rows (paged prefill in
-// shared-prefix mode) into partial states ml[(seg * G + g) * 2 + {0,1}], o[(seg * G + g) * D + dim],
-// seg = row * Hkv + kv head.  For those rows the kernel streams only the pages after the prefix
-// and merges every segment with its prefix partial; shorter rows are attended in full.
-// pages == 0: ordinary decode.
+// keys long (a cascade row) hold a prefix attended separately, for all rows at once.  For a
+// cascade row the kernel streams only the pages after the prefix and leaves each segment
+// (seg = row * Hkv + kv head) as an unnormalised state (m, l, O) in state nstates - 1 of the
+// segment: ml[((seg * nstates + nstates - 1) * G + g) * 2 + {0,1}], o[(... * G + g) * D + dim].
+// States 0 .. nstates - 2 hold the prefix's; cascade_combine_kernel merges them all.  Shorter rows
+// are attended in full and written directly.  pages == 0: ordinary decode.
 struct DecodePrefix {
-  const float* ml;
-  const float* o;
+  float* ml;
+  float* o;
   int32_t pages;
+  int32_t nstates;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -111,18 +113,16 @@ __device__ __forceinline__ float row_reduce_scatter(const float (&x)[8], int row
 }
 
 // Log-sum-exp merge of the partial states in workspace slots base .. base + npieces - 1 into the
-// G output rows at o (one wave).  Pieces are taken 64 at a time, one per lane, with a running
+// G output rows at o -- or, with st_ml given, into one unnormalised state at st_ml / st_o (one
+// wave).  Pieces are taken 64 at a time, one per lane, with a running
 // maximum; the (m, l) loads and the first batch of O loads are issued together so that the
 // common case (npieces <= batch) costs a single round trip to device-coherent memory.
 template <int D, int G>
 __device__ __forceinline__ void merge_pieces(f16* __restrict__ o, const DecodeWorkspace& ws, int64_t base,
-                                             int ndecode, int lane, const float* xml = nullptr,
-                                             const float* xo = nullptr) {
-  // pieces 0 .. ndecode-1 are workspace slots base + i; piece ndecode (when xml is given) is the
-  // segment's shared-prefix partial at xml / xo
-  const int npieces = ndecode + (xml != nullptr ? 1 : 0);
-  auto ml_of = [&](int i) { return i < ndecode ? ws.ml + (base + i) * G * 2 : xml; };
-  auto o_of = [&](int i) { return i < ndecode ? ws.o + (base + i) * G * D : xo; };
+                                             int npieces, int lane, float* st_ml = nullptr,
+                                             float* st_o = nullptr) {
+  auto ml_of = [&](int i) { return ws.ml + (base + i) * G * 2; };
+  auto o_of = [&](int i) { return ws.o + (base + i) * G * D; };
   constexpr int NC = D / kWave;
   constexpr int kPB = 64 / (G * NC) < 2 ? 2 : (64 / (G * NC) > 16 ? 16 : 64 / (G * NC));
   float mx[G], L[G], O[G][NC];
@@ -182,6 +182,18 @@ __device__ __forceinline__ void merge_pieces(f16* __restrict__ o, const DecodeWo
       load_batch(c1);
     }
   }
+  if (st_ml != nullptr) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+      for (int j = 0; j < NC; ++j) st_o[g * D + lane + kWave * j] = O[g][j];
+      if (lane == 0) {
+        st_ml[g * 2 + 0] = mx[g];
+        st_ml[g * 2 + 1] = L[g];
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int g = 0; g < G; ++g) {
     const float inv = L[g] > 0.f ? 1.f / L[g] : 0.f;
@@ -209,6 +221,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   const int cap = min(max_pages * kBlock, max_len);
   const int prefix_keys = px.pages * kBlock;  // rows with at least this many keys use the prefix
   auto uses_prefix = [&](int len) { return px.pages > 0 && len >= prefix_keys; };
+  auto fin_state = [&](int64_t seg) { return (seg * px.nstates + px.nstates - 1) * G; };  // cascade state
   auto row_len = [&](int b) -> int {  // keys of row b; inactive rows have none
     const int sl = seq_lens[b];                       // both loads issue before either is used
     const int act = active != nullptr ? int(active[b]) : 1;
@@ -253,14 +266,14 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     for (int b = wave; b < batch; b += kWavesPerBlock) {
       const bool live = active == nullptr || active[b] != 0;
       if (live && s_off[b + 1] == s_off[b]) {  // no pages to stream
-        for (int i = lane; i < hq * D; i += kWave) {
-          float val = 0.f;
-          if (uses_prefix(s_len[b])) {  // everything it sees is the shared prefix
-            const int64_t ps = int64_t(b) * hq + i / D;  // (row * Hkv + kv head) * G + g
-            const float lp = px.ml[ps * 2 + 1];
-            val = lp > 0.f ? px.o[ps * D + i % D] / lp : 0.f;
+        if (uses_prefix(s_len[b])) {  // everything it sees is the prefix: an empty own state
+          for (int h = 0; h < num_kv_heads; ++h) {
+            const int64_t st = fin_state(int64_t(b) * num_kv_heads + h);
+            for (int i = lane; i < G * D; i += kWave) px.o[st * D + i] = 0.f;
+            if (lane < 2 * G) px.ml[st * 2 + lane] = (lane & 1) ? 0.f : kNegBig;
           }
-          out[int64_t(b) * hq * D + i] = f16(val);
+        } else {
+          for (int i = lane; i < hq * D; i += kWave) out[int64_t(b) * hq * D + i] = f16(0.f);
         }
       }
     }
@@ -489,20 +502,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       }
       const int64_t w_first = range_of(seg_start);
       const int np_seg = int(range_of(seg_end - 1) - w_first + 1);
-      if (np_seg == 1) {  // this wave held the whole segment: write the output
-        if (poff > 0) {  // cascade: merge with the segment's prefix partial first
-#pragma unroll
-          for (int g = 0; g < G; ++g) {
-            const float* pml = px.ml + (int64_t(seg) * G + g) * 2;
-            const float mp = pml[0], lp = pml[1];
-            const float mx = fmaxf(m[g], mp);
-            const float wa = exp2_fast(m[g] - mx), wb = exp2_fast(mp - mx);
-            l[g] = wa * l[g] + wb * lp;
-#pragma unroll
-            for (int ch = 0; ch < NC; ++ch)
-              o_red[g][ch] = wa * o_red[g][ch] + wb * px.o[(int64_t(seg) * G + g) * D + (col + 8 * ch) * 8 + row];
-          }
-        }
+      if (np_seg == 1 && poff == 0) {  // this wave held the whole segment: write the output
         f16* o = out + int64_t(seg) * G * D;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -510,27 +510,34 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
 #pragma unroll
           for (int ch = 0; ch < NC; ++ch) o[g * D + (col + 8 * ch) * 8 + row] = f16(o_red[g][ch] * inv);
         }
-      } else {  // one of several pieces: publish (m, l, O) in slot = segment + range
-        const int64_t slot = int64_t(seg) + r;
+      } else {
+        // publish (m, l, O): one of several pieces to slot = segment + range; a whole segment of
+        // a cascade row to its final state (merged with the prefix's by the combine kernel)
+        const bool whole = np_seg == 1;
+        const int64_t so = whole ? fin_state(seg) : (int64_t(seg) + r) * G;
+        float* dml = (whole ? px.ml : ws.ml) + so * 2;
+        float* dout = (whole ? px.o : ws.o) + so * D;
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
           for (int ch = 0; ch < NC; ++ch)  // 64 lanes cover 64 consecutive floats
-            st_dev(ws.o + (slot * G + g) * D + (col + 8 * ch) * 8 + row, o_red[g][ch]);
+            st_dev(dout + g * D + (col + 8 * ch) * 8 + row, o_red[g][ch]);
         if (lane == 0) {
 #pragma unroll
           for (int g = 0; g < G; ++g) {
-            st_dev(ws.ml + (slot * G + g) * 2 + 0, m[g]);
-            st_dev(ws.ml + (slot * G + g) * 2 + 1, l[g]);
+            st_dev(dml + g * 2 + 0, m[g]);
+            st_dev(dml + g * 2 + 1, l[g]);
           }
         }
         // only the first and the last piece of a wave's range can be a split segment
-        if (pend_n == 0) {
-          pend_seg0 = seg; pend_first0 = int(w_first); pend_np0 = np_seg;
-        } else {
-          pend_seg1 = seg; pend_first1 = int(w_first); pend_np1 = np_seg;
+        if (!whole) {
+          if (pend_n == 0) {
+            pend_seg0 = seg; pend_first0 = int(w_first); pend_np0 = np_seg;
+          } else {
+            pend_seg1 = seg; pend_first1 = int(w_first); pend_np1 = np_seg;
+          }
+          pend_n = pend_n + 1;
         }
-        pend_n = pend_n + 1;
       }
       if (!has_next) break;
       u += np;
@@ -557,10 +564,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       const int npieces = i == 0 ? pend_np0 : pend_np1;
       if (ti != uint32_t(npieces - 1)) continue;
       // Merge pieces slot = seg + w for w = first .. first + npieces - 1 (log-sum-exp weights).
-      const bool with_prefix = uses_prefix(s_len[seg / num_kv_heads]);
+      const bool cascade = uses_prefix(s_len[seg / num_kv_heads]);  // leave a state for the combine
       merge_pieces<D, G>(out + int64_t(seg) * G * D, ws, int64_t(seg) + (i == 0 ? pend_first0 : pend_first1),
-                         npieces, lane, with_prefix ? px.ml + int64_t(seg) * G * 2 : nullptr,
-                         with_prefix ? px.o + int64_t(seg) * G * D : nullptr);
+                         npieces, lane, cascade ? px.ml + fin_state(seg) * 2 : nullptr,
+                         cascade ? px.o + fin_state(seg) * D : nullptr);
       if (lane == 0) reset_ticket(ws.count + seg);
     }
   };
@@ -568,9 +575,37 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   run_range(r_wave, total_units * r_wave / nw, total_units * (r_wave + 1) / nw);
 }
 
+// Cascade rows: merge each segment's prefix states (one per key split) and the state the decode
+// kernel left for its own pages into the fp16 output.  One wave per (row, kv head) segment; rows
+// that are inactive or shorter than the prefix were finished by the decode kernel.  One-wave
+// workgroups spread the state reads over every CU.
+template <int D, int G>
+__global__ __launch_bounds__(kWave) void cascade_combine_kernel(
+    f16* __restrict__ out, const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active,
+    int32_t batch, int32_t num_kv_heads, int32_t cap, DecodePrefix px) {
+  const int lane = threadIdx.x;
+  const int64_t seg = blockIdx.x;
+  if (seg >= int64_t(batch) * num_kv_heads) return;
+  const int b = int(seg / num_kv_heads);
+  const int len = (active == nullptr || active[b] != 0) ? min(seq_lens[b], cap) : 0;
+  if (px.pages <= 0 || len < px.pages * kBlock) return;  // the decode kernel's rule for cascade rows
+  const DecodeWorkspace states{nullptr, px.ml, px.o};  // the segment's states as merge pieces
+  merge_pieces<D, G>(out + seg * G * D, states, seg * px.nstates, px.nstates, lane);
+}
+
 typedef void (*DecodeKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t,
                              const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, float,
                              DecodeWorkspace, DecodePrefix);
+typedef void (*CombineKernel)(f16*, const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, DecodePrefix);
+
+static CombineKernel pick_combine(int d, int g) {
+#define IFN_COMBINE_CASE(DD, GG) \
+  if (d == DD && g == GG) return cascade_combine_kernel<DD, GG>;
+  IFN_COMBINE_CASE(64, 1) IFN_COMBINE_CASE(64, 2) IFN_COMBINE_CASE(64, 4) IFN_COMBINE_CASE(64, 8)
+  IFN_COMBINE_CASE(128, 1) IFN_COMBINE_CASE(128, 2) IFN_COMBINE_CASE(128, 4) IFN_COMBINE_CASE(128, 8)
+#undef IFN_COMBINE_CASE
+  return nullptr;
+}
 
 static DecodeKernel pick_decode(int d, int g) {
 #define IFN_DECODE_CASE(DD, GG) \
@@ -633,19 +668,20 @@ extern "C" int ifn_paged_decode(void* out, const void* query, const void* kv_poo
   k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
-      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws, DecodePrefix{nullptr, nullptr, 0});
+      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws, DecodePrefix{nullptr, nullptr, 0, 0});
   return ifn_launch_status();
 }
 
 namespace ifn {
 
-// Workspace of the shared-prefix entry: [tickets][decode partials][prefix pass key-split
-// partials][per-segment prefix partials].  The tickets are the same kTicketBytes at offset 0 as
-// in every other entry point, so one zeroed workspace serves all of them in any order: each
-// kernel returns every ticket it takes to zero before it ends, and the prefix pass finishes
-// before the decode kernel starts (same stream), so the two take turns on the same array.
+// Workspace of the shared-prefix entry: [tickets][decode partials][states].  The states are
+// nstates = (prefix key splits + 1) per (segment, head): the prefix pass writes the first
+// nstates - 1, the decode kernel the last.  The tickets are the same kTicketBytes at offset 0 as in
+// every other entry point (the prefix pass and the combine take none), so one workspace zeroed
+// once serves all entry points in any order.
 struct SharedLayout {
-  size_t dec_ml, dec_o, split_ml, split_o, px_ml, px_o, bytes;
+  int nstates;
+  size_t dec_ml, dec_o, st_ml, st_o, bytes;
 };
 
 static SharedLayout shared_layout(int32_t batch, int32_t hkv, int32_t g, int32_t d, int64_t waves,
@@ -653,16 +689,13 @@ static SharedLayout shared_layout(int32_t batch, int32_t hkv, int32_t g, int32_t
   SharedLayout L;
   size_t off_ml, off_o;
   const size_t dec = decode_ws_layout(batch, hkv, g, d, waves, &off_ml, &off_o);
-  size_t sml = 0, so = 0;
-  prefix_pass_sizes(batch, hkv * g, hkv, d, key_len, cus, &sml, &so);
-  const size_t segs = size_t(batch) * hkv * g;
+  L.nstates = prefix_pass_splits(batch, hkv * g, hkv, d, key_len, cus) + 1;
+  const size_t states = size_t(batch) * hkv * L.nstates * g;
   L.dec_ml = off_ml;
   L.dec_o = off_o;
-  L.split_ml = dec;
-  L.split_o = align256(L.split_ml + sml);
-  L.px_ml = align256(L.split_o + so);
-  L.px_o = align256(L.px_ml + segs * 2 * sizeof(float));
-  L.bytes = align256(L.px_o + segs * d * sizeof(float));
+  L.st_ml = dec;
+  L.st_o = align256(L.st_ml + states * 2 * sizeof(float));
+  L.bytes = align256(L.st_o + states * d * sizeof(float));
   return L;
 }
 
@@ -704,7 +737,8 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
   const int g = num_q_heads / num_kv_heads;
   DecodeKernel k = pick_decode(head_dim, g);
-  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
+  CombineKernel kc = pick_combine(head_dim, g);
+  if (k == nullptr || kc == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);
@@ -719,16 +753,15 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   IFN_CHECK_ALIGN16(workspace);
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
   uint8_t* wsb = static_cast<uint8_t*>(workspace);
-  float* px_ml = reinterpret_cast<float*>(wsb + L.px_ml);
-  float* px_o = reinterpret_cast<float*>(wsb + L.px_o);
+  const DecodePrefix px{reinterpret_cast<float*>(wsb + L.st_ml), reinterpret_cast<float*>(wsb + L.st_o),
+                        shared_pages, L.nstates};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
-  // 1. every row's queries against the shared pages, once
+  // 1. every row's queries against the shared pages, once (states 0 .. nstates - 2)
   int rc = prefix_pass(static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
-                       prefix_pages, key_len, batch, num_q_heads, num_kv_heads, head_dim, scale * kLog2e,
-                       reinterpret_cast<uint32_t*>(wsb), reinterpret_cast<float*>(wsb + L.split_ml),
-                       reinterpret_cast<float*>(wsb + L.split_o), px_ml, px_o, cus, s);
+                       prefix_pages, key_len, batch, num_q_heads, num_kv_heads, head_dim, scale * kLog2e, px.ml,
+                       px.o, L.nstates, cus, s);
   if (rc != IFN_OK) return rc;
-  // 2. the private pages, merged with the prefix partials
+  // 2. the private pages (state nstates - 1 of cascade rows; other rows are written directly)
   DecodeWorkspace ws;
   ws.count = reinterpret_cast<uint32_t*>(wsb);
   ws.ml = reinterpret_cast<float*>(wsb + L.dec_ml);
@@ -736,6 +769,13 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, s>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
       block_tables, max_pages_per_seq, seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws,
-      DecodePrefix{px_ml, px_o, shared_pages});
+      px);
+  rc = ifn_launch_status();
+  if (rc != IFN_OK) return rc;
+  // 3. merge the states of every cascade segment into the output
+  const int64_t segs = int64_t(batch) * num_kv_heads;
+  const int32_t cap = int32_t(std::min<int64_t>(int64_t(max_pages_per_seq) * kBlock, max_seq_len));
+  kc<<<dim3(unsigned(segs)), dim3(kWave), 0, s>>>(
+      static_cast<f16*>(out), seq_lens, active_mask, batch, num_kv_heads, cap, px);
   return ifn_launch_status();
 }

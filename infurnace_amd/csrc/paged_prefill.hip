@@ -48,14 +48,16 @@ struct PrefillWorkspace {
   float* o;         // [pair][split][D/32][16][64 lanes] unnormalised outputs
 };
 
-// Shared-prefix mode: every query row sees keys [0, key_len) (no causal mask) and the result is
-// written unnormalised, as (m, l, O) in the split-KV partial layout of paged decode --
-// ml[(seg * G + g) * 2 + {0,1}], o[(seg * G + g) * D + dim] with seg = row * Hkv + kv head --
-// for the decode kernel to merge.  key_len == 0 is ordinary causal prefill.
+// Shared-prefix mode: every query row sees keys [0, key_len) (no causal mask) and each key split
+// writes its result unnormalised, as the state (m, l, O), for a later merge:
+// ml[((seg * stride + split) * G + g) * 2 + {0,1}], o[((seg * stride + split) * G + g) * D + dim]
+// with seg = row * Hkv + kv head (stride >= nsplit).  No cross-workgroup merge happens here.
+// key_len == 0 is ordinary causal prefill.
 struct PrefixOut {
   float* ml;
   float* o;
   int32_t key_len;
+  int32_t stride;
 };
 
 struct PrefillPlan {
@@ -404,7 +406,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     lfin = L;
   }
 
-  if (nsplit > 1) {
+  if (nsplit > 1 && !prefix_mode) {
     // Cross-workgroup merge: publish this split's (m, l, O) for head g with device-coherent
     // stores (lane-contiguous), wait for them, take the (query block, head) ticket; the last of
     // the nsplit arrivals combines the others' partials with its own registers.
@@ -454,16 +456,15 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   }
 
   if (!q_ok) return;
-  if (prefix_mode) {  // unnormalised partial for the decode merge (row my_q, kv head kvh, head g)
-    const int64_t pslot = (int64_t(my_q) * num_kv_heads + kvh) * G + g;
-    if (half == 0) {
-      px.ml[pslot * 2 + 0] = mfin;
-      px.ml[pslot * 2 + 1] = lfin;
-    }
+  if (prefix_mode) {  // this split's unnormalised partial (row my_q, kv head kvh, head g)
+    const int64_t pslot = ((int64_t(my_q) * num_kv_heads + kvh) * px.stride + split) * G + g;
+    if (half == 0) *reinterpret_cast<f32x2*>(px.ml + pslot * 2) = f32x2{mfin, lfin};
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) px.o[pslot * D + 32 * dt + 8 * (r / 4) + 4 * half + (r % 4)] = acc[dt][r];
+      for (int a4 = 0; a4 < 4; ++a4)  // 4 consecutive dims per 16-byte store
+        *reinterpret_cast<f32x4*>(px.o + pslot * D + 32 * dt + 8 * a4 + 4 * half) =
+            f32x4{acc[dt][4 * a4], acc[dt][4 * a4 + 1], acc[dt][4 * a4 + 2], acc[dt][4 * a4 + 3]};
     return;
   }
   const float inv = lfin > 0.f ? 1.f / lfin : 0.f;
@@ -494,25 +495,21 @@ static PrefillKernel pick_prefill(int d, int g, int* threads) {
   return nullptr;
 }
 
-void prefix_pass_sizes(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus,
-                       size_t* split_ml_bytes, size_t* split_o_bytes) {
-  const PrefillPlan p = plan_prefill(batch, 0, hq, hkv, d, cus, key_len);
-  *split_ml_bytes = p.nsplit > 1 ? p.ml_bytes : 0;
-  *split_o_bytes = p.nsplit > 1 ? p.o_bytes : 0;
+int prefix_pass_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus) {
+  return plan_prefill(batch, 0, hq, hkv, d, cus, key_len).nsplit;
 }
 
 int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
-                int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, uint32_t* tickets,
-                float* split_ml, float* split_o, float* px_ml, float* px_o, int cus, hipStream_t stream) {
+                int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
+                int32_t stride, int cus, hipStream_t stream) {
   int threads = 0;
   PrefillKernel k = pick_prefill(d, hq / hkv, &threads);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   const PrefillPlan p = plan_prefill(batch, 0, hq, hkv, d, cus, key_len);
-  if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
-  const PrefillWorkspace ws{tickets, split_ml, split_o};
+  if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31 || stride < p.nsplit) return IFN_ERR_UNSUPPORTED;
   k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), unsigned(threads), 0, stream>>>(
-      nullptr, q, pool, num_pages, prefix_pages, 0, batch, hkv, int(p.n_qb), p.nsplit, scale_log2, ws,
-      PrefixOut{px_ml, px_o, key_len});
+      nullptr, q, pool, num_pages, prefix_pages, 0, batch, hkv, int(p.n_qb), p.nsplit, scale_log2,
+      PrefillWorkspace{nullptr, nullptr, nullptr}, PrefixOut{px_ml, px_o, key_len, stride});
   return ifn_launch_status();
 }
 
@@ -571,6 +568,6 @@ extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_po
       reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_table, query_start, num_q_tokens,
-      num_kv_heads, int(p.n_qb), p.nsplit, scale * kLog2e, ws, PrefixOut{nullptr, nullptr, 0});
+      num_kv_heads, int(p.n_qb), p.nsplit, scale * kLog2e, ws, PrefixOut{nullptr, nullptr, 0, 0});
   return ifn_launch_status();
 }
