@@ -130,11 +130,13 @@ size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num
  * ifn_paged_decode for a batch whose rows share leading pages (a prefix-cache
  * hit): prefix_pages[0 .. shared_pages) are pages that every row of at least
  * shared_pages * block_size keys holds, in that order, at the start of its
- * block table.  The shared pages are read once for all rows (an MFMA pass of
- * every row's query over them), then each row streams only its own pages and
- * merges the two partial softmax states.  Same arguments, output and rules as
+ * block table.  Three launches on `stream`: the shared pages are read once for
+ * all rows (an MFMA pass of every row's queries over them, split over keys),
+ * each row streams only its own pages, and a combine merges the partial
+ * softmax states per (row, kv head).  Same arguments, output and rules as
  * ifn_paged_decode otherwise; rows shorter than the prefix are attended in
  * full through their own table.  shared_pages == 0 is ifn_paged_decode.
+ * head_dim 64 or 128 (IFN_ERR_UNSUPPORTED otherwise, as for prefill).
  * The precondition is not checked: a row whose leading table entries differ
  * from prefix_pages is attended as if it held prefix_pages.
  * Replaces: paged_attention (decode) over block tables with identical leading
