@@ -19,7 +19,10 @@ this package's pool, tables and kernels:
   through the fused norm + rotary + append kernel (model.py:183-196);
 * ``clear_slot(slot)`` releases the slot's pages (zeroing them on request:
   buffers.py:67-81), which is what the engine calls on every terminal transition
-  (src/infurnace/engine/engine.py:89,130,166).
+  (src/infurnace/engine/engine.py:89,130,166);
+* a decode batch whose live rows start with the same pages (prefix-cache hits)
+  reads those pages once for the batch (``paged_attention(...,
+  shared_prefix_pages=...)``) when they are at least ``shared_prefix_min_pages``.
 
 The model itself (projections, MLP, logits) stays with the caller.
 """
@@ -53,6 +56,7 @@ class _Step:
     positions: torch.Tensor           # int32 [T]
     query_start: int | None           # prefill only
     max_len: int
+    shared_prefix: torch.Tensor | None = None  # int32 pages every live decode row starts with
 
     def store_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      out: torch.Tensor | None = None) -> torch.Tensor:
@@ -63,7 +67,7 @@ class _Step:
             return paged_attention(q, kv, self.block_tables, None, None, layer=layer, query_start=self.query_start,
                                    out=out)
         return paged_attention(q, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
-                               max_seq_len=self.max_len, out=out)
+                               max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
 
     def prep_store_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, rope: torch.Tensor,
@@ -76,7 +80,7 @@ class _Step:
             return paged_attention(q16, kv, self.block_tables, None, None, layer=layer,
                                    query_start=self.query_start, out=out)
         return paged_attention(q16, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
-                               max_seq_len=self.max_len, out=out)
+                               max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
 
 
 class PagedKVRunner:
@@ -84,7 +88,8 @@ class PagedKVRunner:
 
     def __init__(self, num_layers: int, num_slots: int, max_context: int, num_kv_heads: int, head_dim: int,
                  num_blocks: int, device: str | torch.device = "cuda", block_size: int = 16,
-                 prefix_namespace=None, prefix_capacity_blocks: int | None = None):
+                 prefix_namespace=None, prefix_capacity_blocks: int | None = None,
+                 shared_prefix_min_pages: int = 64):
         if num_slots < 1 or max_context < 1:
             raise RunnerError("num_slots and max_context must be positive")
         self._num_slots, self._max_context = num_slots, max_context
@@ -98,6 +103,9 @@ class PagedKVRunner:
         # settings -- is given; PrefillPlan.prefix_token_ids / prefix_cache_hit (plan.py:14-15)
         self.prefix = (PrefixCache(self.pool, prefix_namespace, prefix_capacity_blocks)
                        if prefix_namespace is not None else None)
+        # below this many common leading pages, decode re-reads them per row (from cache) instead
+        # of paying the shared-prefix path's two extra launches
+        self.shared_prefix_min_pages = max(1, int(shared_prefix_min_pages))
 
     # Runner contract (runner.py:11-21)
     @property
@@ -214,8 +222,23 @@ class PagedKVRunner:
         for i in live:
             lens[i] = positions[i] + 1
         act = np.asarray(active, np.uint8)
+        shared = self._common_pages([slots[i] for i in live])
         return _Step(self, self._dev(sm), self._dev(self._table(slots)), self._dev(lens), self._dev(act),
-                     self._dev(np.asarray(positions, np.int32)), None, int(lens.max()) if len(lens) else 0)
+                     self._dev(np.asarray(positions, np.int32)), None, int(lens.max()) if len(lens) else 0,
+                     self._dev(np.asarray(shared, np.int32)) if len(shared) >= self.shared_prefix_min_pages
+                     else None)
+
+    def _common_pages(self, slots: Sequence[int]) -> list[int]:
+        """Leading pages that every listed slot holds at the same positions (at least two slots),
+        limited to pages complete in every slot."""
+        if len(slots) < 2:
+            return []
+        blocks = [self.mgr.blocks(s) for s in slots]
+        limit = min(min(len(b) for b in blocks), min(self.length(s) for s in slots) // self.block_size)
+        n = 0
+        while n < limit and all(b[n] == blocks[0][n] for b in blocks[1:]):
+            n += 1
+        return blocks[0][:n]
 
     # -- lifecycle --------------------------------------------------------------------------
 

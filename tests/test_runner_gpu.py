@@ -148,3 +148,41 @@ def test_prefix_cache_hit_shares_pages_and_matches_full_prefill(dev):
     assert all(not run.pool.is_free(p) for p in shared)
     assert sorted(run.prefix.evict(3)) == sorted(shared)
     run.pool.check_invariants()
+
+
+def test_decode_batch_over_shared_prefix_uses_one_read(dev):
+    """Rows attached to one cached prompt decode through the shared-prefix path; outputs match."""
+    say("runner: decode over a shared prefix")
+    rng = np.random.default_rng(31)
+    run = PagedKVRunner(L, num_slots=4, max_context=512, num_kv_heads=HKV, head_dim=D, num_blocks=128, device=dev,
+                        prefix_namespace=("toy", "fp16"), shared_prefix_min_pages=2)
+    ref = Reference()
+    prompt = list(range(500, 500 + 100))              # 6 complete blocks + 4 tokens
+    step = run.begin_prefill(0, 0, 100)
+    for l in range(L):
+        q, k, v = _qkv(rng, 100)
+        step.store_attend(l, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))
+        ref.append(0, l, k, v)
+    run.publish_prefix(0, prompt)
+    for s, extra in ((1, 9), (2, 30), (3, 1)):
+        n = run.attach_prefix(s, prompt[:96] + list(range(extra)))
+        assert n == 96
+        for l in range(L):
+            ref.k[(s, l)], ref.v[(s, l)] = ref.k[(0, l)][:96].copy(), ref.v[(0, l)][:96].copy()
+        step = run.begin_prefill(s, n, extra)
+        for l in range(L):
+            q, k, v = _qkv(rng, extra)
+            step.store_attend(l, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))
+            ref.append(s, l, k, v)
+    for it in range(3):
+        rows = [(1, True), (2, True), (0, True), (3, True)]
+        plan = Plan(tuple(s for s, _ in rows), tuple(run.length(s) for s, _ in rows), tuple(a for _, a in rows))
+        step = run.begin_decode(plan)
+        assert step.shared_prefix is not None and step.shared_prefix.numel() == 6
+        for l in range(L):
+            q, k, v = _qkv(rng, len(rows))
+            out = step.store_attend(l, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))
+            for i, (s, _) in enumerate(rows):
+                ref.append(s, l, k[i:i + 1], v[i:i + 1])
+                assert_attn_close(out[i:i + 1], ref.attend(s, l, q[i], None)[None], f"shared decode slot {s} l {l}")
+    run.pool.check_invariants()
