@@ -205,7 +205,10 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 #pragma unroll
   for (int it = 0; it < C::kVPer; ++it) {
     const int idx = min(gt + it * C::kGroupThreads, C::kVItems - 1);
-    const int kq = idx / kChunks, c = idx % kChunks;
+    // key quad fastest: the 8 lanes of one dim chunk write 8 different 8-byte Vt columns of one
+    // row (distinct banks); with the chunk fastest, the transposed writes hit 2 banks 8 ways.
+    // Global loads stay 128-byte contiguous per key row.
+    const int kq = idx % (kPT / 4), c = idx / (kPT / 4);
     v_key[it] = 4 * kq;
     v_hi[it] = 4 * kq >= kPBlock;
     v_goff[it] = ((4 * kq) % kPBlock) * int(tok_stride) + c * 8;
@@ -268,9 +271,9 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
         for (int e = 0; e < 8; ++e) {
           const int w = e / 2;
           const uint32_t a0 = st.v[it][0][w], a1 = st.v[it][1][w], a2 = st.v[it][2][w], a3 = st.v[it][3][w];
-          const u32x2 col4 = (e & 1) == 0
-                                 ? u32x2{(a0 & 0xFFFFu) | (a1 << 16), (a2 & 0xFFFFu) | (a3 << 16)}
-                                 : u32x2{(a0 >> 16) | (a1 & 0xFFFF0000u), (a2 >> 16) | (a3 & 0xFFFF0000u)};
+          // one byte permute per word: {lo(a0), lo(a1)} or {hi(a0), hi(a1)}
+          const uint32_t kSel = (e & 1) == 0 ? 0x05040100u : 0x07060302u;  // e is unrolled: a constant
+          const u32x2 col4 = u32x2{__builtin_amdgcn_perm(a1, a0, kSel), __builtin_amdgcn_perm(a3, a2, kSel)};
           *reinterpret_cast<u32x2*>(vt + v_loff[it] + e * C::kVS) = col4;
         }
       }
@@ -306,18 +309,25 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 #pragma unroll
     for (int r = 1; r < 16; ++r) mx = fmaxf(mx, st[r]);
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mn = fmaxf(m, mx * scale_log2);
-    if (__builtin_amdgcn_ballot_w64(mn > m) != 0) {  // some running max moved: rescale
+    // Lazy rescale: the reference m moves only when a score exceeds it by more than kSlack
+    // (log2 units), so P = 2^(s - m) stays below 2^kSlack and the 16-per-lane accumulator
+    // rescale runs on a few tiles instead of most of them.  acc and lsum stay relative to m, so
+    // the normalised result is unchanged.
+    constexpr float kSlack = 8.f;
+    const float cand = mx * scale_log2;
+    const bool grow = cand > m + kSlack;
+    if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+      const float mn = grow ? cand : m;
       const float alpha = exp2_fast(m - mn);
       lsum *= alpha;
 #pragma unroll
       for (int dt = 0; dt < kDT; ++dt) acc[dt] *= alpha;
+      m = mn;
     }
-    m = mn;
     float pv[16];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
-      pv[r] = exp2_fast(fmaf(st[r], scale_log2, -mn));
+      pv[r] = exp2_fast(fmaf(st[r], scale_log2, -m));
       lsum += pv[r];
     }
     // built by value: element-wise writes into a local vector array end up in scratch
