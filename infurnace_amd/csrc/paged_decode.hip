@@ -202,7 +202,9 @@ __device__ __forceinline__ void merge_pieces(f16* __restrict__ o, const DecodeWo
   }
 }
 
-template <int D, int G>
+// kCascade: compiled with the shared-prefix (cascade) paths; without it every cascade branch
+// folds away and px is ignored.
+template <int D, int G, bool kCascade>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
     int64_t num_pages, const int32_t* __restrict__ block_tables, int32_t max_pages,
@@ -220,7 +222,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   const int hq = num_kv_heads * G;
   const int cap = min(max_pages * kBlock, max_len);
   const int prefix_keys = px.pages * kBlock;  // rows with at least this many keys use the prefix
-  auto uses_prefix = [&](int len) { return px.pages > 0 && len >= prefix_keys; };
+  auto uses_prefix = [&](int len) { return kCascade && px.pages > 0 && len >= prefix_keys; };
   auto fin_state = [&](int64_t seg) { return (seg * px.nstates + px.nstates - 1) * G; };  // cascade state
   auto row_len = [&](int b) -> int {  // keys of row b; inactive rows have none
     const int sl = seq_lens[b];                       // both loads issue before either is used
@@ -607,13 +609,18 @@ static CombineKernel pick_combine(int d, int g) {
   return nullptr;
 }
 
-static DecodeKernel pick_decode(int d, int g) {
+static DecodeKernel pick_decode(int d, int g, bool cascade = false) {
 #define IFN_DECODE_CASE(DD, GG) \
-  if (d == DD && g == GG) return paged_decode_kernel<DD, GG>;
+  if (d == DD && g == GG && !cascade) return paged_decode_kernel<DD, GG, false>;
+#define IFN_CASCADE_CASE(DD, GG) \
+  if (d == DD && g == GG && cascade) return paged_decode_kernel<DD, GG, true>;
   IFN_DECODE_CASE(64, 1) IFN_DECODE_CASE(64, 2) IFN_DECODE_CASE(64, 4) IFN_DECODE_CASE(64, 8)
   IFN_DECODE_CASE(128, 1) IFN_DECODE_CASE(128, 2) IFN_DECODE_CASE(128, 4) IFN_DECODE_CASE(128, 8)
   IFN_DECODE_CASE(256, 1) IFN_DECODE_CASE(256, 2) IFN_DECODE_CASE(256, 4)
+  IFN_CASCADE_CASE(64, 1) IFN_CASCADE_CASE(64, 2) IFN_CASCADE_CASE(64, 4) IFN_CASCADE_CASE(64, 8)
+  IFN_CASCADE_CASE(128, 1) IFN_CASCADE_CASE(128, 2) IFN_CASCADE_CASE(128, 4) IFN_CASCADE_CASE(128, 8)
 #undef IFN_DECODE_CASE
+#undef IFN_CASCADE_CASE
   return nullptr;
 }
 
@@ -736,7 +743,7 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
   const int g = num_q_heads / num_kv_heads;
-  DecodeKernel k = pick_decode(head_dim, g);
+  DecodeKernel k = pick_decode(head_dim, g, true);
   CombineKernel kc = pick_combine(head_dim, g);
   if (k == nullptr || kc == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
