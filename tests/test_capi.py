@@ -80,6 +80,34 @@ def test_paged_decode_host_validation():
     assert call(B=21504) == _capi.IFN_ERR_UNSUPPORTED  # batch beyond the LDS prefix table
 
 
+def test_shared_prefix_decode_host_validation():
+    L = _capi.lib()
+    base = dict(out=A, q=A, pool=A, P=1024, pp=A, S=8, bt=A, W=256, sl=A, am=None, B=32, hq=32, hkv=8, d=128,
+                bs=16, msl=4096, scale=0.0, ws=None, wsb=0)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return L.ifn_paged_decode_shared_prefix(a["out"], a["q"], a["pool"], a["P"], a["pp"], a["S"], a["bt"], a["W"],
+                                                a["sl"], a["am"], a["B"], a["hq"], a["hkv"], a["d"], a["bs"], a["msl"],
+                                                a["scale"], a["ws"], a["wsb"], None)
+
+    assert call(pp=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(out=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(S=-1) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(S=257) == _capi.IFN_ERR_INVALID_ARGUMENT  # more shared pages than table columns
+    assert call(hq=12, hkv=8) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(bs=32) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(d=256, hq=16) == _capi.IFN_ERR_UNSUPPORTED  # the prefix pass (MFMA) covers D 64 and 128
+    assert call(q=A + 4) == _capi.IFN_ERR_ALIGNMENT
+    assert call(B=0) == _capi.IFN_OK
+    # shared_pages == 0 is the plain decode entry point (same checks and codes)
+    assert call(S=0, pp=None) == _capi.IFN_ERR_WORKSPACE
+    sizes = [L.ifn_paged_decode_shared_prefix_workspace_bytes(64, 32, 8, 128, 16, s) for s in (0, 8, 256)]
+    plain = L.ifn_paged_decode_workspace_bytes(64, 32, 8, 128, 16, 4608)
+    assert all(x > plain for x in sizes) and all(x % 256 == 0 for x in sizes)
+    assert L.ifn_paged_decode_shared_prefix_workspace_bytes(0, 32, 8, 128, 16, 8) == 0
+
+
 def test_workspace_sizes():
     L = _capi.lib()
     small = L.ifn_paged_decode_workspace_bytes(1, 16, 8, 128, 16, 512)
