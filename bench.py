@@ -390,6 +390,35 @@ def main() -> int:
     hip.destroy(evs)
     print(f"[bench] timed {K} steps x {L} layers in {wall:.3f} s", file=sys.stderr, flush=True)
 
+    # The same step with the append fused into the decode launch (ifn_paged_decode_append): one
+    # launch per layer instead of two, same output and pool bytes.
+    fused_args = [(out[i].data_ptr(), q[i].data_ptr(), pool.data_ptr() + i * layer_bytes, P, bt.data_ptr(),
+                   w.max_pages, sl.data_ptr(), None, slots.data_ptr(), nk[i].data_ptr(), nv[i].data_ptr(), B, hq,
+                   hkv, d, 16, max_len, scale, ws.data_ptr(), ws_bytes, stream) for i in range(L)]
+    fused_fn = lib.ifn_paged_decode_append
+
+    def fused_step(evs=None, base=0):
+        for i in range(L):
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 2 * i], stream)
+            rc = fused_fn(*fused_args[i])
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 2 * i + 1], stream)
+            if rc:
+                raise RuntimeError(f"fused launch failed in layer {i}: {_capi.status_string(rc)}")
+
+    for _ in range(args.warmup):
+        fused_step()
+    torch.cuda.synchronize()
+    fevs = hip.create(2 * L * K)
+    t0 = time.perf_counter()
+    for s_ in range(K):
+        fused_step(fevs, 2 * L * s_)
+    torch.cuda.synchronize()
+    fused_wall = time.perf_counter() - t0
+    fused_ms = [hip.elapsed_ms(fevs[2 * j], fevs[2 * j + 1]) for j in range(L * K)]
+    hip.destroy(fevs)
+
     dec_bytes = w.decode_bytes()
     dec_s = float(np.mean(dec_ms)) / 1e3
     gbps = dec_bytes / dec_s / 1e9
@@ -481,6 +510,10 @@ def main() -> int:
         "decode_us_per_layer": round(dec_s * 1e6, 3),
         "decode_bytes_per_layer": dec_bytes,
         "kv_append_us_per_layer": round(float(np.mean(app_ms)) * 1e3, 3),
+        "fused_step": {"entry": "ifn_paged_decode_append (store_kv + paged decode in one launch per layer)",
+                       "us_per_layer": round(float(np.mean(fused_ms)) * 1e3, 3),
+                       "two_launch_us_per_layer": round((float(np.mean(app_ms)) + float(np.mean(dec_ms))) * 1e3, 3),
+                       "ms_per_step": round(fused_wall / K * 1e3, 4)},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
         "append_batched": {"workload": "store_kv_layers, 28 layers x 2048 tokens (config 3 prompt), one launch",

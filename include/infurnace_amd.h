@@ -121,6 +121,29 @@ int ifn_paged_decode(void* out, const void* query, const void* kv_pool_layer, in
                      int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
                      size_t workspace_bytes, void* stream);
 
+/*
+ * The decode step's append and attention in one launch: the result (output and
+ * pool) equals ifn_store_kv(kv_pool_layer, num_pages, slot_mapping,
+ * active_mask, new_k, new_v, batch, ...) followed by ifn_paged_decode(...) on
+ * the same stream.  new_k / new_v are [batch][num_kv_heads][head_dim] fp16;
+ * row b appends at slot_mapping[b] when active (out-of-range slots store
+ * nothing, as in ifn_store_kv).  The attention takes the appended token from
+ * new_k / new_v instead of reading it back, so the store needs no ordering
+ * against the reads.  Precondition (true for any paged KV state): an appended
+ * slot is not read by another row of the same call.  Same workspace as
+ * ifn_paged_decode.
+ * Replaces: store_kv then paged_attention of one decode step
+ * (docs/architecture.md:245-246,249-253; contiguous form
+ * src/infurnace/executor/tinygrad/model.py:191-200).
+ */
+int ifn_paged_decode_append(void* out, const void* query, void* kv_pool_layer, int64_t num_pages,
+                            const int32_t* block_tables, int32_t max_pages_per_seq,
+                            const int32_t* seq_lens, const uint8_t* active_mask,
+                            const int32_t* slot_mapping, const void* new_k, const void* new_v,
+                            int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
+                            size_t workspace_bytes, void* stream);
+
 /* Workspace bytes ifn_paged_decode_shared_prefix needs for these shapes. */
 size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num_q_heads,
                                                       int32_t num_kv_heads, int32_t head_dim,

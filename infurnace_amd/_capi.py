@@ -37,6 +37,8 @@ SIGNATURES: dict[str, tuple] = {
     "ifn_paged_decode_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "ifn_paged_decode": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _p, _i32, _i32, _i32, _i32,
                                         _i32, _i32, _f32, _p, _sz, _p]),
+    "ifn_paged_decode_append": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _p, _p, _p, _p, _i32, _i32, _i32,
+                                               _i32, _i32, _i32, _f32, _p, _sz, _p]),
     "ifn_paged_decode_shared_prefix_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "ifn_paged_decode_shared_prefix": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _i32, _p, _p, _i32, _i32,
                                                       _i32, _i32, _i32, _i32, _f32, _p, _sz, _p]),

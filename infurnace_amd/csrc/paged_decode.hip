@@ -67,6 +67,16 @@ struct DecodePrefix {
   int32_t nstates;
 };
 
+// Fused append: store new_k / new_v of every active row at slot_mapping[row] (the store_kv
+// of the same step) inside the decode launch.  The attention reads the appended token from
+// new_k / new_v, not from the pool, so no ordering between the store and the reads is needed.
+struct DecodeAppend {
+  const f16* new_k;         // [batch][Hkv][D]
+  const f16* new_v;
+  const int32_t* slots;     // [batch]
+  f16* pool;                // the layer's pool (the same memory the kernel reads)
+};
+
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Workspace: [tickets: kTicketBytes][ml][o].  A launch of n waves publishes into at most
@@ -203,17 +213,20 @@ __device__ __forceinline__ void merge_pieces(f16* __restrict__ o, const DecodeWo
 }
 
 // kCascade: compiled with the shared-prefix (cascade) paths; without it every cascade branch
-// folds away and px is ignored.
-template <int D, int G, bool kCascade>
+// folds away and px is ignored.  kAppend: compiled with the fused append (ap); otherwise ap is
+// ignored.
+template <int D, int G, bool kCascade, bool kAppend>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
     int64_t num_pages, const int32_t* __restrict__ block_tables, int32_t max_pages,
     const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, int32_t batch,
-    int32_t num_kv_heads, int32_t max_len, float scale_log2, DecodeWorkspace ws, DecodePrefix px) {
+    int32_t num_kv_heads, int32_t max_len, float scale_log2, DecodeWorkspace ws, DecodePrefix px,
+    DecodeAppend ap) {
   constexpr int NC = D / 64;  // 16-byte chunks per lane per token row
   constexpr int S = 2;  // register-ring stages (measured: deeper rings were no faster)
   __shared__ int s_off[kRowInts];  // s_off[b] = pages of rows < b; s_off[batch] = total
   __shared__ int s_len[kRowInts];  // keys of row b (0 for inactive rows)
+  __shared__ int s_slot[kAppend ? kRowInts : 1];  // appended slot of row b, -1 if none
   __shared__ int s_wsum[kWavesPerBlock];
 
   const int tid = threadIdx.x;
@@ -229,6 +242,30 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     const int act = active != nullptr ? int(active[b]) : 1;
     return act != 0 ? min(sl, cap) : 0;
   };
+  const int64_t num_slots = num_pages * kBlock;
+  auto append_slot = [&](int b) -> int {  // the slot row b appends to, -1 for none (store_kv's rule)
+    const int64_t sl = ap.slots[b];
+    const bool act = active == nullptr || active[b] != 0;
+    return act && sl >= 0 && sl < num_slots ? int(sl) : -1;
+  };
+
+  // 0. Fused append: 16-byte chunks of every appended K and V row, spread over the grid.  No
+  // wave of this launch reads these slots (the attention takes the token from new_k / new_v).
+  if constexpr (kAppend) {
+    const int chunks = num_kv_heads * D / 8;  // per row of K (and of V)
+    const int64_t items = int64_t(batch) * 2 * chunks;
+    for (int64_t it = int64_t(blockIdx.x) * kDecodeThreads + tid; it < items;
+         it += int64_t(gridDim.x) * kDecodeThreads) {
+      const int b = int(it / (2 * chunks));
+      const int rem = int(it % (2 * chunks));
+      const int kv = rem / chunks, c = rem % chunks;
+      const int slot = append_slot(b);
+      if (slot < 0) continue;
+      const f16* src = (kv == 0 ? ap.new_k : ap.new_v) + int64_t(b) * num_kv_heads * D + c * 8;
+      f16* dst = ap.pool + (int64_t(kv) * num_slots + slot) * num_kv_heads * D + c * 8;
+      *reinterpret_cast<u32x4*>(dst) = ld16(src);
+    }
+  }
 
   // 1. Exclusive prefix of pages per row, in LDS (every workgroup builds its own copy).
   int running = 0;
@@ -238,6 +275,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     if (i < batch) {
       const int len = row_len(i);
       s_len[i] = len;
+      if constexpr (kAppend) s_slot[i] = append_slot(i);
       pages = len > 0 ? (len + kBlock - 1) / kBlock : 0;
       if (uses_prefix(len)) pages -= px.pages;  // cascade: only the pages after the prefix
     }
@@ -314,6 +352,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     int pend_n = 0, pend_seg0 = 0, pend_seg1 = 0, pend_first0 = 0, pend_first1 = 0, pend_np0 = 0, pend_np1 = 0;
     struct Piece {
       int b, kvh, seg, page0, np, len, poff;  // poff: table entries skipped (shared prefix)
+      int slot;  // fused append: the row's appended slot (-1: none)
       int64_t seg_start, seg_end;
     };
     auto locate = [&](int64_t u) -> Piece {  // unit u -> the piece of this range that starts at u
@@ -334,6 +373,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       P.seg = P.b * num_kv_heads + P.kvh;
       P.len = s_len[P.b];
       P.poff = uses_prefix(P.len) ? px.pages : 0;
+      P.slot = kAppend ? s_slot[P.b] : -1;
       return P;
     };
     // Query rows of a piece and its first two 64-page windows of ids.  The loads are
@@ -354,9 +394,25 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     auto head_of = [&](const Piece& P) {
       return pool + int64_t(P.kvh) * D + int64_t(row) * tok_stride + col * 8;
     };
-    auto issue = [&](const f16* hb, int phys, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool& ok) {
+    auto issue = [&](const Piece& P, const f16* hb, int phys, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool& ok) {
       ok = phys >= 0 && int64_t(phys) < num_pages;
       const f16* base = hb + int64_t(ok ? phys : 0) * page_elems;
+      if constexpr (kAppend) {
+        if (P.slot >= 0 && phys == P.slot / kBlock) {  // the page of the appended token (uniform)
+          const int tok = P.slot % kBlock;
+          const int64_t src = (int64_t(P.b) * num_kv_heads + P.kvh) * D + col * 8;
+#pragma unroll
+          for (int tt = 0; tt < 2; ++tt) {
+            const bool mine = row + 8 * tt == tok;  // this lane's token is the appended one
+#pragma unroll
+            for (int ch = 0; ch < NC; ++ch) {
+              kr[tt][ch] = ld16(mine ? ap.new_k + src + ch * 64 : base + tt * 8 * tok_stride + ch * 64);
+              vr[tt][ch] = ld16(mine ? ap.new_v + src + ch * 64 : base + v_off + tt * 8 * tok_stride + ch * 64);
+            }
+          }
+          return;
+        }
+      }
 #pragma unroll
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -379,7 +435,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     f16x8 qn[kPrefetchQ ? G : 1][NC];
     fetch_q(cur, qv);
     fetch_ids(cur, ids0, ids1);
-    issue(head_of(cur), __builtin_amdgcn_readlane(ids0, 0), kb[0], vb[0], okb[0]);
+    issue(cur, head_of(cur), __builtin_amdgcn_readlane(ids0, 0), kb[0], vb[0], okb[0]);
     for (int64_t u = u_lo;;) {  // one piece per iteration (uniform loop)
       const int np = cur.np, page0 = cur.page0, len = cur.len, seg = cur.seg, poff = cur.poff;
       const int64_t seg_start = cur.seg_start, seg_end = cur.seg_end;
@@ -405,9 +461,9 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       // page k of the piece; k == np is the next piece's first page
       auto load_page = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool& ok) {
         if (k < np)
-          issue(head_base, page_id(k), kr, vr, ok);
+          issue(cur, head_base, page_id(k), kr, vr, ok);
         else if (has_next)
-          issue(head_next, __builtin_amdgcn_readlane(nid0, 0), kr, vr, ok);
+          issue(nxt, head_next, __builtin_amdgcn_readlane(nid0, 0), kr, vr, ok);
       };
       auto consume = [&](int k, u32x4 (&kr)[2][NC], u32x4 (&vr)[2][NC], bool ok) {
         const int p = poff + page0 + k;  // page of the row
@@ -473,7 +529,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       if (k < np) {  // odd page count: the last page sits in slot 0
         shift(k);
         consume(k, kb[0], vb[0], okb[0]);
-        if (has_next) issue(head_next, __builtin_amdgcn_readlane(nid0, 0), kb[0], vb[0], okb[0]);
+        if (has_next) issue(nxt, head_next, __builtin_amdgcn_readlane(nid0, 0), kb[0], vb[0], okb[0]);
       }
       if constexpr (!kPrefetchQ) {
         if (has_next) fetch_q(nxt, qv);
@@ -597,7 +653,7 @@ __global__ __launch_bounds__(kWave) void cascade_combine_kernel(
 
 typedef void (*DecodeKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t,
                              const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, float,
-                             DecodeWorkspace, DecodePrefix);
+                             DecodeWorkspace, DecodePrefix, DecodeAppend);
 typedef void (*CombineKernel)(f16*, const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, DecodePrefix);
 
 static CombineKernel pick_combine(int d, int g) {
@@ -609,18 +665,26 @@ static CombineKernel pick_combine(int d, int g) {
   return nullptr;
 }
 
-static DecodeKernel pick_decode(int d, int g, bool cascade = false) {
+enum class DecodeMode { kPlain, kCascade, kAppend };
+
+static DecodeKernel pick_decode(int d, int g, DecodeMode mode = DecodeMode::kPlain) {
 #define IFN_DECODE_CASE(DD, GG) \
-  if (d == DD && g == GG && !cascade) return paged_decode_kernel<DD, GG, false>;
+  if (d == DD && g == GG && mode == DecodeMode::kPlain) return paged_decode_kernel<DD, GG, false, false>;
 #define IFN_CASCADE_CASE(DD, GG) \
-  if (d == DD && g == GG && cascade) return paged_decode_kernel<DD, GG, true>;
+  if (d == DD && g == GG && mode == DecodeMode::kCascade) return paged_decode_kernel<DD, GG, true, false>;
+#define IFN_APPEND_CASE(DD, GG) \
+  if (d == DD && g == GG && mode == DecodeMode::kAppend) return paged_decode_kernel<DD, GG, false, true>;
   IFN_DECODE_CASE(64, 1) IFN_DECODE_CASE(64, 2) IFN_DECODE_CASE(64, 4) IFN_DECODE_CASE(64, 8)
   IFN_DECODE_CASE(128, 1) IFN_DECODE_CASE(128, 2) IFN_DECODE_CASE(128, 4) IFN_DECODE_CASE(128, 8)
   IFN_DECODE_CASE(256, 1) IFN_DECODE_CASE(256, 2) IFN_DECODE_CASE(256, 4)
   IFN_CASCADE_CASE(64, 1) IFN_CASCADE_CASE(64, 2) IFN_CASCADE_CASE(64, 4) IFN_CASCADE_CASE(64, 8)
   IFN_CASCADE_CASE(128, 1) IFN_CASCADE_CASE(128, 2) IFN_CASCADE_CASE(128, 4) IFN_CASCADE_CASE(128, 8)
+  IFN_APPEND_CASE(64, 1) IFN_APPEND_CASE(64, 2) IFN_APPEND_CASE(64, 4) IFN_APPEND_CASE(64, 8)
+  IFN_APPEND_CASE(128, 1) IFN_APPEND_CASE(128, 2) IFN_APPEND_CASE(128, 4) IFN_APPEND_CASE(128, 8)
+  IFN_APPEND_CASE(256, 1) IFN_APPEND_CASE(256, 2) IFN_APPEND_CASE(256, 4)
 #undef IFN_DECODE_CASE
 #undef IFN_CASCADE_CASE
+#undef IFN_APPEND_CASE
   return nullptr;
 }
 
@@ -637,27 +701,35 @@ extern "C" size_t ifn_paged_decode_workspace_bytes(int32_t batch, int32_t num_q_
                                int64_t(ifn::decode_blocks()) * ifn::kWavesPerBlock, &off_ml, &off_o);
 }
 
-extern "C" int ifn_paged_decode(void* out, const void* query, const void* kv_pool_layer,
-                                int64_t num_pages, const int32_t* block_tables,
-                                int32_t max_pages_per_seq, const int32_t* seq_lens,
-                                const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
-                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                int32_t max_seq_len, float scale, void* workspace,
-                                size_t workspace_bytes, void* stream) {
-  using namespace ifn;
+namespace ifn {
+
+// ifn_paged_decode and ifn_paged_decode_append: the same checks and launch; `ap` carries the
+// fused append (kAppend variant) when its pointers are given.
+static int decode_entry(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                        const int32_t* block_tables, int32_t max_pages_per_seq, const int32_t* seq_lens,
+                        const uint8_t* active_mask, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
+                        size_t workspace_bytes, void* stream, const DecodeAppend& ap) {
+  const bool append = ap.pool != nullptr;
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_tables == nullptr ||
       seq_lens == nullptr)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (append && (ap.new_k == nullptr || ap.new_v == nullptr || ap.slots == nullptr))
     return IFN_ERR_INVALID_ARGUMENT;
   if (batch < 0 || num_pages < 1 || max_pages_per_seq < 1 || num_q_heads < 1 ||
       num_kv_heads < 1 || head_dim < 1 || max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
     return IFN_ERR_INVALID_ARGUMENT;
   if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
-  DecodeKernel k = pick_decode(head_dim, num_q_heads / num_kv_heads);
+  DecodeKernel k = pick_decode(head_dim, num_q_heads / num_kv_heads, append ? DecodeMode::kAppend : DecodeMode::kPlain);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);
+  if (append) {
+    IFN_CHECK_ALIGN16(ap.new_k);
+    IFN_CHECK_ALIGN16(ap.new_v);
+  }
   if (batch == 0) return IFN_OK;
   const int blocks = decode_blocks();
   size_t off_ml, off_o;
@@ -675,8 +747,38 @@ extern "C" int ifn_paged_decode(void* out, const void* query, const void* kv_poo
   k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
-      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws, DecodePrefix{nullptr, nullptr, 0, 0});
+      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws, DecodePrefix{nullptr, nullptr, 0, 0},
+      ap);
   return ifn_launch_status();
+}
+
+}  // namespace ifn
+
+extern "C" int ifn_paged_decode(void* out, const void* query, const void* kv_pool_layer,
+                                int64_t num_pages, const int32_t* block_tables,
+                                int32_t max_pages_per_seq, const int32_t* seq_lens,
+                                const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
+                                int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                int32_t max_seq_len, float scale, void* workspace,
+                                size_t workspace_bytes, void* stream) {
+  return ifn::decode_entry(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                           active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
+                           workspace, workspace_bytes, stream, ifn::DecodeAppend{nullptr, nullptr, nullptr, nullptr});
+}
+
+extern "C" int ifn_paged_decode_append(void* out, const void* query, void* kv_pool_layer, int64_t num_pages,
+                                       const int32_t* block_tables, int32_t max_pages_per_seq,
+                                       const int32_t* seq_lens, const uint8_t* active_mask,
+                                       const int32_t* slot_mapping, const void* new_k, const void* new_v,
+                                       int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                       int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
+                                       size_t workspace_bytes, void* stream) {
+  if (kv_pool_layer == nullptr) return IFN_ERR_INVALID_ARGUMENT;
+  return ifn::decode_entry(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                           active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
+                           workspace, workspace_bytes, stream,
+                           ifn::DecodeAppend{static_cast<const ifn::f16*>(new_k), static_cast<const ifn::f16*>(new_v),
+                                             slot_mapping, static_cast<ifn::f16*>(kv_pool_layer)});
 }
 
 namespace ifn {
@@ -743,7 +845,7 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
   const int g = num_q_heads / num_kv_heads;
-  DecodeKernel k = pick_decode(head_dim, g, true);
+  DecodeKernel k = pick_decode(head_dim, g, DecodeMode::kCascade);
   CombineKernel kc = pick_combine(head_dim, g);
   if (k == nullptr || kc == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
@@ -776,7 +878,7 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, s>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
       block_tables, max_pages_per_seq, seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws,
-      px);
+      px, DecodeAppend{nullptr, nullptr, nullptr, nullptr});
   rc = ifn_launch_status();
   if (rc != IFN_OK) return rc;
   // 3. merge the states of every cascade segment into the output

@@ -27,7 +27,7 @@ import torch
 from .. import _capi
 from ._common import PagedAttentionError, check_pool, current_stream, ptr
 
-__all__ = ["paged_attention", "PagedAttentionError", "workspace_for"]
+__all__ = ["paged_attention", "store_kv_and_decode", "PagedAttentionError", "workspace_for"]
 
 # One zero-initialised workspace per (device, stream): every kernel call leaves
 # the workspace's ticket counters at zero, so the buffer is reused as is.
@@ -174,3 +174,66 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
     _capi.call("ifn_paged_prefill", ptr(out), ptr(query), ptr(pool_layer), P, ptr(table), max_pages,
                query_start, n, hq, hkv, d, bs, float(scale), ptr(ws), ws.numel(), stream)
     return out
+
+
+def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: torch.Tensor,
+                        sequence_lengths: torch.Tensor, active_mask: torch.Tensor | None,
+                        slot_mapping: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor, *, layer: int = 0,
+                        scale: float | None = None, out: torch.Tensor | None = None, block_size: int = 16,
+                        max_seq_len: int | None = None) -> torch.Tensor:
+    """One decode step's append and attention in one launch (``ifn_paged_decode_append``).
+
+    Same result, in ``out`` and in the pool, as ``store_kv(kv_pool, slot_mapping, active_mask,
+    new_k, new_v, layer=layer)`` followed by ``paged_attention(query, kv_pool, block_tables,
+    sequence_lengths, active_mask, layer=layer, ...)`` -- the store of model.py:191-196 and the
+    attention of :196-200.  ``new_k``/``new_v`` are fp16 [B, Hkv, D], ``slot_mapping`` int32 [B].
+    An appended slot must not be read by another row of the call (true of any paged KV state).
+    """
+    from .kv_store import _check_index, _check_rows
+    if slot_mapping is None:
+        raise PagedAttentionError("store_kv_and_decode needs a slot_mapping")
+    pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
+    dev = pool_layer.device
+    if bs != block_size:
+        raise PagedAttentionError(f"kv_pool block_size {bs} != block_size argument {block_size}")
+    if not isinstance(query, torch.Tensor) or query.ndim != 3:
+        raise PagedAttentionError("query must be a rank-3 [B, Hq, D] tensor")
+    n, hq, qd = query.shape
+    if qd != d or hq % hkv != 0:
+        raise PagedAttentionError(f"query [B, {hq}, {qd}] does not match kv heads {hkv} x {d}")
+    _check("query", query, (n, hq, d), (torch.float16,), dev)
+    if not isinstance(block_tables, torch.Tensor) or block_tables.ndim != 2:
+        raise PagedAttentionError("block_tables must be a rank-2 [B, max_pages] int32 tensor")
+    max_pages = block_tables.shape[1]
+    _check("block_tables", block_tables, (n, max_pages), (torch.int32,), dev)
+    _check("sequence_lengths", sequence_lengths, (n,), (torch.int32,), dev)
+    if active_mask is not None:
+        _check("active_mask", active_mask, (n,), (torch.bool, torch.uint8), dev)
+    _check_rows("new_k", new_k, (n,), hkv, d, dev)
+    _check_rows("new_v", new_v, (n,), hkv, d, dev)
+    sm = _check_index("slot_mapping", slot_mapping, n, dev, (torch.int32,))
+    if max_pages < 1:
+        raise PagedAttentionError("block_tables must have at least one column")
+    if out is None:
+        out = torch.zeros_like(query) if active_mask is not None else torch.empty_like(query)
+    else:
+        _check("out", out, (n, hq, d), (torch.float16,), dev)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if not scale > 0:
+        raise PagedAttentionError(f"scale must be positive, got {scale}")
+    cap = max_pages * bs
+    msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
+    if msl < 0:
+        raise PagedAttentionError("max_seq_len must be non-negative")
+    if n == 0:
+        return out
+    stream = current_stream(dev)
+    lib = _capi.lib()
+    nbytes = lib.ifn_paged_decode_workspace_bytes(n, hq, hkv, d, bs, msl)
+    ws = workspace_for(dev, stream, nbytes)
+    _capi.call("ifn_paged_decode_append", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables), max_pages,
+               ptr(sequence_lengths), ptr(active_mask), ptr(sm), ptr(new_k), ptr(new_v), n, hq, hkv, d, bs, msl,
+               float(scale), ptr(ws), ws.numel(), stream)
+    return out
+

@@ -80,6 +80,26 @@ def test_paged_decode_host_validation():
     assert call(B=21504) == _capi.IFN_ERR_UNSUPPORTED  # batch beyond the LDS prefix table
 
 
+def test_fused_append_decode_host_validation():
+    L = _capi.lib()
+    base = dict(out=A, q=A, pool=A, P=1024, bt=A, W=256, sl=A, am=None, sm=A, nk=A, nv=A, B=32, hq=16, hkv=8,
+                d=128, bs=16, msl=4096, scale=0.0, ws=None, wsb=0)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return L.ifn_paged_decode_append(a["out"], a["q"], a["pool"], a["P"], a["bt"], a["W"], a["sl"], a["am"],
+                                         a["sm"], a["nk"], a["nv"], a["B"], a["hq"], a["hkv"], a["d"], a["bs"],
+                                         a["msl"], a["scale"], a["ws"], a["wsb"], None)
+
+    assert call(sm=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(nk=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(pool=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(nv=A + 8) == _capi.IFN_ERR_ALIGNMENT
+    assert call(hq=24) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(B=0) == _capi.IFN_OK
+    assert call() == _capi.IFN_ERR_WORKSPACE  # the same workspace rule as ifn_paged_decode
+
+
 def test_shared_prefix_decode_host_validation():
     L = _capi.lib()
     base = dict(out=A, q=A, pool=A, P=1024, pp=A, S=8, bt=A, W=256, sl=A, am=None, B=32, hq=32, hkv=8, d=128,
