@@ -148,26 +148,52 @@ def run_prefill(lib, hip, dev, g, stream) -> dict:
         j = 0
         for layer in range(L):
             for c in range(4):
+                if evs is not None:
+                    hip.hip.hipEventRecord(evs[3 * j], stream)
                 rc = lib.ifn_store_kv(pool.data_ptr() + layer * lb, w.num_pages, slots.data_ptr() + 4 * c * C, None,
                                       k[layer, c].data_ptr(), v[layer, c].data_ptr(), C, hkv, d, 16, stream)
                 if evs is not None:
-                    hip.hip.hipEventRecord(evs[2 * j], stream)
+                    hip.hip.hipEventRecord(evs[3 * j + 1], stream)
                 rc |= lib.ifn_paged_prefill(out.data_ptr(), q[layer, c].data_ptr(), pool.data_ptr() + layer * lb,
                                             w.num_pages, table.data_ptr(), w.block_table.shape[0], c * C, C, hq, hkv,
                                             d, 16, scale, ws.data_ptr(), ws_bytes, stream)
                 if evs is not None:
-                    hip.hip.hipEventRecord(evs[2 * j + 1], stream)
+                    hip.hip.hipEventRecord(evs[3 * j + 2], stream)
                 if rc:
                     raise RuntimeError(f"prefill launch failed: {rc}")
                 j += 1
 
+    def fused_pass(evs=None):  # ifn_paged_prefill_append: the store and the attention in one launch
+        j = 0
+        for layer in range(L):
+            for c in range(4):
+                if evs is not None:
+                    hip.hip.hipEventRecord(evs[2 * j], stream)
+                rc = lib.ifn_paged_prefill_append(out.data_ptr(), q[layer, c].data_ptr(), pool.data_ptr() + layer * lb,
+                                                  w.num_pages, table.data_ptr(), w.block_table.shape[0], c * C, C,
+                                                  k[layer, c].data_ptr(), v[layer, c].data_ptr(), hq, hkv, d, 16,
+                                                  scale, ws.data_ptr(), ws_bytes, stream)
+                if evs is not None:
+                    hip.hip.hipEventRecord(evs[2 * j + 1], stream)
+                if rc:
+                    raise RuntimeError(f"fused prefill launch failed: {rc}")
+                j += 1
+
     one_pass()
     torch.cuda.synchronize()
-    evs = hip.create(2 * L * 4)
+    evs = hip.create(3 * L * 4)
     one_pass(evs)
     torch.cuda.synchronize()
-    ms = np.asarray([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(L * 4)]).reshape(L, 4)
+    ms = np.asarray([hip.elapsed_ms(evs[3 * j + 1], evs[3 * j + 2]) for j in range(L * 4)]).reshape(L, 4)
+    st_ms = np.asarray([hip.elapsed_ms(evs[3 * j], evs[3 * j + 1]) for j in range(L * 4)]).reshape(L, 4)
     hip.destroy(evs)
+    fused_pass()
+    torch.cuda.synchronize()
+    fevs = hip.create(2 * L * 4)
+    fused_pass(fevs)
+    torch.cuda.synchronize()
+    fms = np.asarray([hip.elapsed_ms(fevs[2 * j], fevs[2 * j + 1]) for j in range(L * 4)]).reshape(L, 4)
+    hip.destroy(fevs)
     flops = np.asarray([w.chunk_flops(c) for c in range(4)], np.float64)
     per_chunk_us = ms.mean(0) * 1e3
     tflops = float(flops.sum() * L / (ms.sum() / 1e3) / 1e12)
@@ -176,7 +202,11 @@ def run_prefill(lib, hip, dev, g, stream) -> dict:
             "attn_us_per_layer": round(float(ms.sum(1).mean() * 1e3), 2),
             "gflop_per_layer": round(float(flops.sum() / 1e9), 3),
             "TFLOP/s": round(tflops, 2), "mfma_peak_TFLOP/s": MFMA_F16_PEAK_TFLOPS,
-            "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4)}
+            "frac": round(tflops / MFMA_F16_PEAK_TFLOPS, 4),
+            "store_us_per_chunk_layer": round(float(st_ms.mean() * 1e3), 2),
+            "fused_us_per_chunk_layer": [round(float(x), 2) for x in fms.mean(0) * 1e3],
+            "fused_us_per_layer": round(float(fms.sum(1).mean() * 1e3), 2),
+            "two_launch_us_per_layer": round(float((ms + st_ms).sum(1).mean() * 1e3), 2)}
 
 
 def run_pre_append(lib, hip, dev, g, stream) -> dict:

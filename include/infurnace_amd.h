@@ -175,6 +175,26 @@ int ifn_paged_decode_shared_prefix(void* out, const void* query, const void* kv_
                                    int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
                                    size_t workspace_bytes, void* stream);
 
+/*
+ * One prefill chunk's append and causal attention: the result (output and
+ * pool) equals storing new_k / new_v ([num_q_tokens][num_kv_heads][head_dim]
+ * fp16) at slot block_table[p / 16] * 16 + p % 16 for p = query_start + t
+ * (skipped where that page id is outside the pool, as ifn_store_kv skips
+ * such slots), then ifn_paged_prefill(...) on the same stream.  With
+ * query_start % 32 == 0 this is one launch in which the attention takes the
+ * chunk's keys from new_k / new_v; otherwise the store and the attention are
+ * two launches.  Same workspace as ifn_paged_prefill.
+ * Replaces: store_kv then paged_attention of one prefill chunk
+ * (docs/architecture.md:245-246; contiguous form
+ * src/infurnace/executor/tinygrad/model.py:116-138).
+ */
+int ifn_paged_prefill_append(void* out, const void* query, void* kv_pool_layer, int64_t num_pages,
+                             const int32_t* block_table, int32_t max_pages, int32_t query_start,
+                             int32_t num_q_tokens, const void* new_k, const void* new_v,
+                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t block_size, float scale, void* workspace, size_t workspace_bytes,
+                             void* stream);
+
 /* Workspace bytes ifn_paged_prefill needs for these shapes. */
 size_t ifn_paged_prefill_workspace_bytes(int32_t num_q_tokens, int32_t query_start,
                                          int32_t num_q_heads, int32_t num_kv_heads,

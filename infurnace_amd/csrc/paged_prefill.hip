@@ -60,6 +60,49 @@ struct PrefixOut {
   int32_t stride;
 };
 
+// Fused append (kAppend variant): the chunk's new_k / new_v [T][Hkv][D] are stored into the pool at
+// the table's slots for positions query_start .. query_start + T - 1, and the attention takes the
+// chunk's keys and values from new_k / new_v, so the stores need no ordering against the reads.
+// Requires query_start % 32 == 0 (a key tile is then wholly before the chunk or wholly in it)
+// and T * Hkv * D * 2 < 2^31 bytes (one buffer resource).
+struct PrefillAppend {
+  const f16* new_k;
+  const f16* new_v;
+  f16* pool;  // the layer's pool (the memory the kernel reads)
+};
+
+// The chunk's K and V rows -> the pool at table[pos / 16] * 16 + pos % 16, pos = query_start + t:
+// 16-byte chunks, item it of `items` per thread in a grid-stride loop.  Rows whose page id is
+// outside the pool are skipped (store_kv skips slots outside the pool).
+__device__ __forceinline__ void store_chunk_rows(f16* __restrict__ pool, int64_t num_pages,
+                                                 const int32_t* __restrict__ table, int32_t query_start, int32_t T,
+                                                 int32_t hkv, int32_t d, const f16* __restrict__ new_k,
+                                                 const f16* __restrict__ new_v, int64_t first, int64_t step) {
+  const int chunks = hkv * d / 8;
+  const int64_t tok_stride = int64_t(hkv) * d;
+  const int64_t items = int64_t(T) * 2 * chunks;
+  for (int64_t it = first; it < items; it += step) {
+    const int t = int(it / (2 * chunks));
+    const int rem = int(it % (2 * chunks));
+    const int kv = rem / chunks, c = rem % chunks;
+    const int pos = query_start + t;
+    const int page = table[pos / kPBlock];
+    if (page < 0 || int64_t(page) >= num_pages) continue;
+    const f16* src = (kv == 0 ? new_k : new_v) + int64_t(t) * tok_stride + c * 8;
+    f16* dst = pool + (int64_t(kv) * num_pages * kPBlock + int64_t(page) * kPBlock + pos % kPBlock) * tok_stride + c * 8;
+    *reinterpret_cast<u32x4*>(dst) = ld16(src);
+  }
+}
+
+// The store alone, for chunks the fused kernel does not take (query_start % 32 != 0).
+__global__ __launch_bounds__(256) void store_chunk_kernel(f16* __restrict__ pool, int64_t num_pages,
+                                                          const int32_t* __restrict__ table, int32_t query_start,
+                                                          int32_t T, int32_t hkv, int32_t d,
+                                                          const f16* __restrict__ new_k, const f16* __restrict__ new_v) {
+  store_chunk_rows(pool, num_pages, table, query_start, T, hkv, d, new_k, new_v,
+                   int64_t(blockIdx.x) * blockDim.x + threadIdx.x, int64_t(gridDim.x) * blockDim.x);
+}
+
 struct PrefillPlan {
   int64_t n_qb;
   int nsplit;
@@ -111,11 +154,12 @@ struct PrefillCfg {
   static constexpr int kVPer = (kVItems + kGroupThreads - 1) / kGroupThreads;
 };
 
-template <int D, int G>
+template <int D, int G, bool kAppend>
 __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
     int64_t num_pages, const int32_t* __restrict__ table, int32_t query_start, int32_t T,
-    int32_t num_kv_heads, int32_t n_qb, int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefixOut px) {
+    int32_t num_kv_heads, int32_t n_qb, int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefixOut px,
+    PrefillAppend ap) {
   using C = PrefillCfg<D, G>;
   constexpr int kDT = C::kDT;
   constexpr int kKSteps = D / 16;
@@ -171,6 +215,12 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   const int64_t tok_stride = int64_t(num_kv_heads) * D;
   const int64_t v_off = num_pages * kPBlock * tok_stride;
   const f16* head_pool = pool + int64_t(kvh) * D;
+
+  // Fused append: 16-byte chunks of the chunk's K and V rows, spread over the grid, stored at
+  // table[pos / 16] * 16 + pos % 16 (skipped when that page id is outside the pool).
+  if constexpr (kAppend)
+    store_chunk_rows(ap.pool, num_pages, table, query_start, T, num_kv_heads, D, ap.new_k, ap.new_v,
+                     int64_t(blockIdx.x) * C::kThreads + tid, int64_t(gridDim.x) * C::kThreads);
   // Page ids: a tile of 32 keys spans exactly two pages.  Lane l of every wave of the group
   // holds page 2*tile + (l & 1) of the group's (l / 2)-th upcoming tile, 32 tiles per window,
   // so a tile's two ids are uniform v_readlane reads -- no dependent table load per tile.
@@ -225,6 +275,11 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     return oka | (okb << 1) | (full << 2);
   };
 
+  // Fused append: buffer resources over the chunk's rows (num_records = T rows; gfx9 format word).
+  const int rsrc_bytes = kAppend ? T * int(tok_stride) * 2 : 0;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_k), 0, rsrc_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_v), 0, rsrc_bytes, 0x00020000);
+
   struct Stage {
     u32x4 k[C::kKPer];
     u32x4 v[C::kVPer][4];
@@ -238,6 +293,28 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     st.flags = tile_flags(i, pa, pb);
     const f16* base_a = head_pool + int64_t((st.flags & 1) ? pa : 0) * page_elems;
     const f16* base_b = head_pool + int64_t((st.flags & 2) ? pb : 0) * page_elems;
+    if constexpr (kAppend) {
+      const int kt = tile_of(i) * kPT;
+      if (kt >= query_start) {  // (uniform; query_start % 32 == 0) every key of the tile is a chunk key
+        // Buffer loads from new_k / new_v: rows past the chunk's end fall outside the resource and
+        // read as zero (their keys are masked), so no address is ever out of bounds.  The whole
+        // byte offset goes in the per-lane operand, which is the one the range check covers.
+        const int so = (int(kt - query_start) * int(tok_stride) + kvh * D) * 2;  // bytes, uniform
+#pragma unroll
+        for (int it = 0; it < C::kKPer; ++it) {
+          const int vo = (k_goff[it] + (k_hi[it] ? kPBlock * int(tok_stride) : 0)) * 2;
+          st.k[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, so + vo, 0, 0));
+        }
+#pragma unroll
+        for (int it = 0; it < C::kVPer; ++it)
+#pragma unroll
+          for (int rr = 0; rr < 4; ++rr) {
+            const int vo = (v_goff[it] + rr * int(tok_stride) + (v_hi[it] ? kPBlock * int(tok_stride) : 0)) * 2;
+            st.v[it][rr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, so + vo, 0, 0));
+          }
+        return;
+      }
+    }
 #pragma unroll
     for (int it = 0; it < C::kKPer; ++it) st.k[it] = ld16((k_hi[it] ? base_b : base_a) + k_goff[it]);
 #pragma unroll
@@ -491,13 +568,13 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 }
 
 typedef void (*PrefillKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t,
-                              int32_t, int32_t, int32_t, float, PrefillWorkspace, PrefixOut);
+                              int32_t, int32_t, int32_t, float, PrefillWorkspace, PrefixOut, PrefillAppend);
 
-static PrefillKernel pick_prefill(int d, int g, int* threads) {
-#define IFN_PREFILL_CASE(DD, GG)                          \
-  if (d == DD && g == GG) {                               \
-    *threads = PrefillCfg<DD, GG>::kThreads;              \
-    return paged_prefill_kernel<DD, GG>;                  \
+static PrefillKernel pick_prefill(int d, int g, int* threads, bool append = false) {
+#define IFN_PREFILL_CASE(DD, GG)                                                               \
+  if (d == DD && g == GG) {                                                                    \
+    *threads = PrefillCfg<DD, GG>::kThreads;                                                   \
+    return append ? paged_prefill_kernel<DD, GG, true> : paged_prefill_kernel<DD, GG, false>;  \
   }
   IFN_PREFILL_CASE(64, 1) IFN_PREFILL_CASE(64, 2) IFN_PREFILL_CASE(64, 4) IFN_PREFILL_CASE(64, 8)
   IFN_PREFILL_CASE(128, 1) IFN_PREFILL_CASE(128, 2) IFN_PREFILL_CASE(128, 4) IFN_PREFILL_CASE(128, 8)
@@ -519,7 +596,8 @@ int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t*
   if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31 || stride < p.nsplit) return IFN_ERR_UNSUPPORTED;
   k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), unsigned(threads), 0, stream>>>(
       nullptr, q, pool, num_pages, prefix_pages, 0, batch, hkv, int(p.n_qb), p.nsplit, scale_log2,
-      PrefillWorkspace{nullptr, nullptr, nullptr}, PrefixOut{px_ml, px_o, key_len, stride});
+      PrefillWorkspace{nullptr, nullptr, nullptr}, PrefixOut{px_ml, px_o, key_len, stride},
+      PrefillAppend{nullptr, nullptr, nullptr});
   return ifn_launch_status();
 }
 
@@ -538,30 +616,48 @@ extern "C" size_t ifn_paged_prefill_workspace_bytes(int32_t num_q_tokens, int32_
   return ifn::plan_prefill(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim, cus).bytes;
 }
 
-extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_pool_layer,
-                                 int64_t num_pages, const int32_t* block_table, int32_t max_pages,
-                                 int32_t query_start, int32_t num_q_tokens, int32_t num_q_heads,
-                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                 float scale, void* workspace, size_t workspace_bytes,
-                                 void* stream) {
-  using namespace ifn;
+namespace ifn {
+
+static int prefill_entry(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                         const int32_t* block_table, int32_t max_pages, int32_t query_start, int32_t num_q_tokens,
+                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float scale,
+                         void* workspace, size_t workspace_bytes, void* stream, PrefillAppend ap) {
+  bool append = ap.pool != nullptr;
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_table == nullptr)
     return IFN_ERR_INVALID_ARGUMENT;
+  if (append && (ap.new_k == nullptr || ap.new_v == nullptr)) return IFN_ERR_INVALID_ARGUMENT;
   if (num_pages < 1 || max_pages < 1 || query_start < 0 || num_q_tokens < 0 || num_q_heads < 1 ||
       num_kv_heads < 1 || head_dim < 1 || num_q_heads % num_kv_heads != 0)
     return IFN_ERR_INVALID_ARGUMENT;
   if (block_size != kPBlock) return IFN_ERR_UNSUPPORTED;
   int threads = 0;
-  PrefillKernel k = pick_prefill(head_dim, num_q_heads / num_kv_heads, &threads);
+  PrefillKernel k = pick_prefill(head_dim, num_q_heads / num_kv_heads, &threads, append);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);
+  if (append) {
+    IFN_CHECK_ALIGN16(ap.new_k);
+    IFN_CHECK_ALIGN16(ap.new_v);
+  }
   if (num_q_tokens == 0) return IFN_OK;
   if (int64_t(query_start) + num_q_tokens > int64_t(max_pages) * kPBlock)
     return IFN_ERR_INVALID_ARGUMENT;  // keys past the end of the block table
   const int cus = device_cu_count();
   if (cus < 1) return IFN_ERR_HIP;
+  if (append && (query_start % 32 != 0 ||
+                 int64_t(num_q_tokens) * num_kv_heads * head_dim * 2 >= (int64_t(1) << 31))) {
+    // not fusable: the store as its own launch, then the plain attention (same result)
+    const int64_t items = int64_t(num_q_tokens) * 2 * num_kv_heads * head_dim / 8;
+    const int64_t grid = std::min<int64_t>((items + 255) / 256, int64_t(cus) * 16);
+    store_chunk_kernel<<<dim3(unsigned(grid)), dim3(256), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+        ap.pool, num_pages, block_table, query_start, num_q_tokens, num_kv_heads, head_dim, ap.new_k, ap.new_v);
+    const int rc = ifn_launch_status();
+    if (rc != IFN_OK) return rc;
+    append = false;
+    ap = PrefillAppend{nullptr, nullptr, nullptr};
+    k = pick_prefill(head_dim, num_q_heads / num_kv_heads, &threads, false);
+  }
   const PrefillPlan p = plan_prefill(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim, cus);
   if (p.n_qb * num_kv_heads * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
   PrefillWorkspace ws{nullptr, nullptr, nullptr};
@@ -578,6 +674,32 @@ extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_po
       reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_table, query_start, num_q_tokens,
-      num_kv_heads, int(p.n_qb), p.nsplit, scale * kLog2e, ws, PrefixOut{nullptr, nullptr, 0, 0});
+      num_kv_heads, int(p.n_qb), p.nsplit, scale * kLog2e, ws, PrefixOut{nullptr, nullptr, 0, 0}, ap);
   return ifn_launch_status();
+}
+
+}  // namespace ifn
+
+extern "C" int ifn_paged_prefill(void* out, const void* query, const void* kv_pool_layer,
+                                 int64_t num_pages, const int32_t* block_table, int32_t max_pages,
+                                 int32_t query_start, int32_t num_q_tokens, int32_t num_q_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                 float scale, void* workspace, size_t workspace_bytes,
+                                 void* stream) {
+  return ifn::prefill_entry(out, query, kv_pool_layer, num_pages, block_table, max_pages, query_start, num_q_tokens,
+                            num_q_heads, num_kv_heads, head_dim, block_size, scale, workspace, workspace_bytes, stream,
+                            ifn::PrefillAppend{nullptr, nullptr, nullptr});
+}
+
+extern "C" int ifn_paged_prefill_append(void* out, const void* query, void* kv_pool_layer, int64_t num_pages,
+                                        const int32_t* block_table, int32_t max_pages, int32_t query_start,
+                                        int32_t num_q_tokens, const void* new_k, const void* new_v,
+                                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t block_size, float scale, void* workspace, size_t workspace_bytes,
+                                        void* stream) {
+  if (kv_pool_layer == nullptr) return IFN_ERR_INVALID_ARGUMENT;
+  return ifn::prefill_entry(out, query, kv_pool_layer, num_pages, block_table, max_pages, query_start, num_q_tokens,
+                            num_q_heads, num_kv_heads, head_dim, block_size, scale, workspace, workspace_bytes, stream,
+                            ifn::PrefillAppend{static_cast<const ifn::f16*>(new_k), static_cast<const ifn::f16*>(new_v),
+                                               static_cast<ifn::f16*>(kv_pool_layer)});
 }

@@ -27,7 +27,8 @@ import torch
 from .. import _capi
 from ._common import PagedAttentionError, check_pool, current_stream, ptr
 
-__all__ = ["paged_attention", "store_kv_and_decode", "PagedAttentionError", "workspace_for"]
+__all__ = ["paged_attention", "store_kv_and_decode", "store_kv_and_prefill", "PagedAttentionError",
+           "workspace_for"]
 
 # One zero-initialised workspace per (device, stream): every kernel call leaves
 # the workspace's ticket counters at zero, so the buffer is reused as is.
@@ -235,5 +236,60 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
     _capi.call("ifn_paged_decode_append", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables), max_pages,
                ptr(sequence_lengths), ptr(active_mask), ptr(sm), ptr(new_k), ptr(new_v), n, hq, hkv, d, bs, msl,
                float(scale), ptr(ws), ws.numel(), stream)
+    return out
+
+
+def store_kv_and_prefill(query: torch.Tensor, kv_pool: torch.Tensor, block_table: torch.Tensor, new_k: torch.Tensor,
+                         new_v: torch.Tensor, *, query_start: int, layer: int = 0, scale: float | None = None,
+                         out: torch.Tensor | None = None, block_size: int = 16) -> torch.Tensor:
+    """One prefill chunk's append and causal attention (``ifn_paged_prefill_append``).
+
+    Same result, in ``out`` and in the pool, as ``store_kv`` of ``new_k``/``new_v`` [T, Hkv, D] at
+    the table's slots for positions query_start .. query_start + T - 1 followed by
+    ``paged_attention(query, ..., query_start=query_start)`` -- the store of model.py:134-138 and
+    the attention of :116-132.  One launch when query_start % 32 == 0, else the store and the
+    attention as two launches.
+    """
+    from .kv_store import _check_rows
+    pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
+    dev = pool_layer.device
+    if bs != block_size:
+        raise PagedAttentionError(f"kv_pool block_size {bs} != block_size argument {block_size}")
+    if not isinstance(query, torch.Tensor) or query.ndim != 3:
+        raise PagedAttentionError("query must be a rank-3 [T, Hq, D] tensor")
+    n, hq, qd = query.shape
+    if qd != d or hq % hkv != 0:
+        raise PagedAttentionError(f"query [T, {hq}, {qd}] does not match kv heads {hkv} x {d}")
+    _check("query", query, (n, hq, d), (torch.float16,), dev)
+    _check_rows("new_k", new_k, (n,), hkv, d, dev)
+    _check_rows("new_v", new_v, (n,), hkv, d, dev)
+    query_start = int(query_start)
+    if query_start < 0:
+        raise PagedAttentionError(f"query_start must be non-negative, got {query_start}")
+    if not isinstance(block_table, torch.Tensor):
+        raise PagedAttentionError("block_table must be a torch.Tensor")
+    table = block_table.reshape(-1) if block_table.ndim == 2 and block_table.shape[0] == 1 else block_table
+    if table.ndim != 1:
+        raise PagedAttentionError("block_table must be [max_pages] or [1, max_pages]")
+    max_pages = table.shape[0]
+    _check("block_table", table, (max_pages,), (torch.int32,), dev)
+    if query_start + n > max_pages * bs:
+        raise PagedAttentionError(f"query_start + T = {query_start + n} exceeds the table's {max_pages * bs} slots")
+    if out is None:
+        out = torch.empty_like(query)
+    else:
+        _check("out", out, (n, hq, d), (torch.float16,), dev)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if not scale > 0:
+        raise PagedAttentionError(f"scale must be positive, got {scale}")
+    if n == 0:
+        return out
+    stream = current_stream(dev)
+    lib = _capi.lib()
+    nbytes = lib.ifn_paged_prefill_workspace_bytes(n, query_start, hq, hkv, d, bs)
+    ws = workspace_for(dev, stream, nbytes)
+    _capi.call("ifn_paged_prefill_append", ptr(out), ptr(query), ptr(pool_layer), P, ptr(table), max_pages,
+               query_start, n, ptr(new_k), ptr(new_v), hq, hkv, d, bs, float(scale), ptr(ws), ws.numel(), stream)
     return out
 

@@ -36,7 +36,7 @@ import numpy as np
 import torch
 
 from .cache import BlockPool, KVCacheError, KVManager, PagedKVCache, PrefixCache
-from .kernels import paged_attention, qk_norm_rope_append, store_kv, store_kv_and_decode
+from .kernels import paged_attention, qk_norm_rope_append, store_kv, store_kv_and_decode, store_kv_and_prefill
 
 __all__ = ["PagedKVRunner", "RunnerError"]
 
@@ -62,10 +62,14 @@ class _Step:
                      out: torch.Tensor | None = None) -> torch.Tensor:
         """Append this step's k, v (fp16 [T, Hkv, D]) for ``layer``, then attend with q (fp16 [T, Hq, D]).
 
-        A decode step without a shared prefix does both in one launch (``store_kv_and_decode``).
+        A prefill chunk, and a decode step without a shared prefix, do both in one launch
+        (``store_kv_and_prefill`` / ``store_kv_and_decode``).
         """
         kv = self.runner.cache.kv
-        if self.query_start is None and self.shared_prefix is None:
+        if self.query_start is not None:
+            return store_kv_and_prefill(q, kv, self.block_tables, k, v, query_start=self.query_start, layer=layer,
+                                        out=out)
+        if self.shared_prefix is None:
             return store_kv_and_decode(q, kv, self.block_tables, self.seq_lens, self.active, self.slot_mapping, k, v,
                                        layer=layer, max_seq_len=self.max_len, out=out)
         store_kv(kv, self.slot_mapping, self.active, k, v, layer=layer)

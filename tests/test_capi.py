@@ -100,6 +100,25 @@ def test_fused_append_decode_host_validation():
     assert call() == _capi.IFN_ERR_WORKSPACE  # the same workspace rule as ifn_paged_decode
 
 
+def test_fused_append_prefill_host_validation():
+    L = _capi.lib()
+    base = dict(out=A, q=A, pool=A, P=1024, bt=A, W=256, qs=0, T=512, nk=A, nv=A, hq=16, hkv=8, d=128, bs=16,
+                scale=0.0, ws=None, wsb=0)
+
+    def call(**kw):
+        a = {**base, **kw}
+        return L.ifn_paged_prefill_append(a["out"], a["q"], a["pool"], a["P"], a["bt"], a["W"], a["qs"], a["T"],
+                                          a["nk"], a["nv"], a["hq"], a["hkv"], a["d"], a["bs"], a["scale"], a["ws"],
+                                          a["wsb"], None)
+
+    assert call(nk=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(pool=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(nv=A + 8) == _capi.IFN_ERR_ALIGNMENT
+    assert call(d=256) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(T=0) == _capi.IFN_OK
+    assert call(qs=4000, T=200) == _capi.IFN_ERR_INVALID_ARGUMENT  # keys past the table
+
+
 def test_shared_prefix_decode_host_validation():
     L = _capi.lib()
     base = dict(out=A, q=A, pool=A, P=1024, pp=A, S=8, bt=A, W=256, sl=A, am=None, B=32, hq=32, hkv=8, d=128,

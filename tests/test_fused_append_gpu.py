@@ -13,7 +13,7 @@ import torch
 import oracle
 from gpu_util import assert_attn_close, randn16, say, to_dev
 from infurnace_amd import workloads
-from infurnace_amd.kernels import paged_attention, store_kv, store_kv_and_decode
+from infurnace_amd.kernels import paged_attention, store_kv, store_kv_and_decode, store_kv_and_prefill
 
 pytestmark = pytest.mark.gpu
 
@@ -103,4 +103,80 @@ def test_config2_full_size_28_layer_step(dev):
         o1 = paged_attention(q, pool1, bt, sl, None, layer=layer)
         o2 = store_kv_and_decode(q, pool2, bt, sl, None, slots, nk, nv, layer=layer)
         assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), f"layer {layer}"
+    assert torch.equal(pool1.view(torch.int16), pool2.view(torch.int16))
+
+
+def _prefill_both(dev, pool, table, qs, q, nk, nv):
+    T = q.shape[0]
+    p1, p2 = to_dev(pool, dev), to_dev(pool, dev)
+    tb = to_dev(table, dev)
+    pos = np.arange(qs, qs + T)
+    slots = (table[pos // 16].astype(np.int64) * 16 + pos % 16)
+    slots = np.where((table[pos // 16] >= 0) & (table[pos // 16] < pool.shape[1]), slots, -1).astype(np.int32)
+    qd, kd, vd = to_dev(q, dev), to_dev(nk, dev), to_dev(nv, dev)
+    store_kv(p1, to_dev(slots, dev), None, kd, vd)
+    o1 = paged_attention(qd, p1, tb, None, None, query_start=qs)
+    o2 = store_kv_and_prefill(qd, p2, tb, kd, vd, query_start=qs)
+    return p1, o1, p2, o2, slots
+
+
+@pytest.mark.parametrize("qs,T", [(0, 512), (512, 512), (1536, 512), (0, 37), (64, 100), (96, 200), (2016, 33),
+                                  (16, 50), (40, 90)])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 128), (16, 8, 64)])
+def test_fused_prefill_equals_store_then_prefill(dev, qs, T, hq, hkv, d):
+    """Aligned starts (one launch) and unaligned ones (two launches); chunk ends inside a tile."""
+    say(f"fused prefill qs={qs} T={T} hq={hq} hkv={hkv} d={d}")
+    rng = np.random.default_rng(qs * 7 + T + hq + d)
+    pages = -(-(qs + T) // 16)
+    P = pages + 9
+    table = rng.permutation(P)[:pages].astype(np.int32)
+    pool = rng.standard_normal((2, P, 16, hkv, d), dtype=np.float32).astype(np.float16)
+    f = lambda *s: rng.standard_normal(s, dtype=np.float32).astype(np.float16)
+    q, nk, nv = f(T, hq, d), f(T, hkv, d), f(T, hkv, d)
+    p1, o1, p2, o2, slots = _prefill_both(dev, pool, table, qs, q, nk, nv)
+    assert torch.equal(p1.view(torch.int16), p2.view(torch.int16)), "pool differs from store_kv's"
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), "output differs from the two-launch chunk"
+    exp_pool = pool.copy()
+    oracle.store_kv(exp_pool, slots, None, nk, nv)
+    lens = np.asarray([qs + T], np.int32)
+    assert_attn_close(o2, oracle.paged_attention(q[None], exp_pool, table[None], lens)[0], f"qs={qs} T={T}")
+
+
+def test_fused_prefill_bad_chunk_page(dev):
+    """A chunk page id outside the pool: nothing stored there, its keys contribute nothing -- as
+    store_kv (slot skipped) then prefill (page masked)."""
+    say("fused prefill bad chunk page")
+    rng = np.random.default_rng(51)
+    qs, T, hq, hkv, d = 64, 96, 16, 8, 128
+    pages = (qs + T) // 16
+    P = pages + 4
+    table = rng.permutation(P)[:pages].astype(np.int32)
+    table[6] = P + 100  # a chunk page (keys 96..111)
+    pool = rng.standard_normal((2, P, 16, hkv, d), dtype=np.float32).astype(np.float16)
+    f = lambda *s: rng.standard_normal(s, dtype=np.float32).astype(np.float16)
+    q, nk, nv = f(T, hq, d), f(T, hkv, d), f(T, hkv, d)
+    p1, o1, p2, o2, _ = _prefill_both(dev, pool, table, qs, q, nk, nv)
+    assert torch.equal(p1.view(torch.int16), p2.view(torch.int16))
+    assert torch.equal(o1.view(torch.int16), o2.view(torch.int16))
+
+
+def test_fused_prefill_config3_chunks(dev):
+    """Config 3: four 512-token chunks of a 2048-token prompt, fused, vs the two-launch chunks."""
+    say("fused prefill config3")
+    w = workloads.config3()
+    g = torch.Generator(device=dev).manual_seed(33)
+    pool1 = randn16((2, w.num_pages, 16, 8, 128), g, dev)
+    pool2 = pool1.clone()
+    tb = to_dev(w.block_table, dev)
+    for c in range(4):
+        qs = c * w.chunk
+        q = randn16((w.chunk, 16, 128), g, dev)
+        nk = randn16((w.chunk, 8, 128), g, dev)
+        nv = randn16((w.chunk, 8, 128), g, dev)
+        pos = np.arange(qs, qs + w.chunk)
+        slots = to_dev((w.block_table[pos // 16].astype(np.int64) * 16 + pos % 16).astype(np.int32), dev)
+        store_kv(pool1, slots, None, nk, nv)
+        o1 = paged_attention(q, pool1, tb, None, None, query_start=qs)
+        o2 = store_kv_and_prefill(q, pool2, tb, nk, nv, query_start=qs)
+        assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), f"chunk {c}"
     assert torch.equal(pool1.view(torch.int16), pool2.view(torch.int16))
