@@ -232,23 +232,21 @@ class PagedKVRunner:
         for i in live:
             lens[i] = positions[i] + 1
         act = np.asarray(active, np.uint8)
-        shared = self._common_pages([slots[i] for i in live])
-        return _Step(self, self._dev(sm), self._dev(self._table(slots)), self._dev(lens), self._dev(act),
+        table = self._table(slots)
+        shared = self._common_pages(table[live], lens[live])
+        return _Step(self, self._dev(sm), self._dev(table), self._dev(lens), self._dev(act),
                      self._dev(np.asarray(positions, np.int32)), None, int(lens.max()) if len(lens) else 0,
-                     self._dev(np.asarray(shared, np.int32)) if len(shared) >= self.shared_prefix_min_pages
-                     else None)
+                     self._dev(shared) if len(shared) >= self.shared_prefix_min_pages else None)
 
-    def _common_pages(self, slots: Sequence[int]) -> list[int]:
-        """Leading pages that every listed slot holds at the same positions (at least two slots),
-        limited to pages complete in every slot."""
-        if len(slots) < 2:
-            return []
-        blocks = [self.mgr.blocks(s) for s in slots]
-        limit = min(min(len(b) for b in blocks), min(self.length(s) for s in slots) // self.block_size)
-        n = 0
-        while n < limit and all(b[n] == blocks[0][n] for b in blocks[1:]):
-            n += 1
-        return blocks[0][:n]
+    def _common_pages(self, table: np.ndarray, lens: np.ndarray) -> np.ndarray:
+        """Leading page ids that every row of ``table`` holds at the same columns (at least two
+        rows), limited to pages complete in every row (``lens`` keys)."""
+        if table.shape[0] < 2:
+            return np.zeros(0, np.int32)
+        limit = int(lens.min()) // self.block_size
+        same = (table[:, :limit] == table[0, :limit]).all(axis=0)
+        n = int(np.argmin(same)) if not same.all() else limit
+        return np.ascontiguousarray(table[0, :n], dtype=np.int32)
 
     # -- lifecycle --------------------------------------------------------------------------
 
