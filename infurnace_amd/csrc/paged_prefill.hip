@@ -31,7 +31,8 @@
 //    16 fp32 scores of a 32-key tile are exactly the B operands of two
 //    K = 16 steps once converted to fp16 (the key order inside a step is a
 //    permutation shared by both operands, which a contraction allows).  V is
-//    stored transposed in LDS (Vt[d][key]) so the A operand is two 8-byte reads.
+//    stored as it is in the pool, [key][d], and the A operand (4 keys x 1 dim per
+//    lane, twice) comes from two transposing LDS reads (ds_read_b64_tr_b16).
 //  * K/V rows are gathered page by page through the block table; keys at or
 //    past the end of the sequence or in an invalid page are zero-filled and
 //    masked.
@@ -141,17 +142,17 @@ struct PrefillCfg {
   static constexpr int kThreads = kWaves * kWave;
   static constexpr int kGroupThreads = G * kWave;
   static constexpr int kKS = D + 8;    // K tile row stride (halves)
-  static constexpr int kVS = kPT + 4;  // Vt row stride (halves)
-  static constexpr int kBufHalves = kPT * kKS + D * kVS;  // one (group, buffer): K tile + Vt tile
+  // V row stride (halves): 32 bytes past a multiple of 128 bytes, so the 4 rows one 16-lane group
+  // reads in a transposing load sit on disjoint banks
+  static constexpr int kVS = D + 16;
+  static constexpr int kBufHalves = kPT * kKS + kPT * kVS;  // one (group, buffer): K tile + V tile
   static constexpr int kTileBytes = 2 * kGroups * kBufHalves * 2;
   static constexpr int kDT = D / 32;
   // merge area: (m, l) of every wave, then the accumulators of groups 1.. (lane-contiguous)
   static constexpr int kMergeBytes = kWaves * 32 * 2 * 4 + (kGroups - 1) * G * kDT * 16 * kWave * 4;
   static constexpr int kLdsBytes = kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes;
   static constexpr int kKItems = kPT * (D / 8);        // 16-byte K chunks per tile
-  static constexpr int kVItems = (kPT / 4) * (D / 8);  // 4 keys x 8 dims per V item
   static constexpr int kKPer = (kKItems + kGroupThreads - 1) / kGroupThreads;
-  static constexpr int kVPer = (kVItems + kGroupThreads - 1) / kGroupThreads;
 };
 
 template <int D, int G, bool kAppend>
@@ -242,27 +243,18 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 
   // Per-thread constants of the tile copy: which page half, the element offset inside the page
   // and the LDS offset of each item (the same for every tile).
-  int k_goff[C::kKPer], k_loff[C::kKPer], v_goff[C::kVPer], v_loff[C::kVPer], v_key[C::kVPer];
-  bool k_hi[C::kKPer], v_hi[C::kVPer];
+  // K and V items: 16 bytes (8 dims) of one key row; V uses the K item's row and chunk
+  int k_goff[C::kKPer], k_loff[C::kKPer], v_loff[C::kKPer], k_key[C::kKPer];
+  bool k_hi[C::kKPer];
 #pragma unroll
   for (int it = 0; it < C::kKPer; ++it) {
     const int idx = min(gt + it * C::kGroupThreads, C::kKItems - 1);
     const int j = idx / kChunks, c = idx % kChunks;
     k_hi[it] = j >= kPBlock;
+    k_key[it] = j;
     k_goff[it] = (j % kPBlock) * int(tok_stride) + c * 8;
     k_loff[it] = j * C::kKS + c * 8;
-  }
-#pragma unroll
-  for (int it = 0; it < C::kVPer; ++it) {
-    const int idx = min(gt + it * C::kGroupThreads, C::kVItems - 1);
-    // key quad fastest: the 8 lanes of one dim chunk write 8 different 8-byte Vt columns of one
-    // row (distinct banks); with the chunk fastest, the transposed writes hit 2 banks 8 ways.
-    // Global loads stay 128-byte contiguous per key row.
-    const int kq = idx % (kPT / 4), c = idx / (kPT / 4);
-    v_key[it] = 4 * kq;
-    v_hi[it] = 4 * kq >= kPBlock;
-    v_goff[it] = ((4 * kq) % kPBlock) * int(tok_stride) + c * 8;
-    v_loff[it] = c * 8 * C::kVS + 4 * kq;
+    v_loff[it] = j * C::kVS + c * 8;
   }
   const int64_t page_elems = int64_t(kPBlock) * tok_stride;
 
@@ -282,7 +274,7 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 
   struct Stage {
     u32x4 k[C::kKPer];
-    u32x4 v[C::kVPer][4];
+    u32x4 v[C::kKPer];
     int flags;
   };
   // Global -> registers: this thread's share of the tile.  Every address is a real row (an
@@ -304,58 +296,40 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
         for (int it = 0; it < C::kKPer; ++it) {
           const int vo = (k_goff[it] + (k_hi[it] ? kPBlock * int(tok_stride) : 0)) * 2;
           st.k[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, so + vo, 0, 0));
+          st.v[it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, so + vo, 0, 0));
         }
-#pragma unroll
-        for (int it = 0; it < C::kVPer; ++it)
-#pragma unroll
-          for (int rr = 0; rr < 4; ++rr) {
-            const int vo = (v_goff[it] + rr * int(tok_stride) + (v_hi[it] ? kPBlock * int(tok_stride) : 0)) * 2;
-            st.v[it][rr] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, so + vo, 0, 0));
-          }
         return;
       }
     }
 #pragma unroll
-    for (int it = 0; it < C::kKPer; ++it) st.k[it] = ld16((k_hi[it] ? base_b : base_a) + k_goff[it]);
-#pragma unroll
-    for (int it = 0; it < C::kVPer; ++it)
-#pragma unroll
-      for (int rr = 0; rr < 4; ++rr)
-        st.v[it][rr] = ld16((v_hi[it] ? base_b : base_a) + v_off + v_goff[it] + rr * tok_stride);
+    for (int it = 0; it < C::kKPer; ++it) {
+      const f16* src = (k_hi[it] ? base_b : base_a) + k_goff[it];
+      st.k[it] = ld16(src);
+      st.v[it] = ld16(src + v_off);
+    }
   };
   auto store_tile = [&](int i, int buf, Stage& st) __attribute__((always_inline)) {  // registers -> LDS
     f16* ks = k_tile(buf);
-    f16* vt = v_tile(buf);
+    f16* vs = v_tile(buf);
     if (!(st.flags & 4)) {  // zero V rows of keys past the end or in an invalid page (K is masked)
       const int kt = tile_of(i) * kPT;
 #pragma unroll
-      for (int it = 0; it < C::kVPer; ++it)
-#pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          const int key = v_key[it] + rr;
-          const bool ok = ((st.flags >> (key >= kPBlock ? 1 : 0)) & 1) && kt + key < total;
-          st.v[it][rr] = ok ? st.v[it][rr] : u32x4{0u, 0u, 0u, 0u};
-        }
+      for (int it = 0; it < C::kKPer; ++it) {
+        const int key = k_key[it];
+        const bool ok = ((st.flags >> (key >= kPBlock ? 1 : 0)) & 1) && kt + key < total;
+        st.v[it] = ok ? st.v[it] : u32x4{0u, 0u, 0u, 0u};
+      }
     }
 #pragma unroll
     for (int it = 0; it < C::kKPer; ++it)
-      if (gt + it * C::kGroupThreads < C::kKItems) *reinterpret_cast<u32x4*>(ks + k_loff[it]) = st.k[it];
-#pragma unroll
-    for (int it = 0; it < C::kVPer; ++it) {
-      if (gt + it * C::kGroupThreads < C::kVItems) {
-        // dim e of the 4 keys -> one 8-byte Vt write; halves picked from 32-bit words by value
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int w = e / 2;
-          const uint32_t a0 = st.v[it][0][w], a1 = st.v[it][1][w], a2 = st.v[it][2][w], a3 = st.v[it][3][w];
-          // one byte permute per word: {lo(a0), lo(a1)} or {hi(a0), hi(a1)}
-          const uint32_t kSel = (e & 1) == 0 ? 0x05040100u : 0x07060302u;  // e is unrolled: a constant
-          const u32x2 col4 = u32x2{__builtin_amdgcn_perm(a1, a0, kSel), __builtin_amdgcn_perm(a3, a2, kSel)};
-          *reinterpret_cast<u32x2*>(vt + v_loff[it] + e * C::kVS) = col4;
-        }
+      if (gt + it * C::kGroupThreads < C::kKItems) {
+        *reinterpret_cast<u32x4*>(ks + k_loff[it]) = st.k[it];
+        *reinterpret_cast<u32x4*>(vs + v_loff[it]) = st.v[it];
       }
-    }
   };
+
+  // transposing V reads: lane = 16 g + 4 r + q reads key row 4 (lane / 32) + r, dims 16 (g % 2) + 4 q
+  const int tr_off = (4 * half + (lane % 16) / 4) * C::kVS + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
 
   float m = kNegBig, lsum = 0.f;
   f32x16 acc[kDT];
@@ -418,8 +392,14 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
         const int kb = 16 * u;
-        const f16x4 lo = *reinterpret_cast<const f16x4*>(vt + (32 * dt + col) * C::kVS + kb + 4 * half);
-        const f16x4 hi = *reinterpret_cast<const f16x4*>(vt + (32 * dt + col) * C::kVS + kb + 8 + 4 * half);
+        // A = V^T for dims 32 dt + col, keys kb + 4 half + 0..3 and kb + 8 + 4 half + 0..3: in each
+        // 16-lane group, lane 4r + q reads 4 dims of key row r and the read hands lane i dim i
+        // of the 4 rows
+        const f16* vp = vt + tr_off + kb * C::kVS + 32 * dt;
+        const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                       (__attribute__((address_space(3))) v4i16*)(vp)));
+        const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                       (__attribute__((address_space(3))) v4i16*)(vp + 8 * C::kVS)));
         const f16x8 a = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[u], acc[dt], 0, 0, 0);
       }
