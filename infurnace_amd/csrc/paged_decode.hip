@@ -633,35 +633,62 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   run_range(r_wave, total_units * r_wave / nw, total_units * (r_wave + 1) / nw);
 }
 
-// Cascade rows: merge each segment's prefix states (one per key split) and the state the decode
-// kernel left for its own pages into the fp16 output.  One wave per (row, kv head) segment; rows
-// that are inactive or shorter than the prefix were finished by the decode kernel.  One-wave
-// workgroups spread the state reads over every CU.
-template <int D, int G>
+// Cascade rows: merge each (segment, head)'s prefix states (one per key split) and the state the
+// decode kernel left for its own pages into the fp16 output.  One single-wave workgroup per
+// (row, kv head, head); rows that are inactive or shorter than the prefix were finished by the
+// decode kernel.  Lane s holds state s's (m, l); every state's O slice is requested before any is
+// used (indices clamped, weights zero past the last state), so the merge is two round trips.
+constexpr int kMaxStates = 17;  // prefix key splits (at most 16) + the decode state
+
+template <int D>
 __global__ __launch_bounds__(kWave) void cascade_combine_kernel(
     f16* __restrict__ out, const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active,
-    int32_t batch, int32_t num_kv_heads, int32_t cap, DecodePrefix px) {
+    int32_t batch, int32_t num_kv_heads, int32_t G, int32_t cap, DecodePrefix px) {
+  constexpr int NC = D / kWave;
   const int lane = threadIdx.x;
-  const int64_t seg = blockIdx.x;
-  if (seg >= int64_t(batch) * num_kv_heads) return;
+  const int64_t sg = blockIdx.x;  // (row * Hkv + kv head) * G + head
+  if (sg >= int64_t(batch) * num_kv_heads * G) return;
+  const int64_t seg = sg / G;
+  const int g = int(sg % G);
   const int b = int(seg / num_kv_heads);
   const int len = (active == nullptr || active[b] != 0) ? min(seq_lens[b], cap) : 0;
   if (px.pages <= 0 || len < px.pages * kBlock) return;  // the decode kernel's rule for cascade rows
-  const DecodeWorkspace states{nullptr, px.ml, px.o};  // the segment's states as merge pieces
-  merge_pieces<D, G>(out + seg * G * D, states, seg * px.nstates, px.nstates, lane);
+  const int ns = px.nstates;
+  auto state = [&](int s) { return (seg * ns + min(s, ns - 1)) * G + g; };
+  const float mv = px.ml[state(lane) * 2 + 0];
+  const float lv = px.ml[state(lane) * 2 + 1];
+  float o[kMaxStates][NC];
+#pragma unroll
+  for (int s = 0; s < kMaxStates; ++s)
+#pragma unroll
+    for (int j = 0; j < NC; ++j) o[s][j] = px.o[state(s) * D + lane + kWave * j];
+  const float mx = wave_max(lane < ns ? mv : kNegBig);
+  const float w = lane < ns ? exp2_fast(mv - mx) : 0.f;
+  const float L = wave_sum(w * lv);
+  float acc[NC];
+#pragma unroll
+  for (int j = 0; j < NC; ++j) acc[j] = 0.f;
+#pragma unroll
+  for (int s = 0; s < kMaxStates; ++s) {
+    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+#pragma unroll
+    for (int j = 0; j < NC; ++j) acc[j] = fmaf(ws, o[s][j], acc[j]);
+  }
+  const float inv = L > 0.f ? 1.f / L : 0.f;
+  f16* dst = out + sg * D;
+#pragma unroll
+  for (int j = 0; j < NC; ++j) dst[lane + kWave * j] = f16(acc[j] * inv);
 }
 
 typedef void (*DecodeKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t,
                              const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, float,
                              DecodeWorkspace, DecodePrefix, DecodeAppend);
-typedef void (*CombineKernel)(f16*, const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, DecodePrefix);
+typedef void (*CombineKernel)(f16*, const int32_t*, const uint8_t*, int32_t, int32_t, int32_t, int32_t,
+                              DecodePrefix);
 
-static CombineKernel pick_combine(int d, int g) {
-#define IFN_COMBINE_CASE(DD, GG) \
-  if (d == DD && g == GG) return cascade_combine_kernel<DD, GG>;
-  IFN_COMBINE_CASE(64, 1) IFN_COMBINE_CASE(64, 2) IFN_COMBINE_CASE(64, 4) IFN_COMBINE_CASE(64, 8)
-  IFN_COMBINE_CASE(128, 1) IFN_COMBINE_CASE(128, 2) IFN_COMBINE_CASE(128, 4) IFN_COMBINE_CASE(128, 8)
-#undef IFN_COMBINE_CASE
+static CombineKernel pick_combine(int d) {
+  if (d == 64) return cascade_combine_kernel<64>;
+  if (d == 128) return cascade_combine_kernel<128>;
   return nullptr;
 }
 
@@ -798,7 +825,7 @@ static SharedLayout shared_layout(int32_t batch, int32_t hkv, int32_t g, int32_t
   SharedLayout L;
   size_t off_ml, off_o;
   const size_t dec = decode_ws_layout(batch, hkv, g, d, waves, &off_ml, &off_o);
-  L.nstates = prefix_pass_splits(batch, hkv * g, hkv, d, key_len, cus) + 1;
+  L.nstates = prefix_pass_splits(batch, hkv * g, hkv, d, key_len, cus) + 1;  // <= kMaxStates
   const size_t states = size_t(batch) * hkv * L.nstates * g;
   L.dec_ml = off_ml;
   L.dec_o = off_o;
@@ -846,7 +873,7 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
   const int g = num_q_heads / num_kv_heads;
   DecodeKernel k = pick_decode(head_dim, g, DecodeMode::kCascade);
-  CombineKernel kc = pick_combine(head_dim, g);
+  CombineKernel kc = pick_combine(head_dim);
   if (k == nullptr || kc == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
@@ -858,6 +885,7 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   const int32_t key_len = shared_pages * kBlock;
   const SharedLayout L = shared_layout(batch, num_kv_heads, g, head_dim, int64_t(blocks) * kWavesPerBlock,
                                       key_len, cus);
+  if (L.nstates > kMaxStates) return IFN_ERR_UNSUPPORTED;  // the combine merges at most kMaxStates
   if (workspace == nullptr || workspace_bytes < L.bytes) return IFN_ERR_WORKSPACE;
   IFN_CHECK_ALIGN16(workspace);
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
@@ -884,7 +912,7 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   // 3. merge the states of every cascade segment into the output
   const int64_t segs = int64_t(batch) * num_kv_heads;
   const int32_t cap = int32_t(std::min<int64_t>(int64_t(max_pages_per_seq) * kBlock, max_seq_len));
-  kc<<<dim3(unsigned(segs)), dim3(kWave), 0, s>>>(
-      static_cast<f16*>(out), seq_lens, active_mask, batch, num_kv_heads, cap, px);
+  kc<<<dim3(unsigned(segs * g)), dim3(kWave), 0, s>>>(
+      static_cast<f16*>(out), seq_lens, active_mask, batch, num_kv_heads, g, cap, px);
   return ifn_launch_status();
 }
