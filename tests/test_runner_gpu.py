@@ -186,3 +186,85 @@ def test_decode_batch_over_shared_prefix_uses_one_read(dev):
                 ref.append(s, l, k[i:i + 1], v[i:i + 1])
                 assert_attn_close(out[i:i + 1], ref.attend(s, l, q[i], None)[None], f"shared decode slot {s} l {l}")
     run.pool.check_invariants()
+
+
+def test_randomized_engine_trace(dev):
+    """A seeded random engine trace: prompts with prefix-cache hits, chunked prefills of varied
+    sizes (aligned and unaligned starts), batched decodes with padding rows, shared-prefix
+    decode batches, releases and slot reuse -- every attention output checked against the
+    contiguous-cache oracle."""
+    say("runner: randomized engine trace")
+    rng = np.random.default_rng(2026)
+    n_slots = 5
+    run = PagedKVRunner(L, num_slots=n_slots, max_context=768, num_kv_heads=HKV, head_dim=D, num_blocks=400,
+                        device=dev, prefix_namespace=("toy", "fp16"), shared_prefix_min_pages=2)
+    ref = Reference()
+    prompts = {}
+    block_kv = {}  # (token prefix through block i) -> per-layer K/V of block i, first publisher's
+    base_prompt = [int(t) for t in rng.integers(0, 1000, size=160)]  # shared by several requests
+    seen = {"shared_steps": 0, "unaligned_chunks": 0}
+
+    def prefill_prompt(slot, toks):
+        n = run.attach_prefix(slot, toks)
+        for l in range(L):  # a cache hit's pages hold the K/V of the request that published them
+            if n:
+                blocks = [block_kv[(tuple(toks[:16 * (i + 1)]), l)] for i in range(n // 16)]
+                ref.k[(slot, l)] = np.concatenate([kb for kb, _ in blocks])
+                ref.v[(slot, l)] = np.concatenate([vb for _, vb in blocks])
+        pos = n
+        while pos < len(toks):
+            T = int(min(len(toks) - pos, rng.choice([16, 32, 37, 64, 100])))
+            seen["unaligned_chunks"] += pos % 32 != 0
+            step = run.begin_prefill(slot, pos, T)
+            for l in range(L):
+                q, k, v = _qkv(rng, T)
+                out = step.store_attend(l, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))
+                ref.append(slot, l, k, v)
+                assert_attn_close(out, ref.attend(slot, l, q, pos), f"prefill slot {slot} pos {pos} T {T}")
+            pos += T
+        prompts[slot] = list(toks)
+        run.publish_prefix(slot, toks)
+        for i in range(len(toks) // 16):  # blocks already cached keep their first publisher's K/V
+            for l in range(L):
+                key = (tuple(toks[:16 * (i + 1)]), l)
+                if key not in block_kv:
+                    block_kv[key] = (ref.k[(slot, l)][16 * i:16 * (i + 1)].copy(),
+                                     ref.v[(slot, l)][16 * i:16 * (i + 1)].copy())
+
+    for rnd in range(6):
+        free = [s for s in range(n_slots) if s not in prompts]
+        for s in free[:int(rng.integers(1, len(free) + 1)) if free else 0]:
+            extra = [int(t) for t in rng.integers(0, 1000, size=int(rng.integers(1, 90)))]
+            toks = (base_prompt[:int(rng.choice([16, 48, 96, 160]))] if rng.random() < 0.8 else []) + extra
+            prefill_prompt(s, toks)
+        live = sorted(prompts)
+        sharing = [s for s in live if prompts[s][:32] == base_prompt[:32]]
+        for _ in range(int(rng.integers(2, 5))):
+            # every live slot, or only those that started from the shared prompt (a batch whose
+            # rows can share leading pages)
+            batch = sharing if len(sharing) >= 2 and rng.random() < 0.5 else live
+            rows = [(s, True) for s in batch] + [(int(rng.integers(0, n_slots)), False)]
+            plan = Plan(tuple(s for s, _ in rows), tuple(run.length(s) if a else 0 for s, a in rows),
+                        tuple(a for _, a in rows))
+            step = run.begin_decode(plan)
+            seen["shared_steps"] += step.shared_prefix is not None
+            for l in range(L):
+                q, k, v = _qkv(rng, len(rows))
+                out = step.store_attend(l, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))
+                for i, (s, a) in enumerate(rows):
+                    if not a:
+                        continue
+                    ref.append(s, l, k[i:i + 1], v[i:i + 1])
+                    assert_attn_close(out[i:i + 1], ref.attend(s, l, q[i], None)[None], f"decode round {rnd} slot {s}")
+            for s, a in rows:
+                if a:
+                    prompts[s] = prompts[s] + [-1]  # decoded tokens never match a prompt
+        for s in list(prompts)[:int(rng.integers(1, 3))]:
+            run.clear_slot(s, zero=bool(rng.random() < 0.5))
+            ref.clear(s)
+            del prompts[s]
+        run.pool.check_invariants()
+        run.prefix.check_invariants()
+    # the trace went through every path: prefix-cache hits, shared-prefix decode, unaligned chunks
+    assert run.prefix.stats.hit_blocks > 0 and seen["shared_steps"] > 0 and seen["unaligned_chunks"] > 0, \
+        (run.prefix.stats, seen)
