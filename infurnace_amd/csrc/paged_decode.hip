@@ -251,21 +251,39 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
 
   // 0. Fused append: 16-byte chunks of every appended K and V row, spread over the grid.  No
   // wave of this launch reads these slots (the attention takes the token from new_k / new_v).
-  if constexpr (kAppend) {
-    const int chunks = num_kv_heads * D / 8;  // per row of K (and of V)
-    const int64_t items = int64_t(batch) * 2 * chunks;
-    for (int64_t it = int64_t(blockIdx.x) * kDecodeThreads + tid; it < items;
-         it += int64_t(gridDim.x) * kDecodeThreads) {
-      const int b = int(it / (2 * chunks));
-      const int rem = int(it % (2 * chunks));
-      const int kv = rem / chunks, c = rem % chunks;
-      const int slot = append_slot(b);
-      if (slot < 0) continue;
-      const f16* src = (kv == 0 ? ap.new_k : ap.new_v) + int64_t(b) * num_kv_heads * D + c * 8;
-      f16* dst = ap.pool + (int64_t(kv) * num_slots + slot) * num_kv_heads * D + c * 8;
-      *reinterpret_cast<u32x4*>(dst) = ld16(src);
+  // A thread's first chunk is loaded here and stored once its attention work is done
+  // (flush_append), so the copy adds no round trip to the start of the launch.
+  const int app_chunks = num_kv_heads * D / 8;  // per row of K (and of V)
+  const int64_t app_items = kAppend ? int64_t(batch) * 2 * app_chunks : 0;
+  // item it: row b = it / (2 chunks), K or V, 16-byte chunk c; the slot comes from the LDS table
+  // (filled below)
+  auto app_src = [&](int64_t it) __attribute__((always_inline)) {
+    const int b = int(it / (2 * app_chunks)), rem = int(it % (2 * app_chunks));
+    return (rem / app_chunks == 0 ? ap.new_k : ap.new_v) + int64_t(b) * num_kv_heads * D + (rem % app_chunks) * 8;
+  };
+  auto app_dst = [&](int64_t it) __attribute__((always_inline)) -> f16* {  // null: nothing to store
+    const int b = int(it / (2 * app_chunks)), rem = int(it % (2 * app_chunks));
+    const int slot = s_slot[b];
+    return slot < 0 ? nullptr
+                    : ap.pool + (int64_t(rem / app_chunks) * num_slots + slot) * num_kv_heads * D + (rem % app_chunks) * 8;
+  };
+  const int64_t app_first = int64_t(blockIdx.x) * kDecodeThreads + tid;
+  u32x4 app_data = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (kAppend)
+    if (app_first < app_items) app_data = ld16(app_src(app_first));
+  auto flush_append = [&]() __attribute__((always_inline)) {
+    if constexpr (kAppend) {
+      if (app_first < app_items) {
+        f16* d0 = app_dst(app_first);
+        if (d0 != nullptr) *reinterpret_cast<u32x4*>(d0) = app_data;
+      }
+      for (int64_t it = app_first + int64_t(gridDim.x) * kDecodeThreads; it < app_items;
+           it += int64_t(gridDim.x) * kDecodeThreads) {  // more rows than one chunk per thread
+        f16* d = app_dst(it);
+        if (d != nullptr) *reinterpret_cast<u32x4*>(d) = ld16(app_src(it));
+      }
     }
-  }
+  };
 
   // 1. Exclusive prefix of pages per row, in LDS (every workgroup builds its own copy).
   int running = 0;
@@ -320,7 +338,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   }
 
   const int64_t total_units = int64_t(running) * num_kv_heads;
-  if (total_units == 0) return;
+  if (total_units == 0) {
+    flush_append();
+    return;
+  }
   const int64_t nw = min(int64_t(gridDim.x) * kWavesPerBlock, total_units);
   // Static balanced split: range r covers units [T*r/nw, (T*(r+1))/nw), one per wave, so
   // every wave streams the same number of 8 KiB units.  Workgroup i runs on XCD i % 8
@@ -334,7 +355,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   const int64_t blk = nblk % kXcds == 0 ? (blockIdx.x % kXcds) * (nblk / kXcds) + blockIdx.x / kXcds
                                         : int64_t(blockIdx.x);
   const int64_t r_wave = blk * kWavesPerBlock + wave;
-  if (r_wave >= nw) return;
+  if (r_wave >= nw) {
+    flush_append();
+    return;
+  }
   auto range_of = [&](int64_t u) -> int64_t { return ((u + 1) * nw - 1) / total_units; };
 
   const int row = lane / 8;  // tokens row and row+8 of a page
@@ -631,6 +655,7 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
   };
 
   run_range(r_wave, total_units * r_wave / nw, total_units * (r_wave + 1) / nw);
+  flush_append();
 }
 
 // Cascade rows: merge each (segment, head)'s prefix states (one per key split) and the state the
