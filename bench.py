@@ -543,6 +543,9 @@ def main() -> int:
         "fused_step": {"entry": "ifn_paged_decode_append (store_kv + paged decode in one launch per layer)",
                        "us_per_layer": round(float(np.mean(fused_ms)) * 1e3, 3),
                        "two_launch_us_per_layer": round((float(np.mean(app_ms)) + float(np.mean(dec_ms))) * 1e3, 3),
+                       # what the append adds to a decode launch when fused into it
+                       "append_marginal_us_per_layer": round((float(np.mean(fused_ms)) - float(np.mean(dec_ms))) * 1e3,
+                                                             3),
                        "ms_per_step": round(fused_wall / K * 1e3, 4)},
         "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
                      "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
