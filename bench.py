@@ -263,8 +263,10 @@ def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> di
     store_kv (one token per row) then decode per layer; HIP events around every decode launch.
     For a table with shared pages the roofline counts each physical page once (`unique`); the
     logical K/V a launch attends is reported beside it.  Such a workload is timed through the
-    shared-prefix entry point (prefix pass + decode over private pages, both inside the events) and
-    through the plain decode entry point."""
+    shared-prefix entry point (prefix pass + decode over private pages, both inside the events),
+    through the plain decode with cached page loads (the same entry with no shared pages: the path
+    for rows that share pages outside a common leading run) and through ifn_paged_decode, whose
+    streaming page loads re-read shared pages from HBM."""
     import torch
     B, hq, hkv, d, P = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.num_pages
     pool = torch.empty((layers, 2, P, 16, hkv, d), dtype=torch.float16, device=dev)
@@ -285,16 +287,17 @@ def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> di
     lb = pool[0].numel() * 2
     scale = 1.0 / np.sqrt(d)
 
-    def one(layer, shared, evs=None, j=0):
+    def one(layer, mode, evs=None, j=0):
         rc = lib.ifn_store_kv(pool.data_ptr() + layer * lb, P, slots.data_ptr(), None, nk[layer].data_ptr(),
                               nk[layer].data_ptr(), B, hkv, d, 16, stream)
         if evs is not None:
             hip.hip.hipEventRecord(evs[2 * j], stream)
-        if shared:
+        if mode in ("prefix", "cached"):
+            n_sp = sp if mode == "prefix" else 0
             rc |= lib.ifn_paged_decode_shared_prefix(
-                out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P, prefix.data_ptr(), sp,
-                bt.data_ptr(), w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, ws.data_ptr(),
-                ws_bytes, stream)
+                out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P,
+                prefix.data_ptr() if n_sp else None, n_sp, bt.data_ptr(), w.max_pages, sl.data_ptr(), None, B, hq,
+                hkv, d, 16, max_len, scale, ws.data_ptr(), ws_bytes, stream)
         else:
             rc |= lib.ifn_paged_decode(out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P,
                                        bt.data_ptr(), w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len,
@@ -304,22 +307,23 @@ def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> di
         if rc:
             raise RuntimeError(f"{w.name}: launch failed: {rc}")
 
-    def timed(shared: bool) -> float:
+    def timed(mode: str) -> float:
         for layer in range(layers):
-            one(layer, shared)
+            one(layer, mode)
         torch.cuda.synchronize()
         n = layers * reps
         evs = hip.create(2 * n)
         for r in range(reps):
             for layer in range(layers):
-                one(layer, shared, evs, r * layers + layer)
+                one(layer, mode, evs, r * layers + layer)
         torch.cuda.synchronize()
         us = float(np.mean([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(n)])) * 1e3
         hip.destroy(evs)
         return us
 
-    us = timed(bool(sp))
-    us_plain = timed(False) if sp else us
+    us = timed("prefix" if sp else "stream")
+    us_cached = timed("cached") if sp else None
+    us_stream = timed("stream") if sp else us
     del pool
     uniq = w.decode_bytes(unique=True)
     logical = w.decode_bytes()
@@ -330,7 +334,8 @@ def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> di
            "frac": round(gbps / HBM_PEAK_GBPS, 4), "logical_bytes_per_layer": logical,
            "effective_GB/s": round(logical / (us / 1e6) / 1e9, 1)}
     if sp:
-        res["plain_decode_us_per_layer"] = round(us_plain, 2)
+        res["plain_decode_us_per_layer"] = round(us_cached, 2)  # cached page loads
+        res["plain_stream_decode_us_per_layer"] = round(us_stream, 2)
     return res
 
 

@@ -107,6 +107,10 @@ size_t ifn_paged_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int3
  * max_seq_len; a page id outside [0, num_pages) contributes no keys (no
  * out-of-bounds read).  max_seq_len is the host-side upper bound of seq_lens
  * that sizes the launch and the workspace.
+ * Page loads are streamed (non-temporal hint): each page is expected to be read
+ * by one row of the batch.  Batches whose rows share pages go through
+ * ifn_paged_decode_shared_prefix (shared_pages == 0 when the shared pages are
+ * not a common leading run), which keeps pages in the caches.
  * The workspace must be zero-filled once when created; every call leaves its
  * counters at zero again, so one workspace serves any number of calls on one
  * stream (calls overlapping on two streams need two workspaces).
@@ -158,7 +162,9 @@ size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num
  * each row streams only its own pages, and a combine merges the partial
  * softmax states per (row, kv head).  Same arguments, output and rules as
  * ifn_paged_decode otherwise; rows shorter than the prefix are attended in
- * full through their own table.  shared_pages == 0 is ifn_paged_decode.
+ * full through their own table.  shared_pages == 0 is ifn_paged_decode with
+ * cached page loads, for batches whose rows share pages anywhere in their
+ * tables (prefix_pages may then be NULL).
  * head_dim 64 or 128 (IFN_ERR_UNSUPPORTED otherwise, as for prefill).
  * The precondition is not checked: a row whose leading table entries differ
  * from prefix_pages is attended as if it held prefix_pages.

@@ -13,8 +13,10 @@
 // A workgroup of 256 lanes owns kTok whole tokens; each lane issues all of its
 // loads before its first store so kTok x 16 B per lane are in flight.  The slot
 // and active flag are read once per token (uniform across the workgroup, so
-// they become scalar loads).  Rows that are inactive or whose slot lies outside
-// the pool write nothing.
+// they become scalar loads).  The source rows are read with the non-temporal
+// hint (read once): the batched 28-layer x 2048-token append measured 75 us
+// against 96 us with plain loads.  Rows that are inactive or whose slot lies
+// outside the pool write nothing.
 #include "ifn_common.hpp"
 
 namespace ifn {
@@ -46,7 +48,7 @@ __global__ __launch_bounds__(kStoreThreads) void store_kv_1024(
       const int64_t s = slot_mapping[t];
       if (s >= 0 && s < num_slots) slot[i] = s;
     }
-    if (slot[i] >= 0) buf[i] = ld16(src + int64_t(t) * kRowBytes);
+    if (slot[i] >= 0) buf[i] = ld16_stream(src + int64_t(t) * kRowBytes);
   }
 #pragma unroll
   for (int i = 0; i < kTok; ++i)
@@ -72,7 +74,7 @@ __global__ __launch_bounds__(kStoreThreads) void store_kv_generic(
   for (int c = threadIdx.x; c < 2 * row_chunks; c += kStoreThreads) {
     const bool is_v = c >= row_chunks;
     const int64_t o = int64_t(is_v ? c - row_chunks : c) * 16;
-    st16((is_v ? dv : dk) + o, ld16((is_v ? sv : sk) + o));
+    st16((is_v ? dv : dk) + o, ld16_stream((is_v ? sv : sk) + o));
   }
 }
 

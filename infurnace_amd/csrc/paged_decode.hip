@@ -23,7 +23,8 @@
 //  * Each K/V page is fetched once and reused from registers by every query
 //    head of its GQA group.  Inside a page, lane = 8*row + col: every load
 //    instruction reads 8 token rows x 128 contiguous bytes; each lane holds 2
-//    tokens.  q.k uses v_dot2_f32_f16 (fp32 accumulation) and three DPP steps
+//    tokens.  The page loads carry the non-temporal hint (each byte is read
+//    once per launch).  q.k uses v_dot2_f32_f16 (fp32 accumulation) and three DPP steps
 //    inside the row; the online softmax runs in base 2 per (lane row, head).
 //    At the end of a piece the 8 lane rows merge: (m, l) by butterflies, O by
 //    a reduce-scatter that leaves lane 8*row + col holding element `row` of
@@ -214,8 +215,11 @@ __device__ __forceinline__ void merge_pieces(f16* __restrict__ o, const DecodeWo
 
 // kCascade: compiled with the shared-prefix (cascade) paths; without it every cascade branch
 // folds away and px is ignored.  kAppend: compiled with the fused append (ap); otherwise ap is
-// ignored.
-template <int D, int G, bool kCascade, bool kAppend>
+// ignored.  kStream: K/V page loads carry the non-temporal hint.  That is right when every page is
+// read once per launch (config 2: 60.8 -> 55.2 us per launch on one box) and wrong when rows of the
+// batch share pages, which the caches would otherwise serve (config 5 read through this kernel:
+// 122.6 -> 149 us); the cached-load variant is kept for batches with shared pages.
+template <int D, int G, bool kCascade, bool kAppend, bool kStream = true>
 __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool,
     int64_t num_pages, const int32_t* __restrict__ block_tables, int32_t max_pages,
@@ -430,8 +434,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
             const bool mine = row + 8 * tt == tok;  // this lane's token is the appended one
 #pragma unroll
             for (int ch = 0; ch < NC; ++ch) {
-              kr[tt][ch] = ld16(mine ? ap.new_k + src + ch * 64 : base + tt * 8 * tok_stride + ch * 64);
-              vr[tt][ch] = ld16(mine ? ap.new_v + src + ch * 64 : base + v_off + tt * 8 * tok_stride + ch * 64);
+              const f16* ks_ = mine ? ap.new_k + src + ch * 64 : base + tt * 8 * tok_stride + ch * 64;
+              const f16* vs_ = mine ? ap.new_v + src + ch * 64 : base + v_off + tt * 8 * tok_stride + ch * 64;
+              kr[tt][ch] = kStream ? ld16_stream(ks_) : ld16(ks_);
+              vr[tt][ch] = kStream ? ld16_stream(vs_) : ld16(vs_);
             }
           }
           return;
@@ -441,8 +447,10 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
       for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
         for (int ch = 0; ch < NC; ++ch) {
-          kr[tt][ch] = ld16(base + tt * 8 * tok_stride + ch * 64);
-          vr[tt][ch] = ld16(base + v_off + tt * 8 * tok_stride + ch * 64);
+          const f16* ks_ = base + tt * 8 * tok_stride + ch * 64;
+          const f16* vs_ = base + v_off + tt * 8 * tok_stride + ch * 64;
+          kr[tt][ch] = kStream ? ld16_stream(ks_) : ld16(ks_);
+          vr[tt][ch] = kStream ? ld16_stream(vs_) : ld16(vs_);
         }
     };
 
@@ -717,7 +725,9 @@ static CombineKernel pick_combine(int d) {
   return nullptr;
 }
 
-enum class DecodeMode { kPlain, kCascade, kAppend };
+// kPlain streams its pages; kPlainCached is the same kernel with cached page loads, for batches whose
+// rows share pages outside a common leading run.
+enum class DecodeMode { kPlain, kPlainCached, kCascade, kAppend };
 
 static DecodeKernel pick_decode(int d, int g, DecodeMode mode = DecodeMode::kPlain) {
 #define IFN_DECODE_CASE(DD, GG) \
@@ -726,6 +736,8 @@ static DecodeKernel pick_decode(int d, int g, DecodeMode mode = DecodeMode::kPla
   if (d == DD && g == GG && mode == DecodeMode::kCascade) return paged_decode_kernel<DD, GG, true, false>;
 #define IFN_APPEND_CASE(DD, GG) \
   if (d == DD && g == GG && mode == DecodeMode::kAppend) return paged_decode_kernel<DD, GG, false, true>;
+#define IFN_CACHED_CASE(DD, GG) \
+  if (d == DD && g == GG && mode == DecodeMode::kPlainCached) return paged_decode_kernel<DD, GG, false, false, false>;
   IFN_DECODE_CASE(64, 1) IFN_DECODE_CASE(64, 2) IFN_DECODE_CASE(64, 4) IFN_DECODE_CASE(64, 8)
   IFN_DECODE_CASE(128, 1) IFN_DECODE_CASE(128, 2) IFN_DECODE_CASE(128, 4) IFN_DECODE_CASE(128, 8)
   IFN_DECODE_CASE(256, 1) IFN_DECODE_CASE(256, 2) IFN_DECODE_CASE(256, 4)
@@ -734,9 +746,13 @@ static DecodeKernel pick_decode(int d, int g, DecodeMode mode = DecodeMode::kPla
   IFN_APPEND_CASE(64, 1) IFN_APPEND_CASE(64, 2) IFN_APPEND_CASE(64, 4) IFN_APPEND_CASE(64, 8)
   IFN_APPEND_CASE(128, 1) IFN_APPEND_CASE(128, 2) IFN_APPEND_CASE(128, 4) IFN_APPEND_CASE(128, 8)
   IFN_APPEND_CASE(256, 1) IFN_APPEND_CASE(256, 2) IFN_APPEND_CASE(256, 4)
+  IFN_CACHED_CASE(64, 1) IFN_CACHED_CASE(64, 2) IFN_CACHED_CASE(64, 4) IFN_CACHED_CASE(64, 8)
+  IFN_CACHED_CASE(128, 1) IFN_CACHED_CASE(128, 2) IFN_CACHED_CASE(128, 4) IFN_CACHED_CASE(128, 8)
+  IFN_CACHED_CASE(256, 1) IFN_CACHED_CASE(256, 2) IFN_CACHED_CASE(256, 4)
 #undef IFN_DECODE_CASE
 #undef IFN_CASCADE_CASE
 #undef IFN_APPEND_CASE
+#undef IFN_CACHED_CASE
   return nullptr;
 }
 
@@ -755,13 +771,14 @@ extern "C" size_t ifn_paged_decode_workspace_bytes(int32_t batch, int32_t num_q_
 
 namespace ifn {
 
-// ifn_paged_decode and ifn_paged_decode_append: the same checks and launch; `ap` carries the
-// fused append (kAppend variant) when its pointers are given.
+// ifn_paged_decode, ifn_paged_decode_append and ifn_paged_decode_shared_prefix with no shared
+// pages: the same checks and launch; `ap` carries the fused append (kAppend variant) when its
+// pointers are given; `cached` selects the cached-load plain variant.
 static int decode_entry(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
                         const int32_t* block_tables, int32_t max_pages_per_seq, const int32_t* seq_lens,
                         const uint8_t* active_mask, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                         int32_t head_dim, int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
-                        size_t workspace_bytes, void* stream, const DecodeAppend& ap) {
+                        size_t workspace_bytes, void* stream, const DecodeAppend& ap, bool cached = false) {
   const bool append = ap.pool != nullptr;
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_tables == nullptr ||
       seq_lens == nullptr)
@@ -773,7 +790,8 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
     return IFN_ERR_INVALID_ARGUMENT;
   if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
-  DecodeKernel k = pick_decode(head_dim, num_q_heads / num_kv_heads, append ? DecodeMode::kAppend : DecodeMode::kPlain);
+  DecodeKernel k = pick_decode(head_dim, num_q_heads / num_kv_heads,
+                               append ? DecodeMode::kAppend : (cached ? DecodeMode::kPlainCached : DecodeMode::kPlain));
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
@@ -883,10 +901,10 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
                                               int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
                                               size_t workspace_bytes, void* stream) {
   using namespace ifn;
-  if (shared_pages == 0)
-    return ifn_paged_decode(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
-                            active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
-                            workspace, workspace_bytes, stream);
+  if (shared_pages == 0)  // no common leading run: plain decode with cached page loads
+    return decode_entry(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                        active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
+                        workspace, workspace_bytes, stream, DecodeAppend{nullptr, nullptr, nullptr, nullptr}, true);
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_tables == nullptr ||
       seq_lens == nullptr || prefix_pages == nullptr)
     return IFN_ERR_INVALID_ARGUMENT;

@@ -76,7 +76,10 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
     (int32 [S] on the device) declares that every row of at least
     S * block_size keys starts its table with these S pages (a prefix-cache
     hit); they are then read once for the whole batch instead of once per row.
-    The declaration is trusted, not checked.
+    The declaration is trusted, not checked.  Without it the decode streams its
+    pages (non-temporal loads, each page expected to be read by one row); an
+    empty ``shared_prefix_pages`` declares rows that share pages outside a
+    common leading run, and the decode then keeps pages in the caches.
 
     Prefill (``query_start`` given): ``query`` [T, Hq, D] of one sequence,
     ``block_tables`` int32 [max_pages] or [1, max_pages]; ``sequence_lengths`` is

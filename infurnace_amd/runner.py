@@ -22,7 +22,9 @@ this package's pool, tables and kernels:
   (src/infurnace/engine/engine.py:89,130,166);
 * a decode batch whose live rows start with the same pages (prefix-cache hits)
   reads those pages once for the batch (``paged_attention(...,
-  shared_prefix_pages=...)``) when they are at least ``shared_prefix_min_pages``.
+  shared_prefix_pages=...)``) when they are at least ``shared_prefix_min_pages``;
+  a batch whose rows share pages otherwise keeps its page loads cached (an empty
+  ``shared_prefix_pages``), since the default decode streams every page once.
 
 The model itself (projections, MLP, logits) stays with the caller.
 """
@@ -56,7 +58,8 @@ class _Step:
     positions: torch.Tensor           # int32 [T]
     query_start: int | None           # prefill only
     max_len: int
-    shared_prefix: torch.Tensor | None = None  # int32 pages every live decode row starts with
+    # int32 pages every live decode row starts with; empty: rows share pages elsewhere (cached page loads)
+    shared_prefix: torch.Tensor | None = None
 
     def store_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      out: torch.Tensor | None = None) -> torch.Tensor:
@@ -234,9 +237,14 @@ class PagedKVRunner:
         act = np.asarray(active, np.uint8)
         table = self._table(slots)
         shared = self._common_pages(table[live], lens[live])
+        if len(shared) >= self.shared_prefix_min_pages:
+            prefix = self._dev(shared)
+        elif self._any_shared(table[live], lens[live]):
+            prefix = self._dev(np.zeros(0, np.int32))
+        else:
+            prefix = None
         return _Step(self, self._dev(sm), self._dev(table), self._dev(lens), self._dev(act),
-                     self._dev(np.asarray(positions, np.int32)), None, int(lens.max()) if len(lens) else 0,
-                     self._dev(shared) if len(shared) >= self.shared_prefix_min_pages else None)
+                     self._dev(np.asarray(positions, np.int32)), None, int(lens.max()) if len(lens) else 0, prefix)
 
     def _common_pages(self, table: np.ndarray, lens: np.ndarray) -> np.ndarray:
         """Leading page ids that every row of ``table`` holds at the same columns (at least two
@@ -247,6 +255,14 @@ class PagedKVRunner:
         same = (table[:, :limit] == table[0, :limit]).all(axis=0)
         n = int(np.argmin(same)) if not same.all() else limit
         return np.ascontiguousarray(table[0, :n], dtype=np.int32)
+
+    def _any_shared(self, table: np.ndarray, lens: np.ndarray) -> bool:
+        """Whether a page id occurs in more than one of the rows' used table entries (``lens`` keys)."""
+        if table.shape[0] < 2:
+            return False
+        used = -(-lens.astype(np.int64) // self.block_size)
+        pages = np.concatenate([table[i, :used[i]] for i in range(table.shape[0])])
+        return len(np.unique(pages)) != len(pages)
 
     # -- lifecycle --------------------------------------------------------------------------
 

@@ -150,12 +150,15 @@ def test_prefix_cache_hit_shares_pages_and_matches_full_prefill(dev):
     run.pool.check_invariants()
 
 
-def test_decode_batch_over_shared_prefix_uses_one_read(dev):
-    """Rows attached to one cached prompt decode through the shared-prefix path; outputs match."""
-    say("runner: decode over a shared prefix")
+@pytest.mark.parametrize("min_pages", [2, 64])
+def test_decode_batch_over_shared_prefix_uses_one_read(dev, min_pages):
+    """Rows attached to one cached prompt decode through the shared-prefix path (6 common pages,
+    min_pages 2), or with cached page loads when the common run is below the threshold
+    (min_pages 64); outputs match in both."""
+    say(f"runner: decode over a shared prefix, min_pages={min_pages}")
     rng = np.random.default_rng(31)
     run = PagedKVRunner(L, num_slots=4, max_context=512, num_kv_heads=HKV, head_dim=D, num_blocks=128, device=dev,
-                        prefix_namespace=("toy", "fp16"), shared_prefix_min_pages=2)
+                        prefix_namespace=("toy", "fp16"), shared_prefix_min_pages=min_pages)
     ref = Reference()
     prompt = list(range(500, 500 + 100))              # 6 complete blocks + 4 tokens
     step = run.begin_prefill(0, 0, 100)
@@ -178,7 +181,7 @@ def test_decode_batch_over_shared_prefix_uses_one_read(dev):
         rows = [(1, True), (2, True), (0, True), (3, True)]
         plan = Plan(tuple(s for s, _ in rows), tuple(run.length(s) for s, _ in rows), tuple(a for _, a in rows))
         step = run.begin_decode(plan)
-        assert step.shared_prefix is not None and step.shared_prefix.numel() == 6
+        assert step.shared_prefix is not None and step.shared_prefix.numel() == (6 if min_pages == 2 else 0)
         for l in range(L):
             q, k, v = _qkv(rng, len(rows))
             out = step.store_attend(l, to_dev(q, dev), to_dev(k, dev), to_dev(v, dev))

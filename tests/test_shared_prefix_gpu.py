@@ -156,3 +156,19 @@ def test_workspace_shared_with_other_entry_points(dev):
                                  query_start=int(lens[1]) - t)
             ref2 = oracle.paged_attention(qp[None], pool, table[1:2], lens[1:2])[0]
             assert_attn_close(o2, ref2, f"rep {rep} prefill")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (16, 8, 64)])
+def test_no_common_prefix_cached_loads_equal_streaming(dev, hq, hkv, d):
+    """shared_pages == 0 is the plain decode with cached page loads: bit-identical to
+    ifn_paged_decode (streaming loads) on tables whose rows share pages, and to the oracle."""
+    say(f"cached plain decode hq={hq} hkv={hkv} d={d}")
+    rng = np.random.default_rng(hq + hkv + d)
+    pool, table, lens, q, prefix = _shared(rng, 12, [0, 3, 40, 160, 700], hq, hkv, d)
+    # two rows swap their shared pages' order, so the shared pages form no common leading run
+    table[1, :12] = table[1, :12][::-1]
+    args = (to_dev(q, dev), to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev), None)
+    cached = paged_attention(*args, shared_prefix_pages=torch.zeros(0, dtype=torch.int32, device=dev))
+    streamed = paged_attention(*args)
+    assert torch.equal(cached.view(torch.int16), streamed.view(torch.int16))
+    assert_attn_close(cached, oracle.paged_attention(q, pool, table, lens), f"hq={hq} hkv={hkv} d={d}")
