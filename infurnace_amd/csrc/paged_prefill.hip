@@ -15,10 +15,12 @@
 //    every group the same), and the G waves of a group share each K/V tile
 //    staged in LDS.  At the end the groups merge log-sum-exp style through
 //    LDS.
-//  * Tiles are double-buffered in LDS and staged two deep in registers: while
-//    tile i is multiplied, tile i+1 goes from registers to the other LDS
-//    buffer and tile i+2's 16-byte global loads are in flight.  Page ids come
-//    from a lane window (two per tile), so no load waits on a table load.
+//  * Tiles are double-buffered in LDS with one register stage: step i first
+//    moves tile i+1 from registers to the other LDS buffer and issues tile
+//    i+2's 16-byte global loads, then multiplies tile i.  A tile's K and V^T
+//    fragments are read from LDS in one batch each, ahead of the MFMAs that
+//    use them.  Page ids come from a lane window (two per tile), so no load
+//    waits on a table load.
 //    Only the G waves of a key group share its tiles, so they synchronise
 //    through a per-group count in LDS instead of a workgroup barrier.
 //  * Workgroup i runs on XCD i % 8; the kv head is i % Hkv, so for Hkv = 8
@@ -342,12 +344,31 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     const int kt = tile_of(i) * kPT;
     const f16* ks = k_tile(buf);
     const f16* vt = v_tile(buf);
+    // All K fragments, then the S MFMAs; the V^T fragments are requested right behind them, so
+    // their LDS latency runs under the softmax.  (The scheduling barriers keep that order.)
     f32x16 st = f32x16{};
+    f16x8 kf[kKSteps];
 #pragma unroll
-    for (int s = 0; s < kKSteps; ++s) {
-      const f16x8 a = *reinterpret_cast<const f16x8*>(ks + col * C::kKS + 16 * s + 8 * half);
-      st = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, qreg[s], st, 0, 0, 0);
-    }
+    for (int s = 0; s < kKSteps; ++s) kf[s] = *reinterpret_cast<const f16x8*>(ks + col * C::kKS + 16 * s + 8 * half);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int s = 0; s < kKSteps; ++s) st = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[s], qreg[s], st, 0, 0, 0);
+    __builtin_amdgcn_sched_barrier(0);
+    // A = V^T for dims 32 dt + col, keys 16 u + 4 half + 0..3 (lo) and 16 u + 8 + 4 half + 0..3 (hi):
+    // in each 16-lane group, lane 4r + q reads 4 dims of key row r and the read hands lane i dim i
+    // of the 4 rows
+    f16x4 vlo[kDT][2], vhi[kDT][2];
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const f16* vp = vt + tr_off + 16 * u * C::kVS + 32 * dt;
+        vlo[dt][u] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                   (__attribute__((address_space(3))) v4i16*)(vp)));
+        vhi[dt][u] = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                                   (__attribute__((address_space(3))) v4i16*)(vp + 8 * C::kVS)));
+      }
+    __builtin_amdgcn_sched_barrier(0);
     // causal mask (key_pos <= query_pos), end of sequence and invalid pages -- only on tiles
     // that are not entirely visible; raw scores, the scale is folded into the exponent below
     if (!(flags & 4)) {
@@ -393,61 +414,53 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     for (int dt = 0; dt < kDT; ++dt)
 #pragma unroll
       for (int u = 0; u < 2; ++u) {
-        const int kb = 16 * u;
-        // A = V^T for dims 32 dt + col, keys kb + 4 half + 0..3 and kb + 8 + 4 half + 0..3: in each
-        // 16-lane group, lane 4r + q reads 4 dims of key row r and the read hands lane i dim i
-        // of the 4 rows
-        const f16* vp = vt + tr_off + kb * C::kVS + 32 * dt;
-        const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                       (__attribute__((address_space(3))) v4i16*)(vp)));
-        const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                                                       (__attribute__((address_space(3))) v4i16*)(vp + 8 * C::kVS)));
+        const f16x4 lo = vlo[dt][u], hi = vhi[dt][u];
         const f16x8 a = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         acc[dt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a, pb[u], acc[dt], 0, 0, 0);
       }
   };
 
-  // Sweep: iteration i multiplies the group's tile i*kGroups + grp from LDS buffer i&1; tile i+1
-  // waits in registers and tile i+2's loads are in flight.  Tile i lives in register stage i&1,
-  // so the loop is unrolled by two.  Every iteration ends with the wave's tile-store count (below);
-  // the config-3 prefill measured 82.6 us per layer this way against 85.5 us with a workgroup
-  // barrier per iteration.
+  // Sweep: step i multiplies the group's tile i*kGroups + grp from LDS buffer i&1.  It first
+  // stores tile i+1 (in registers since step i-1) into buffer (i+1)&1 and issues tile i+2's
+  // loads into the same register stage, so a tile's loads have one step to arrive.  Against two
+  // register stages (tile i+1 stored after the multiply) this measured the same at config 3
+  // (81.6 us per layer) and 1.5% faster fused (86.9 against 88.3 us), with 9 fewer registers.
   auto has = [&](int i) __attribute__((always_inline)) { return i < iters && tile_of(i) < n_tiles; };
-  Stage s0, s1;
-  s0.flags = s1.flags = 0;
-  // Loads are unconditional (tiles past the end read page 0 and are never used): with a fixed
-  // number of loads per iteration, waiting for tile i+1 never waits for tile i+2.
+  Stage s0;
+  s0.flags = 0;
+  // Loads are unconditional (tiles past the end read page 0 and are never used), so every
+  // iteration waits for a fixed number of loads.
   load_tile(0, s0);
-  load_tile(1, s1);
 #pragma unroll
   for (int st = 0; st < kKSteps; ++st) asm volatile("" ::"v"(qreg[st]));  // query loads done before the loop
   // Per key group synchronisation: a group's G waves share its tiles and nothing else, so instead of
-  // a workgroup barrier per iteration each wave counts its completed tile stores in LDS (release) and
-  // waits for its group's count before reading a tile (acquire).  The wait is bounded (a safety net:
-  // both waves of a group run the same loop, so the count always arrives).
+  // a workgroup barrier per iteration each wave counts its finished steps in LDS (release) and
+  // waits for its group's count before the next step (acquire).  After the wait, every wave of the
+  // group has stored tile i and finished multiplying tile i-1, whose buffer tile i+1 reuses; no
+  // wave runs more than one step ahead of its group.  The wait is bounded (a safety net: the
+  // waves of a group run the same number of steps, so the count always arrives).  The
+  // config-3 prefill measured 82.6 us per layer this way against 85.5 us with a workgroup
+  // barrier per iteration.
   __shared__ int s_grp_cnt[C::kGroups];
   if (tid < C::kGroups) s_grp_cnt[tid] = 0;
   if (has(0)) store_tile(0, 0, s0);
-  __syncthreads();
   int cur_flags = s0.flags;
+  load_tile(1, s0);
+  __syncthreads();
   auto group_wait = [&](int target) __attribute__((always_inline)) {
     for (int spins = 0; spins < (1 << 20); ++spins) {
       if (__hip_atomic_load(&s_grp_cnt[grp], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
       __builtin_amdgcn_s_sleep(1);
     }
   };
-  auto step = [&](int i, Stage& next, Stage& free_stage) __attribute__((always_inline)) {
+  for (int i = 0; i < iters; ++i) {
     const int fl = cur_flags;
-    load_tile(i + 2, free_stage);
-    if (i > 0) group_wait(G * i);  // tile i stored by every wave of the group
+    if (i > 0) group_wait(G * i);  // every wave of the group has finished step i - 1
+    if (has(i + 1)) store_tile(i + 1, (i + 1) & 1, s0);
+    cur_flags = s0.flags;
+    load_tile(i + 2, s0);
     if (has(i)) compute_tile(i, i & 1, fl);
-    if (has(i + 1)) store_tile(i + 1, (i + 1) & 1, next);
-    cur_flags = next.flags;
     if (lane == 0) __hip_atomic_fetch_add(&s_grp_cnt[grp], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
-  };
-  for (int i = 0; i < iters; i += 2) {
-    step(i, s1, s0);
-    if (i + 1 < iters) step(i + 1, s0, s1);
   }
 
   __syncthreads();  // every group is done with the tile buffers, which the merge area reuses
