@@ -9,12 +9,14 @@
 // v_mfma_f32_32x32x16_f16 (32x32 output tile, K = 16 per instruction):
 //
 //  * Workgroup = (block of 32 queries, kv head), over every key the block can
-//    see -- no split across workgroups, so no partials leave the CU.  Its
-//    waves are G query heads x kGroups key groups: group k takes the 32-key
-//    tiles t = k, k + kGroups, ... (interleaved, so the causal diagonal costs
-//    every group the same), and the G waves of a group share each K/V tile
-//    staged in LDS.  At the end the groups merge log-sum-exp style through
-//    LDS.
+//    see; when those pairs cannot cover the CUs, up to kMaxSplit workgroups
+//    share a pair's key tiles (interleaved) and the last to finish merges
+//    their partials through the workspace.  The waves are G query heads x
+//    kGroups key groups: group k takes the 32-key tiles t = k, k + kGroups,
+//    ... of its workgroup (interleaved, so the causal diagonal costs every
+//    group the same), and the G waves of a group share each K/V tile staged
+//    in LDS.  At the end the groups merge log-sum-exp style through LDS, each
+//    wave finishing its own share of the head dims.
 //  * Tiles are double-buffered in LDS with one register stage: step i first
 //    moves tile i+1 from registers to the other LDS buffer and issues tile
 //    i+2's 16-byte global loads, then multiplies tile i.  A tile's K and V^T
@@ -465,65 +467,95 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
 
   __syncthreads();  // every group is done with the tile buffers, which the merge area reuses
   const float ltot = lsum + __shfl_xor(lsum, 32);
+  // From here on the work is spread over all waves: wave (grp, g) finishes the dims blocks dt of
+  // head g with dt % kGroups == grp -- the key groups' log-sum-exp merge, the key-split merge and
+  // the output stores.  (With group 0 doing all of it, the epilogue of a config-3 chunk took
+  // about 5.5 us.)  The arithmetic and its order are the same as one wave doing everything.
+  auto owns = [&](int dt) __attribute__((always_inline)) { return dt % C::kGroups == grp; };
   float mfin = m, lfin = ltot;
   if constexpr (C::kGroups > 1) {
-    // Log-sum-exp merge of the key groups through LDS: groups 1.. publish, group 0 combines.
-    float* mlb = reinterpret_cast<float*>(smem);                 // [wave][32][2]
-    float* accb = mlb + C::kWaves * 32 * 2;                       // [(grp-1)*G + g][dt][r][lane]
+    // Every wave publishes (m, l) and the blocks it does not own; LDS rows are 16 bytes per lane
+    // (4 consecutive accumulator entries), 1 KB per instruction.
+    float* mlb = reinterpret_cast<float*>(smem);  // [wave][32][2]
+    f32x4* accb = reinterpret_cast<f32x4*>(mlb + C::kWaves * 32 * 2);  // [g][dt][group other than dt's owner][4][lane]
+    auto blk = [&](int gg, int dt, int k, int r4) __attribute__((always_inline)) {
+      const int ko = k - (k > dt % C::kGroups ? 1 : 0);
+      return accb + (((gg * kDT + dt) * (C::kGroups - 1) + ko) * 4 + r4) * kWave + lane;
+    };
     if (half == 0) {
       mlb[(wave * 32 + col) * 2 + 0] = m;
       mlb[(wave * 32 + col) * 2 + 1] = ltot;
     }
-    if (grp > 0) {
 #pragma unroll
-      for (int dt = 0; dt < kDT; ++dt)
+    for (int dt = 0; dt < kDT; ++dt)
+      if (!owns(dt))
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          accb[((((grp - 1) * G + g) * kDT + dt) * 16 + r) * kWave + lane] = acc[dt][r];
-    }
+        for (int r4 = 0; r4 < 4; ++r4)
+          *blk(g, dt, grp, r4) = f32x4{acc[dt][4 * r4], acc[dt][4 * r4 + 1], acc[dt][4 * r4 + 2], acc[dt][4 * r4 + 3]};
     __syncthreads();
-    if (grp != 0) return;
-    float mxg = m;
+    float mk[C::kGroups], lk[C::kGroups];
 #pragma unroll
-    for (int k = 1; k < C::kGroups; ++k) mxg = fmaxf(mxg, mlb[((k * G + g) * 32 + col) * 2]);
-    const float w0 = exp2_fast(m - mxg);
-    float L = w0 * ltot;
+    for (int k = 0; k < C::kGroups; ++k) {
+      mk[k] = mlb[((k * G + g) * 32 + col) * 2];
+      lk[k] = mlb[((k * G + g) * 32 + col) * 2 + 1];
+    }
+    float mxg = mk[0];
 #pragma unroll
-    for (int dt = 0; dt < kDT; ++dt) acc[dt] *= w0;
+    for (int k = 1; k < C::kGroups; ++k) mxg = fmaxf(mxg, mk[k]);
+    float wk[C::kGroups];
 #pragma unroll
-    for (int k = 1; k < C::kGroups; ++k) {
-      const float wk = exp2_fast(mlb[((k * G + g) * 32 + col) * 2] - mxg);
-      L = fmaf(wk, mlb[((k * G + g) * 32 + col) * 2 + 1], L);
+    for (int k = 0; k < C::kGroups; ++k) wk[k] = exp2_fast(mk[k] - mxg);
+    float L = wk[0] * lk[0];
 #pragma unroll
-      for (int dt = 0; dt < kDT; ++dt)
+    for (int k = 1; k < C::kGroups; ++k) L = fmaf(wk[k], lk[k], L);
 #pragma unroll
-        for (int r = 0; r < 16; ++r)
-          acc[dt][r] = fmaf(wk, accb[((((k - 1) * G + g) * kDT + dt) * 16 + r) * kWave + lane], acc[dt][r]);
+    for (int dt = 0; dt < kDT; ++dt) {
+      if (!owns(dt)) continue;
+      f32x16 o;
+#pragma unroll
+      for (int k = 0; k < C::kGroups; ++k) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          f32x4 x;
+          if (k == grp)
+            x = f32x4{acc[dt][4 * r4], acc[dt][4 * r4 + 1], acc[dt][4 * r4 + 2], acc[dt][4 * r4 + 3]};
+          else
+            x = *blk(g, dt, k, r4);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) o[4 * r4 + e] = k == 0 ? x[e] * wk[0] : fmaf(wk[k], x[e], o[4 * r4 + e]);
+        }
+      }
+      acc[dt] = o;
     }
     mfin = mxg;
     lfin = L;
   }
 
   if (nsplit > 1 && !prefix_mode) {
-    // Cross-workgroup merge: publish this split's (m, l, O) for head g with device-coherent
-    // stores (lane-contiguous), wait for them, take the (query block, head) ticket; the last of
-    // the nsplit arrivals combines the others' partials with its own registers.
+    // Cross-workgroup merge: every wave publishes its blocks of this split's (m, l, O) for head g
+    // with device-coherent stores (lane-contiguous); once all are acknowledged, one thread per
+    // head takes the (query block, head) ticket.  The last of the nsplit arrivals combines the
+    // partials of every split, its own included (read back from memory), in split order, so the
+    // result does not depend on which workgroup arrived last.
+    __shared__ uint32_t s_ticket[G];
     constexpr int kSlotO = kDT * 16 * kWave;  // floats of O per (pair, split)
     const int64_t pair = (int64_t(qb) * num_kv_heads + kvh) * G + g;
     const int64_t slot = pair * nsplit + split;
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt)
+      if (owns(dt))
 #pragma unroll
-      for (int r = 0; r < 16; ++r) st_dev(ws.o + slot * kSlotO + (dt * 16 + r) * kWave + lane, acc[dt][r]);
-    st_dev(ws.ml + (slot * kWave + lane) * 2 + 0, mfin);
-    st_dev(ws.ml + (slot * kWave + lane) * 2 + 1, lfin);
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's partial is acknowledged
-    uint32_t t = 0;
-    if (lane == 0) t = __hip_atomic_fetch_add(ws.count + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    t = __builtin_amdgcn_readfirstlane(t);
-    if (t != uint32_t(nsplit - 1)) return;
-    // Combine every split's partial -- this wave's own included, read back from memory -- in
-    // split order, so the result does not depend on which workgroup arrived last.
+        for (int r = 0; r < 16; ++r) st_dev(ws.o + slot * kSlotO + (dt * 16 + r) * kWave + lane, acc[dt][r]);
+    if (grp == 0) {
+      st_dev(ws.ml + (slot * kWave + lane) * 2 + 0, mfin);
+      st_dev(ws.ml + (slot * kWave + lane) * 2 + 1, lfin);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are acknowledged
+    __syncthreads();                // ... and every other wave's
+    if (grp == 0 && lane == 0)
+      s_ticket[g] = __hip_atomic_fetch_add(ws.count + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_ticket[g] != uint32_t(nsplit - 1)) return;
     float mo[kMaxSplit], lo[kMaxSplit];
     float mx = kNegBig;
 #pragma unroll
@@ -536,46 +568,50 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
     }
     lfin = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < kDT; ++dt) acc[dt] = f32x16{};
+    for (int dt = 0; dt < kDT; ++dt)
+      if (owns(dt)) acc[dt] = f32x16{};
 #pragma unroll
     for (int s2 = 0; s2 < kMaxSplit; ++s2) {
       if (s2 < nsplit) {
-        const float wk = exp2_fast(mo[s2] - mx);
-        lfin = fmaf(wk, lo[s2], lfin);
+        const float wsp = exp2_fast(mo[s2] - mx);
+        lfin = fmaf(wsp, lo[s2], lfin);
         const float* so = ws.o + (pair * nsplit + s2) * kSlotO;
 #pragma unroll
         for (int dt = 0; dt < kDT; ++dt)
+          if (owns(dt))
 #pragma unroll
-          for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(wk, ld_dev(so + (dt * 16 + r) * kWave + lane), acc[dt][r]);
+            for (int r = 0; r < 16; ++r) acc[dt][r] = fmaf(wsp, ld_dev(so + (dt * 16 + r) * kWave + lane), acc[dt][r]);
       }
     }
     mfin = mx;  // acc and lfin are now relative to the maximum over all splits
-    if (lane == 0) reset_ticket(ws.count + pair);
+    if (grp == 0 && lane == 0) reset_ticket(ws.count + pair);
   }
 
   if (!q_ok) return;
   if (prefix_mode) {  // this split's unnormalised partial (row my_q, kv head kvh, head g)
     const int64_t pslot = ((int64_t(my_q) * num_kv_heads + kvh) * px.stride + split) * G + g;
-    if (half == 0) *reinterpret_cast<f32x2*>(px.ml + pslot * 2) = f32x2{mfin, lfin};
+    if (half == 0 && grp == 0) *reinterpret_cast<f32x2*>(px.ml + pslot * 2) = f32x2{mfin, lfin};
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt)
+      if (owns(dt))
 #pragma unroll
-      for (int a4 = 0; a4 < 4; ++a4)  // 4 consecutive dims per 16-byte store
-        *reinterpret_cast<f32x4*>(px.o + pslot * D + 32 * dt + 8 * a4 + 4 * half) =
-            f32x4{acc[dt][4 * a4], acc[dt][4 * a4 + 1], acc[dt][4 * a4 + 2], acc[dt][4 * a4 + 3]};
+        for (int a4 = 0; a4 < 4; ++a4)  // 4 consecutive dims per 16-byte store
+          *reinterpret_cast<f32x4*>(px.o + pslot * D + 32 * dt + 8 * a4 + 4 * half) =
+              f32x4{acc[dt][4 * a4], acc[dt][4 * a4 + 1], acc[dt][4 * a4 + 2], acc[dt][4 * a4 + 3]};
     return;
   }
   const float inv = lfin > 0.f ? 1.f / lfin : 0.f;
   f16* orow = out + (int64_t(my_q) * hq + head) * D;
 #pragma unroll
   for (int dt = 0; dt < kDT; ++dt)
+    if (owns(dt))
 #pragma unroll
-    for (int a4 = 0; a4 < 4; ++a4) {
-      const int d0 = 32 * dt + 8 * a4 + 4 * half;
-      *reinterpret_cast<f16x4*>(orow + d0) =
-          f16x4{f16(acc[dt][4 * a4] * inv), f16(acc[dt][4 * a4 + 1] * inv),
-                f16(acc[dt][4 * a4 + 2] * inv), f16(acc[dt][4 * a4 + 3] * inv)};
-    }
+      for (int a4 = 0; a4 < 4; ++a4) {
+        const int d0 = 32 * dt + 8 * a4 + 4 * half;
+        *reinterpret_cast<f16x4*>(orow + d0) =
+            f16x4{f16(acc[dt][4 * a4] * inv), f16(acc[dt][4 * a4 + 1] * inv),
+                  f16(acc[dt][4 * a4 + 2] * inv), f16(acc[dt][4 * a4 + 3] * inv)};
+      }
 }
 
 typedef void (*PrefillKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t,
