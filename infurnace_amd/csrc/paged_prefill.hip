@@ -181,9 +181,17 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
-  const int g = wave % G;
-  const int grp = wave / G;
-  const int gt = tid - grp * C::kGroupThreads;  // thread index inside the key group
+  // Waves w and w + 4 share a SIMD, whose issue arbitration favours the older one: with key group k
+  // made of waves G*k .. G*k + G - 1, groups 0 and 1 (waves 0-3) finished their tiles about 2 us
+  // before groups 2 and 3 at config 3.  So every key group takes as many older as younger waves
+  // (G = 2: waves w and 7 - w; G = 4: waves {0, 2, 5, 7} and {1, 3, 4, 6}), each SIMD still
+  // hosting two different groups; the groups then keep the same pace (config 3: 1-3% faster,
+  // same output).
+  const int hw = wave & 3, young = wave >> 2;
+  constexpr bool kMix = C::kWaves == 8 && C::kGroups > 1;
+  const int grp = !kMix ? wave / G : (G == 2 ? (young ? 3 - hw : hw) : ((hw + young) & 1));
+  const int g = !kMix ? wave % G : (G == 2 ? young : 2 * young + (hw >> 1));
+  const int gt = g * kWave + lane;  // thread index inside the key group
   const int hq = num_kv_heads * G;
   const int head = kvh * G + g;
   const bool prefix_mode = px.key_len > 0;
@@ -476,15 +484,15 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   if constexpr (C::kGroups > 1) {
     // Every wave publishes (m, l) and the blocks it does not own; LDS rows are 16 bytes per lane
     // (4 consecutive accumulator entries), 1 KB per instruction.
-    float* mlb = reinterpret_cast<float*>(smem);  // [wave][32][2]
+    float* mlb = reinterpret_cast<float*>(smem);  // [grp][g][32][2]
     f32x4* accb = reinterpret_cast<f32x4*>(mlb + C::kWaves * 32 * 2);  // [g][dt][group other than dt's owner][4][lane]
     auto blk = [&](int gg, int dt, int k, int r4) __attribute__((always_inline)) {
       const int ko = k - (k > dt % C::kGroups ? 1 : 0);
       return accb + (((gg * kDT + dt) * (C::kGroups - 1) + ko) * 4 + r4) * kWave + lane;
     };
     if (half == 0) {
-      mlb[(wave * 32 + col) * 2 + 0] = m;
-      mlb[(wave * 32 + col) * 2 + 1] = ltot;
+      mlb[((grp * G + g) * 32 + col) * 2 + 0] = m;
+      mlb[((grp * G + g) * 32 + col) * 2 + 1] = ltot;
     }
 #pragma unroll
     for (int dt = 0; dt < kDT; ++dt)
