@@ -106,38 +106,42 @@ class BlockPool:
 
     def retain(self, ids: Iterable[int], owner: str = "active") -> None:
         """Add one ``owner`` reference to each (allocated) page, e.g. a shared prefix."""
-        ids = list(ids)
         counts = self._owner(owner)
-        self._check_ids(ids)
-        for i in ids:
-            if self._is_free[i]:
-                raise BlockPoolError(f"block {i} is free; cannot retain it")
-        for i in ids:
-            counts[i] += 1
+        arr = self._as_ids(ids)
+        if arr.size and self._is_free[arr].any():
+            i = int(arr[np.argmax(self._is_free[arr])])
+            raise BlockPoolError(f"block {i} is free; cannot retain it")
+        np.add.at(counts, arr, 1)
 
     def free(self, ids: Iterable[int], owner: str = "active") -> list[int]:
         """Drop one ``owner`` reference per id; returns the pages that became free.
 
         Validated as a whole before anything changes, so a stale id or a double
         free leaves the pool untouched.  A page still held by another owner kind
-        (prefix cache, in-flight work) stays allocated.
+        (prefix cache, in-flight work) stays allocated.  Pages return to the free
+        list in the order of their last occurrence in ``ids``.
         """
-        ids = list(ids)
         counts = self._owner(owner)
-        self._check_ids(ids)
-        need: dict[int, int] = {}
-        for i in ids:
-            need[i] = need.get(i, 0) + 1
-        for i, k in need.items():
-            if counts[i] < k:
-                raise BlockPoolError(f"block {i} has {int(counts[i])} {owner} reference(s), cannot drop {k}")
-        released = []
-        for i in ids:
-            counts[i] -= 1
-            if not self._is_free[i] and all(c[i] == 0 for c in self._counts.values()):
-                self._is_free[i] = True
-                self._free.append(i)
-                released.append(i)
+        arr = self._as_ids(ids)
+        if arr.size == 0:
+            return []
+        uniq, need = np.unique(arr, return_counts=True)
+        short = counts[uniq] < need
+        if short.any():
+            j = int(np.argmax(short))
+            raise BlockPoolError(f"block {int(uniq[j])} has {int(counts[uniq[j]])} {owner} reference(s), "
+                                 f"cannot drop {int(need[j])}")
+        np.subtract.at(counts, arr, 1)
+        total = sum(c[uniq] for c in self._counts.values())
+        newly = uniq[(total == 0) & ~self._is_free[uniq]]
+        if newly.size == 0:
+            return []
+        # last occurrence of each id in ``ids``: the moment its count reached zero
+        rev_first = np.unique(arr[::-1], return_index=True)[1]
+        last = (arr.size - 1 - rev_first)[np.searchsorted(uniq, newly)]
+        released = [int(i) for i in newly[np.argsort(last, kind="stable")]]
+        self._is_free[released] = True
+        self._free.extend(released)
         return released
 
     def mark_in_flight(self, ids: Iterable[int]) -> None:
@@ -174,11 +178,28 @@ class BlockPool:
             raise BlockPoolError(f"unknown owner {owner!r}; expected one of {OWNERS}") from None
 
     def _check_ids(self, ids: Sequence[int]) -> None:
-        for i in ids:
-            if not isinstance(i, (int, np.integer)) or not 0 <= int(i) < self.num_blocks:
-                raise BlockPoolError(f"block id {i!r} outside [0, {self.num_blocks})")
-            if self.dummy_block is not None and int(i) == self.dummy_block:
+        self._as_ids(ids)
+
+    def _as_ids(self, ids: Iterable[int]) -> np.ndarray:
+        """``ids`` as an int64 array, every entry a valid, non-dummy page id (else BlockPoolError)."""
+        if isinstance(ids, np.ndarray):
+            arr = ids.reshape(-1)
+        else:
+            ids = list(ids)
+            for i in ids:
+                if not isinstance(i, (int, np.integer)) or isinstance(i, bool):
+                    raise BlockPoolError(f"block id {i!r} outside [0, {self.num_blocks})")
+            arr = np.asarray(ids, np.int64)
+        if arr.size and arr.dtype.kind not in "iu":
+            raise BlockPoolError(f"block ids must be integers, got dtype {arr.dtype}")
+        arr = arr.astype(np.int64, copy=False)
+        if arr.size:
+            bad = (arr < 0) | (arr >= self.num_blocks)
+            if bad.any():
+                raise BlockPoolError(f"block id {int(arr[np.argmax(bad)])} outside [0, {self.num_blocks})")
+            if self.dummy_block is not None and (arr == self.dummy_block).any():
                 raise BlockPoolError("the dummy block cannot be retained or freed")
+        return arr
 
     def build_block_table(self, seqs: Sequence[Sequence[int]], max_pages: int | None = None) -> np.ndarray:
         pad = 0 if self.dummy_block is None else self.dummy_block

@@ -56,12 +56,24 @@ __device__ __forceinline__ float dpp(float x) {
 constexpr int kDppXor1 = 0xB1;         // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;         // quad_perm [2,3,0,1]
 constexpr int kDppHalfMirror = 0x141;  // row_half_mirror: lane i <-> 7-i within 8 lanes
+constexpr int kDppMirror = 0x140;      // row_mirror: lane i <-> 15-i within 16 lanes
 
 // Sum over each aligned group of 8 lanes; every lane of the group gets the total.
 __device__ __forceinline__ float sum8(float x) {
   x += dpp<kDppXor1>(x);
   x += dpp<kDppXor2>(x);
   x += dpp<kDppHalfMirror>(x);
+  return x;
+}
+
+// Sum over each aligned group of N lanes (N = 4, 8 or 16); every lane of the group gets the total.
+template <int N>
+__device__ __forceinline__ float sum_lanes(float x) {
+  static_assert(N == 4 || N == 8 || N == 16, "DPP row reductions cover 4, 8 or 16 lanes");
+  x += dpp<kDppXor1>(x);
+  x += dpp<kDppXor2>(x);
+  if constexpr (N >= 8) x += dpp<kDppHalfMirror>(x);
+  if constexpr (N == 16) x += dpp<kDppMirror>(x);
   return x;
 }
 
@@ -97,29 +109,88 @@ __device__ __forceinline__ float ld_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Device-coherent 8- and 16-byte accesses through a buffer resource: the same sc1 cache policy
+// as st_dev / ld_dev (agent scope: written through to, and read from, the device coherence
+// point), one instruction per lane instead of one per float.  Offsets are in bytes; an offset
+// past the resource reads zero and writes nothing.
+constexpr int kCpolDevice = 16;  // cache-policy operand of the buffer builtins: sc1
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, int(bytes), 0x00020000);
+}
+__device__ __forceinline__ f32x4 ld_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kCpolDevice));
+}
+__device__ __forceinline__ f32x2 ld_dev2(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x2, __builtin_amdgcn_raw_buffer_load_b64(r, off, 0, kCpolDevice));
+}
+__device__ __forceinline__ void st_dev4(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kCpolDevice);
+}
+__device__ __forceinline__ void st_dev2(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x2 v) {
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, v), r, off, 0, kCpolDevice);
+}
+
+// Compiler-only barrier: no memory access is moved across it.  The split-KV handoff relies on
+// the order of relaxed device-scope accesses (partial stores, then the ticket, then the merge
+// loads); the hardware keeps that order (stores are acknowledged before s_waitcnt returns, and
+// the merge loads sit behind a branch on the ticket's value), and these barriers keep the
+// compiler from reordering them.
+__device__ __forceinline__ void compiler_fence() { asm volatile("" ::: "memory"); }
+
+// Waits until every memory access this wave issued has completed (stores acknowledged).
+__device__ __forceinline__ void wait_all_mem() {
+  compiler_fence();
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0)
+  compiler_fence();
+}
+
 // Called by all threads after their st_dev partial stores.  Waits until every store of
 // the workgroup is acknowledged, then one thread takes a ticket; returns true in the
 // workgroup that arrives last (ticket == last), which then merges with ld_dev.
 __device__ __forceinline__ bool arrive_last(uint32_t* counter, uint32_t last, uint32_t* s_ticket) {
-  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): stores acknowledged
+  wait_all_mem();
   __syncthreads();
   if (threadIdx.x == 0)
     *s_ticket = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  return *s_ticket == last;
+  const bool last_one = *s_ticket == last;
+  compiler_fence();
+  return last_one;
 }
 
 // Wave-level variant: each wavefront publishes and merges on its own (no workgroup barrier).
 __device__ __forceinline__ bool wave_arrive_last(uint32_t* counter, uint32_t last, int lane) {
-  __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores acknowledged
+  wait_all_mem();  // this wave's partial stores acknowledged
   uint32_t t = 0;
   if (lane == 0) t = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  return uint32_t(__builtin_amdgcn_readfirstlane(int(t))) == last;
+  const bool last_one = uint32_t(__builtin_amdgcn_readfirstlane(int(t))) == last;
+  compiler_fence();
+  return last_one;
 }
 
 __device__ __forceinline__ void reset_ticket(uint32_t* counter) {
   __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+
+// Split-KV workspace of the decode kernels: tickets (zero between calls), then the partial
+// states (m in log2 units, l) and unnormalised outputs of split segments.
+struct DecodeWorkspace {
+  uint32_t* count;  // one ticket per segment; every call returns the tickets it used to zero
+  float* ml;        // [slot][heads][2]
+  float* o;         // [slot][heads][head_dim]
+};
+
+// Fused append: store new_k / new_v of every active row at slot_mapping[row] (the store_kv
+// of the same step) inside the decode launch.  The attention reads the appended token from
+// new_k / new_v, not from the pool, so no ordering between the store and the reads is needed.
+struct DecodeAppend {
+  const f16* new_k;         // [batch][Hkv][D]
+  const f16* new_v;
+  const int32_t* slots;     // [batch]
+  f16* pool;                // the layer's pool (the same memory the kernel reads)
+};
+
+static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Number of CUs of the current device (queried once per device; 0 when there is none).
 inline int device_cu_count() {
@@ -145,6 +216,15 @@ int prefix_pass_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_
 int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
                 int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
                 int32_t stride, int cus, hipStream_t stream);
+
+// Whole-row decode (paged_decode_rows.hip), used by the decode entry points when the token row
+// (num_kv_heads x head_dim fp16) is 2 KiB and its (head_dim, group) is compiled.
+bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d);
+size_t rows_decode_ws_bytes(int32_t batch, int32_t hq, int32_t d, int blocks);
+int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
+                       int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
+                       int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
+                       const DecodeAppend& ap, bool cached, hipStream_t stream);
 
 }  // namespace ifn
 

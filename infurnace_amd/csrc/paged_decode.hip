@@ -48,11 +48,6 @@ constexpr int kMaxBatch = kRowInts - 1;
 constexpr int kMaxWaves = 1024 * kWavesPerBlock;  // waves of a launch are capped at this
 constexpr int kXcds = 8;            // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 
-struct DecodeWorkspace {
-  uint32_t* count;  // [batch * num_kv_heads] tickets, zero between calls
-  float* ml;        // [slot][G][2]  (max in log2 units, sum); slot = segment + wave
-  float* o;         // [slot][G][head_dim] unnormalised outputs
-};
 
 // Shared-prefix (cascade) mode: the first `pages` pages of every row at least pages * block_size
 // keys long (a cascade row) hold a prefix attended separately, for all rows at once.  For a
@@ -68,17 +63,6 @@ struct DecodePrefix {
   int32_t nstates;
 };
 
-// Fused append: store new_k / new_v of every active row at slot_mapping[row] (the store_kv
-// of the same step) inside the decode launch.  The attention reads the appended token from
-// new_k / new_v, not from the pool, so no ordering between the store and the reads is needed.
-struct DecodeAppend {
-  const f16* new_k;         // [batch][Hkv][D]
-  const f16* new_v;
-  const int32_t* slots;     // [batch]
-  f16* pool;                // the layer's pool (the same memory the kernel reads)
-};
-
-static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Workspace: [tickets: kTicketBytes][ml][o].  A launch of n waves publishes into at most
 // segments + n slots (slot = segment + range index).
@@ -643,11 +627,12 @@ __global__ __launch_bounds__(kDecodeThreads) void paged_decode_kernel(
     }
     if (pend_n == 0) return;
     // Tickets for the range's split segments (at most its first and last piece).
-    __builtin_amdgcn_s_waitcnt(0);  // every partial store of this wave acknowledged
+    wait_all_mem();  // every partial store of this wave acknowledged
     uint32_t t = 0;
     if (lane < pend_n)
       t = __hip_atomic_fetch_add(ws.count + (lane == 0 ? pend_seg0 : pend_seg1), 1u, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
+    compiler_fence();  // the merge loads below stay behind the ticket
     for (int i = 0; i < pend_n; ++i) {
       const uint32_t ti = uint32_t(__builtin_amdgcn_readlane(int(t), i));
       const int seg = i == 0 ? pend_seg0 : pend_seg1;
@@ -765,8 +750,11 @@ extern "C" size_t ifn_paged_decode_workspace_bytes(int32_t batch, int32_t num_q_
       max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
     return 0;
   size_t off_ml, off_o;
-  return ifn::decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
-                               int64_t(ifn::decode_blocks()) * ifn::kWavesPerBlock, &off_ml, &off_o);
+  const int blocks = ifn::decode_blocks();
+  const size_t per_head = ifn::decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
+                                                int64_t(blocks) * ifn::kWavesPerBlock, &off_ml, &off_o);
+  const size_t rows = ifn::rows_decode_ws_bytes(batch, num_q_heads, head_dim, blocks);
+  return per_head > rows ? per_head : rows;
 }
 
 namespace ifn {
@@ -790,9 +778,12 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
     return IFN_ERR_INVALID_ARGUMENT;
   if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
-  DecodeKernel k = pick_decode(head_dim, num_q_heads / num_kv_heads,
-                               append ? DecodeMode::kAppend : (cached ? DecodeMode::kPlainCached : DecodeMode::kPlain));
-  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
+  const bool rows = rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim);
+  DecodeKernel k = rows ? nullptr
+                        : pick_decode(head_dim, num_q_heads / num_kv_heads,
+                                      append ? DecodeMode::kAppend
+                                             : (cached ? DecodeMode::kPlainCached : DecodeMode::kPlain));
+  if (!rows && k == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);
@@ -803,17 +794,23 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
   if (batch == 0) return IFN_OK;
   const int blocks = decode_blocks();
   size_t off_ml, off_o;
-  const size_t need = decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
-                                       int64_t(blocks) * kWavesPerBlock, &off_ml, &off_o);
+  const size_t need = rows ? rows_decode_ws_bytes(batch, num_q_heads, head_dim, blocks)
+                           : decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
+                                              int64_t(blocks) * kWavesPerBlock, &off_ml, &off_o);
   if (workspace == nullptr || workspace_bytes < need) return IFN_ERR_WORKSPACE;
   IFN_CHECK_ALIGN16(workspace);
   if (device_cu_count() < 1) return IFN_ERR_HIP;
+  if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
+  if (rows)
+    return rows_decode_launch(static_cast<f16*>(out), static_cast<const f16*>(query),
+                              static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
+                              seq_lens, active_mask, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+                              scale * kLog2e, workspace, blocks, ap, cached, reinterpret_cast<hipStream_t>(stream));
   DecodeWorkspace ws;
   uint8_t* wsb = static_cast<uint8_t*>(workspace);
   ws.count = reinterpret_cast<uint32_t*>(wsb);
   ws.ml = reinterpret_cast<float*>(wsb + off_ml);
   ws.o = reinterpret_cast<float*>(wsb + off_o);
-  if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
   k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
@@ -888,9 +885,13 @@ extern "C" size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, 
     return 0;
   int cus = ifn::device_cu_count();
   if (cus < 1) cus = 256;
-  return ifn::shared_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
-                            int64_t(ifn::decode_blocks()) * ifn::kWavesPerBlock, shared_pages * block_size, cus)
-      .bytes;
+  const int blocks = ifn::decode_blocks();
+  const size_t shared = ifn::shared_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
+                                           int64_t(blocks) * ifn::kWavesPerBlock, shared_pages * block_size, cus)
+                            .bytes;
+  // shared_pages == 0 runs the plain decode (whole-row kernel where compiled)
+  const size_t rows = ifn::rows_decode_ws_bytes(batch, num_q_heads, head_dim, blocks);
+  return shared > rows ? shared : rows;
 }
 
 extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, const void* kv_pool_layer,

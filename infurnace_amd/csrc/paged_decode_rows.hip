@@ -1,0 +1,512 @@
+// Paged GQA decode over whole token rows (gfx950), for pools whose token row -- num_kv_heads x
+// head_dim fp16 -- is 2 KiB: Qwen3-0.6B and Qwen3-8B (8 KV heads x 128), and 4 x 256 / 16 x 64.
+//
+// Replaces the reference's documented paged_attention for decode
+// (docs/architecture.md:246; placeholder src/infurnace/kernels/paged_attention.py) whose contiguous
+// semantics are src/infurnace/executor/tinygrad/model.py:196-200: read positions [0, pos], upcast
+// fp16 K/V to fp32, scaled_dot_product_attention with scale 1/sqrt(head_dim) and query head h ->
+// kv head h / group.
+//
+// Decode is HBM-bound.  On MI355X a gather of 16-token pages reads fastest when every load
+// instruction takes whole, contiguous token rows, so this kernel is organised around rows:
+//
+//  * Workgroup ranges over the flat token list.  The tokens of all rows, row after row, form one
+//    list of T tokens; workgroup w (one per CU, 8 waves) takes tokens [T w / N, T (w+1) / N), so
+//    ragged batches cost every CU the same bytes.  Workgroups are remapped so that each XCD
+//    streams a contiguous eighth of the list.  A range is cut into pieces at row boundaries.
+//  * Inside a piece the 8 waves interleave by token: wave w takes positions a + w + 8 i, so at
+//    any moment the workgroup reads 8 consecutive token rows of one page (16 KiB of K and 16 KiB
+//    of V, contiguous).  A wave reads a whole token row -- every kv head -- with two 16-byte loads
+//    per lane for K and two for V: lane = (64 / Hkv) * kv_head + col holds 16-byte chunks col and
+//    col + 64 / Hkv of its head, so each load instruction reads 1 KiB in 128-byte runs.  The wave
+//    keeps an S-stage register ring of tokens in flight; page ids sit one per lane (64 per
+//    window) and are read with v_readlane.
+//  * q.k uses v_dot2_f32_f16 (fp32 accumulation) and a DPP reduction over the head's lanes; the
+//    online softmax runs in base 2 per (lane, query head of the kv head's group).  Each K/V row
+//    is fetched once and reused from registers by every query head of its GQA group.
+//  * At the end of a piece the 8 waves merge log-sum-exp style through LDS, so one state per
+//    (row, workgroup) leaves the CU.  A row held by one workgroup is written directly; a row split
+//    over several workgroups is merged by the workgroup that arrives last (device-coherent
+//    partial stores, one ticket per row, taken once at the end of the range).
+#include "ifn_common.hpp"
+
+namespace ifn {
+
+constexpr int kRowsWaves = 8;
+constexpr int kRowsThreads = kRowsWaves * kWave;
+constexpr int kRowsMaxBatch = 4096;  // rows per call (LDS token-offset table)
+constexpr int kRowsBlock = 16;       // tokens per page compiled in
+constexpr int kRowsXcds = 8;         // MI355X: workgroups dispatched round-robin over 8 XCDs
+constexpr int kMergeBatch = 20;      // split states loaded per round trip of the final merge
+// Cost of starting a row, in tokens.  A range that holds the end of one row and the start of the
+// next pays a second start-up, a second merge of its waves and possibly two split merges, so the
+// split counts each non-empty row as kRowStartCost tokens longer (virtual tokens in front of it).
+constexpr int kRowStartCost = 24;
+
+// Workspace: [tickets: kTicketBytes][ml][o].  Slot = row + range index: the workgroups holding a
+// row are consecutive ranges, so (row, range) -> row + range is unique and below batch + ranges.
+// A split state is (m, l) and the unnormalised output O, in fp32.
+static inline size_t rows_ws_layout(int32_t batch, int32_t hq, int32_t d, int64_t ranges, size_t* off_ml,
+                                    size_t* off_o) {
+  const size_t slots = size_t(batch) + size_t(ranges);
+  size_t off = kTicketBytes;
+  *off_ml = off;
+  off = align256(off + slots * hq * 2 * sizeof(float));
+  *off_o = off;
+  off = align256(off + slots * hq * d * sizeof(float));
+  return off;
+}
+
+// kAppend: the step's store_kv is fused in (ap); kStream: K/V row loads carry the non-temporal
+// hint (each row read once per launch; wrong when rows of the batch share pages).  S: tokens in
+// flight per wave.
+template <int D, int G, int HKV, int S, bool kAppend, bool kStream>
+__global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
+    f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
+    const int32_t* __restrict__ block_tables, int32_t max_pages, const int32_t* __restrict__ seq_lens,
+    const uint8_t* __restrict__ active, int32_t batch, int32_t max_len, float scale_log2, DecodeWorkspace ws,
+    DecodeAppend ap) {
+  constexpr int LPH = kWave / HKV;  // lanes per kv head
+  constexpr int ROW = HKV * D;      // fp16 elements per token row
+  constexpr int HQ = HKV * G;
+  constexpr int GR = G < 2 ? G : 2;  // query heads per kv head merged per LDS round
+  constexpr int D4 = D / 4;
+  static_assert(ROW == 2 * kWave * 8, "a token row is two 16-byte chunks per lane");
+  static_assert(G % GR == 0, "merge rounds cover the group");
+  __shared__ int s_cum[kRowsMaxBatch + 1];            // tokens of the rows before b
+  __shared__ int s_slot[kAppend ? kRowsMaxBatch : 1];  // appended slot of row b, -1 if none
+  __shared__ int s_wsum[kRowsWaves];
+  __shared__ float s_m[kRowsWaves][HQ];
+  __shared__ float s_l[kRowsWaves][HQ];
+  __shared__ f32x4 s_acc[kRowsWaves][HKV * GR][D4];
+  __shared__ uint32_t s_ticket[2];
+
+  const int tid = threadIdx.x;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+  const int lane = tid % kWave;
+  const int cap = min(max_pages * kRowsBlock, max_len);
+  const int64_t num_slots = num_pages * kRowsBlock;
+  auto row_len = [&](int b) -> int {  // keys of row b; inactive rows have none
+    const int sl = seq_lens[b];
+    const int act = active != nullptr ? int(active[b]) : 1;
+    return act != 0 ? max(0, min(sl, cap)) : 0;
+  };
+  auto append_slot = [&](int b) -> int {  // the slot row b appends to, -1 for none (store_kv's rule)
+    const int64_t sl = ap.slots[b];
+    const bool act = active == nullptr || active[b] != 0;
+    return act && sl >= 0 && sl < num_slots ? int(sl) : -1;
+  };
+
+  // Fused append: 16-byte chunks of every appended K and V row, spread over the grid.  No wave of
+  // this launch reads these slots (the attention takes the appended token from new_k / new_v).
+  // A thread's first chunk is loaded at launch and stored once the attention work is done.
+  constexpr int kAppChunks = ROW / 8;  // per row of K (and of V)
+  const int64_t app_items = kAppend ? int64_t(batch) * 2 * kAppChunks : 0;
+  auto app_src = [&](int64_t it) __attribute__((always_inline)) {
+    const int b = int(it / (2 * kAppChunks)), rem = int(it % (2 * kAppChunks));
+    return (rem / kAppChunks == 0 ? ap.new_k : ap.new_v) + int64_t(b) * ROW + (rem % kAppChunks) * 8;
+  };
+  auto app_dst = [&](int64_t it) __attribute__((always_inline)) -> f16* {  // null: nothing to store
+    const int b = int(it / (2 * kAppChunks)), rem = int(it % (2 * kAppChunks));
+    const int slot = s_slot[b];
+    return slot < 0 ? nullptr : ap.pool + (int64_t(rem / kAppChunks) * num_slots + slot) * ROW + (rem % kAppChunks) * 8;
+  };
+  const int64_t app_first = int64_t(blockIdx.x) * kRowsThreads + tid;
+  u32x4 app_data = u32x4{0u, 0u, 0u, 0u};
+  if constexpr (kAppend)
+    if (app_first < app_items) app_data = ld16(app_src(app_first));
+  auto flush_append = [&]() __attribute__((always_inline)) {
+    if constexpr (kAppend) {
+      if (app_first < app_items) {
+        f16* d0 = app_dst(app_first);
+        if (d0 != nullptr) st16(d0, app_data);
+      }
+      for (int64_t it = app_first + int64_t(gridDim.x) * kRowsThreads; it < app_items;
+           it += int64_t(gridDim.x) * kRowsThreads) {
+        f16* d = app_dst(it);
+        if (d != nullptr) st16(d, ld16(app_src(it)));
+      }
+    }
+  };
+
+  // 1. Offsets of the rows in the split's (virtual) token list, in LDS (every workgroup builds its
+  // own copy): row b occupies [s_cum[b], s_cum[b + 1]), its keys the last len of those positions
+  // (kRowStartCost virtual positions in front of every non-empty row).
+  int running = 0;
+  for (int base = 0; base < batch; base += kRowsThreads) {
+    const int i = base + tid;
+    int len = 0;
+    if (i < batch) {
+      len = row_len(i);
+      if (len > 0) len += kRowStartCost;
+      if constexpr (kAppend) s_slot[i] = append_slot(i);
+    }
+    int x = len;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == kWave - 1) s_wsum[wave] = x;
+    __syncthreads();
+    int wpre = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < kRowsWaves; ++w) {
+      const int v = s_wsum[w];
+      wpre += w < wave ? v : 0;
+      tot += v;
+    }
+    if (i < batch) s_cum[i] = running + wpre + x - len;
+    running += tot;
+    __syncthreads();
+  }
+  if (tid == 0) s_cum[batch] = running;
+  __syncthreads();
+
+  // Active rows with no keys get zeros (workgroup 0, one wave per row).
+  if (blockIdx.x == 0) {
+    for (int b = wave; b < batch; b += kRowsWaves) {
+      const bool live = active == nullptr || active[b] != 0;
+      if (live && s_cum[b + 1] == s_cum[b])
+        for (int i = lane; i < HQ * D; i += kWave) out[int64_t(b) * HQ * D + i] = f16(0.f);
+    }
+  }
+
+  // nr = min(workgroups, T) ranges, so that no range is empty (the split merge counts ranges).  A
+  // range may still hold no key (only virtual positions); it then has no piece and takes no ticket.
+  const int64_t T = running;
+  const int64_t nb = gridDim.x;
+  const int64_t nr = min(nb, T);
+  const int64_t blk = nb % kRowsXcds == 0 ? (blockIdx.x % kRowsXcds) * (nb / kRowsXcds) + blockIdx.x / kRowsXcds
+                                          : int64_t(blockIdx.x);
+  if (blk >= nr) {
+    flush_append();
+    return;
+  }
+  const int64_t t0 = T * blk / nr, t1 = T * (blk + 1) / nr;
+  // range holding flat token t: the largest r with T r / nr <= t
+  auto range_of = [&](int64_t t) -> int64_t { return ((t + 1) * nr - 1) / T; };
+  auto locate = [&](int64_t t) -> int {  // the row holding flat token t (t < T)
+    int lo = 0, hi = batch - 1;
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (s_cum[mid] <= t) lo = mid; else hi = mid - 1;
+    }
+    return __builtin_amdgcn_readfirstlane(lo);
+  };
+
+  // split partials: O [slot][HQ][D] and (m, l) [slot][HQ][2], slot < batch + gridDim.x
+  const uint32_t n_slots = uint32_t(batch) + gridDim.x;
+  const __amdgpu_buffer_rsrc_t r_o = make_rsrc(ws.o, n_slots * HQ * D * 4u);
+  const __amdgpu_buffer_rsrc_t r_ml = make_rsrc(ws.ml, n_slots * HQ * 2u * 4u);
+
+  const int hd = lane / LPH, col = lane % LPH;
+  const int off0 = hd * D + 8 * col, off1 = off0 + 8 * LPH;  // this lane's two chunks of a token row
+  const int64_t v_off = num_pages * kRowsBlock * int64_t(ROW);
+
+  int pend_n = 0, pend_b0 = 0, pend_b1 = 0, pend_f0 = 0, pend_f1 = 0, pend_np0 = 0, pend_np1 = 0;
+
+  for (int64_t t = t0; t < t1;) {  // one piece (row segment) per iteration; uniform over the workgroup
+    const int b = locate(t);
+    const int cb = s_cum[b] + kRowStartCost;  // position of the row's first key
+    const int len = s_cum[b + 1] - cb;
+    const int a = int(max<int64_t>(t, cb) - cb);
+    const int e = int(min<int64_t>(t1, int64_t(cb) + len) - cb);
+    if (a >= e) {  // only virtual positions of this row in the range
+      t = int64_t(cb) + e;
+      continue;
+    }
+    const int slot_b = kAppend ? s_slot[b] : -1;
+
+    // Query rows (b, hd * G + g), chunks col and col + LPH; the piece's page ids, one per lane.
+    f16x8 qv[G][2];
+    const f16* qrow = q + (int64_t(b) * HQ + hd * G) * D;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      qv[g][0] = as_h8(ld16(qrow + g * D + 8 * col));
+      qv[g][1] = as_h8(ld16(qrow + g * D + 8 * (col + LPH)));
+    }
+    const int pg0 = a / kRowsBlock;
+    const int npg = (e - 1) / kRowsBlock - pg0 + 1;
+    const int32_t* bt = block_tables + int64_t(b) * max_pages + pg0;
+    int ids0 = bt[min(lane, npg - 1)];
+    int ids1 = bt[min(lane + kWave, npg - 1)];
+    int cur_w = 0;
+
+    // this wave's tokens: positions a + wave + 8 i, i < nw
+    const int rem = e - a - wave;
+    const int nw = rem > 0 ? (rem + kRowsWaves - 1) / kRowsWaves : 0;
+    auto rel_page = [&](int i) { return (a + wave + kRowsWaves * i) / kRowsBlock - pg0; };
+    auto page_of = [&](int i) -> int {
+      const int rp = rel_page(i);
+      return (rp >> 6) == cur_w ? __builtin_amdgcn_readlane(ids0, rp & 63) : __builtin_amdgcn_readlane(ids1, rp & 63);
+    };
+    auto shift = [&](int i) {  // token i's page enters the next 64-page window of the piece
+      if ((rel_page(i) >> 6) != cur_w) {
+        ids0 = ids1;
+        ++cur_w;
+        ids1 = bt[min(kWave * (cur_w + 1) + lane, npg - 1)];
+      }
+    };
+    auto issue = [&](int i, u32x4 (&kr)[2], u32x4 (&vr)[2], bool& ok) {
+      const int p = a + wave + kRowsWaves * i;
+      const int phys = page_of(i);
+      ok = phys >= 0 && int64_t(phys) < num_pages;
+      const int64_t tok = int64_t(ok ? phys : 0) * kRowsBlock + p % kRowsBlock;
+      const f16* kb = pool + tok * ROW;
+      const f16* vb = pool + v_off + tok * ROW;
+      if constexpr (kAppend) {
+        if (ok && tok == slot_b) {  // the appended token (uniform): read it from new_k / new_v
+          kb = ap.new_k + int64_t(b) * ROW;
+          vb = ap.new_v + int64_t(b) * ROW;
+        }
+      }
+      kr[0] = kStream ? ld16_stream(kb + off0) : ld16(kb + off0);
+      kr[1] = kStream ? ld16_stream(kb + off1) : ld16(kb + off1);
+      vr[0] = kStream ? ld16_stream(vb + off0) : ld16(vb + off0);
+      vr[1] = kStream ? ld16_stream(vb + off1) : ld16(vb + off1);
+    };
+
+    float m[G], l[G], acc[G][16];
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      m[g] = kNegBig;
+      l[g] = 0.f;
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc[g][j] = 0.f;
+    }
+    auto consume = [&](u32x4 (&kr)[2], u32x4 (&vr)[2], bool ok) {
+      if (!ok) {  // a page id outside the pool contributes no key (uniform)
+        vr[0] = u32x4{0u, 0u, 0u, 0u};
+        vr[1] = u32x4{0u, 0u, 0u, 0u};
+      }
+      float vf[16];
+      const f16x8 v0 = as_h8(vr[0]), v1 = as_h8(vr[1]);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        vf[j] = float(v0[j]);
+        vf[8 + j] = float(v1[j]);
+      }
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float s = dot8(qv[g][0], as_h8(kr[0]), 0.f);
+        s = dot8(qv[g][1], as_h8(kr[1]), s);
+        s = sum_lanes<LPH>(s);
+        s = ok ? s * scale_log2 : -INFINITY;
+        const float mn = fmaxf(m[g], s);
+        const float alpha = exp2_fast(m[g] - mn);
+        const float pr = exp2_fast(s - mn);
+        l[g] = fmaf(l[g], alpha, pr);
+        m[g] = mn;
+#pragma unroll
+        for (int j = 0; j < 16; ++j) acc[g][j] = fmaf(pr, vf[j], acc[g][j] * alpha);
+      }
+    };
+
+    // S-stage register ring: token i + S - 1 is requested while token i is consumed.  The
+    // requests are unconditional (past the wave's last token they re-read that token, which the
+    // caches still hold), so the number of loads in flight is fixed and every wait counts exactly
+    // -- a conditional request would make the compiler wait for all loads before each token.
+    // The scheduling barriers keep the loads ahead of the arithmetic.
+    u32x4 kb_[S][2], vb_[S][2];
+    bool okb[S];
+    if (nw > 0) {
+#pragma unroll
+      for (int s = 0; s < S - 1; ++s) issue(min(s, nw - 1), kb_[s], vb_[s], okb[s]);
+      int i = 0;
+      for (; i + S <= nw; i += S) {
+#pragma unroll
+        for (int s = 0; s < S; ++s) {
+          shift(i + s);
+          const int sn = (s + S - 1) % S;
+          issue(min(i + s + S - 1, nw - 1), kb_[sn], vb_[sn], okb[sn]);
+          __builtin_amdgcn_sched_barrier(0);
+          consume(kb_[s], vb_[s], okb[s]);
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < S - 1; ++s)
+        if (i + s < nw) {
+          shift(i + s);
+          consume(kb_[s], vb_[s], okb[s]);
+        }
+    }
+
+    // Merge the 8 waves through LDS: (m, l) of every query head, then the accumulators in rounds of
+    // GR heads per kv head.  One thread per 4 output dims combines the waves' states.
+    if (col == 0) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        s_m[wave][hd * G + g] = m[g];
+        s_l[wave][hd * G + g] = l[g];
+      }
+    }
+    const bool whole = a == 0 && e == len;   // this workgroup holds the whole row
+    const int64_t slot = int64_t(b) + blk;   // split-partial slot of (row b, this range)
+#pragma unroll
+    for (int r = 0; r < G / GR; ++r) {
+#pragma unroll
+      for (int gg = 0; gg < GR; ++gg) {
+        const int g = r * GR + gg;
+        f32x4* dst = s_acc[wave][hd * GR + gg];
+        dst[2 * col] = f32x4{acc[g][0], acc[g][1], acc[g][2], acc[g][3]};
+        dst[2 * col + 1] = f32x4{acc[g][4], acc[g][5], acc[g][6], acc[g][7]};
+        dst[2 * (col + LPH)] = f32x4{acc[g][8], acc[g][9], acc[g][10], acc[g][11]};
+        dst[2 * (col + LPH) + 1] = f32x4{acc[g][12], acc[g][13], acc[g][14], acc[g][15]};
+      }
+      __syncthreads();
+      for (int idx = tid; idx < HKV * GR * D4; idx += kRowsThreads) {
+        const int hg = idx / D4, d4 = idx % D4;
+        const int qh = (hg / GR) * G + r * GR + hg % GR;
+        float mw[kRowsWaves];
+        float M = kNegBig;
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; ++w) {
+          mw[w] = s_m[w][qh];
+          M = fmaxf(M, mw[w]);
+        }
+        float L = 0.f;
+        f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int w = 0; w < kRowsWaves; ++w) {
+          const float wt = exp2_fast(mw[w] - M);
+          L = fmaf(wt, s_l[w][qh], L);
+          const f32x4 a4 = s_acc[w][hg][d4];
+          O = f32x4{fmaf(wt, a4[0], O[0]), fmaf(wt, a4[1], O[1]), fmaf(wt, a4[2], O[2]), fmaf(wt, a4[3], O[3])};
+        }
+        if (whole) {
+          const float inv = L > 0.f ? 1.f / L : 0.f;
+          *reinterpret_cast<f16x4*>(out + (int64_t(b) * HQ + qh) * D + 4 * d4) =
+              f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
+        } else {
+          st_dev4(r_o, uint32_t(((slot * HQ + qh) * D + 4 * d4) * 4), O);
+          if (d4 == 0) st_dev2(r_ml, uint32_t((slot * HQ + qh) * 2 * 4), f32x2{M, L});
+        }
+      }
+      __syncthreads();
+    }
+    if (!whole) {  // only the first and the last piece of a range can be split
+      const int first = int(range_of(cb)), last = int(range_of(int64_t(cb) + len - 1));
+      if (pend_n == 0) {
+        pend_b0 = b; pend_f0 = first; pend_np0 = last - first + 1;
+      } else {
+        pend_b1 = b; pend_f1 = first; pend_np1 = last - first + 1;
+      }
+      ++pend_n;
+    }
+    t = int64_t(cb) + e;
+  }
+
+  if (pend_n > 0) {
+    // Tickets for the range's split rows: every partial store of the workgroup acknowledged first.
+    wait_all_mem();
+    __syncthreads();
+    if (tid < pend_n)
+      s_ticket[tid] = __hip_atomic_fetch_add(ws.count + (tid == 0 ? pend_b0 : pend_b1), 1u, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    compiler_fence();  // the merge loads below stay behind the ticket
+    for (int k = 0; k < pend_n; ++k) {
+      const int np = k == 0 ? pend_np0 : pend_np1;
+      if (s_ticket[k] != uint32_t(np - 1)) continue;
+      const int b = k == 0 ? pend_b0 : pend_b1;
+      const int64_t slot0 = int64_t(b) + (k == 0 ? pend_f0 : pend_f1);
+      // Log-sum-exp merge of the row's np states (slots slot0 .. slot0 + np - 1, in range order).
+      // The D / 4 lanes of a query head (a lane group) share its (m, l) loads: lane j of the
+      // group loads state j's, the group reduces the maximum and the weights, and every lane
+      // reads a state's weight from its loader with a lane shuffle.  A lane then issues one
+      // 16-byte O load per state, kMergeBatch states per round trip.
+      constexpr int GL = D4 < kWave ? D4 : kWave;  // lanes sharing a query head
+      const int gbase = lane & ~(GL - 1), gj = lane - gbase;
+      for (int idx = tid; idx < HQ * D4; idx += kRowsThreads) {
+        const int qh = idx / D4, d4 = idx % D4;
+        float M = kNegBig, L = 0.f;
+        f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int j0 = 0; j0 < np; j0 += GL) {
+          const int cnt = min(GL, np - j0);
+          const f32x2 ml = ld_dev2(r_ml, uint32_t(((slot0 + j0 + min(gj, cnt - 1)) * HQ + qh) * 2 * 4));
+          const float mj = gj < cnt ? ml[0] : kNegBig;
+          float gm = mj;
+#pragma unroll
+          for (int o = 1; o < GL; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
+          const float nm = fmaxf(M, gm);
+          const float sc = exp2_fast(M - nm);
+          O = f32x4{O[0] * sc, O[1] * sc, O[2] * sc, O[3] * sc};
+          M = nm;
+          const float wj = gj < cnt ? exp2_fast(mj - M) : 0.f;
+          float ls = wj * ml[1];
+#pragma unroll
+          for (int o = 1; o < GL; o <<= 1) ls += __shfl_xor(ls, o);
+          L = fmaf(L, sc, ls);
+          for (int u0 = 0; u0 < cnt; u0 += kMergeBatch) {
+            f32x4 oj[kMergeBatch];
+#pragma unroll
+            for (int u = 0; u < kMergeBatch; ++u)
+              oj[u] = ld_dev4(r_o, uint32_t(((slot0 + j0 + min(u0 + u, cnt - 1)) * HQ + qh) * D * 4 + d4 * 16));
+#pragma unroll
+            for (int u = 0; u < kMergeBatch; ++u) {
+              const float w = __shfl(wj, gbase + min(u0 + u, cnt - 1));
+              if (u0 + u < cnt)
+                O = f32x4{fmaf(w, oj[u][0], O[0]), fmaf(w, oj[u][1], O[1]), fmaf(w, oj[u][2], O[2]),
+                          fmaf(w, oj[u][3], O[3])};
+            }
+          }
+        }
+        const float inv = L > 0.f ? 1.f / L : 0.f;
+        *reinterpret_cast<f16x4*>(out + (int64_t(b) * HQ + qh) * D + 4 * d4) =
+            f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
+      }
+      if (tid == 0) reset_ticket(ws.count + b);
+    }
+  }
+  flush_append();
+}
+
+typedef void (*RowsKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, const int32_t*,
+                           const uint8_t*, int32_t, int32_t, float, DecodeWorkspace, DecodeAppend);
+
+constexpr int kRowsStages = 2;
+
+static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream) {
+#define IFN_ROWS_CASE(DD, GG, HH)                                                                  \
+  if (d == DD && g == GG && hkv == HH) {                                                           \
+    if (append) return decode_rows_kernel<DD, GG, HH, kRowsStages, true, true>;                    \
+    return stream ? decode_rows_kernel<DD, GG, HH, kRowsStages, false, true>                       \
+                  : decode_rows_kernel<DD, GG, HH, kRowsStages, false, false>;                     \
+  }
+  IFN_ROWS_CASE(128, 1, 8) IFN_ROWS_CASE(128, 2, 8) IFN_ROWS_CASE(128, 4, 8)
+  IFN_ROWS_CASE(64, 1, 16) IFN_ROWS_CASE(64, 2, 16)
+  IFN_ROWS_CASE(256, 1, 4) IFN_ROWS_CASE(256, 2, 4)
+#undef IFN_ROWS_CASE
+  return nullptr;
+}
+
+bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d) {
+  return batch <= kRowsMaxBatch && hq % hkv == 0 && batch <= kMaxTickets &&
+         pick_rows(d, hq / hkv, hkv, false, true) != nullptr;
+}
+
+size_t rows_decode_ws_bytes(int32_t batch, int32_t hq, int32_t d, int blocks) {
+  size_t off_ml, off_o;
+  return rows_ws_layout(batch, hq, d, blocks, &off_ml, &off_o);
+}
+
+int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
+                       int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
+                       int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
+                       const DecodeAppend& ap, bool cached, hipStream_t stream) {
+  RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached);
+  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
+  size_t off_ml, off_o;
+  rows_ws_layout(batch, hq, d, blocks, &off_ml, &off_o);
+  uint8_t* wsb = static_cast<uint8_t*>(workspace);
+  DecodeWorkspace ws;
+  ws.count = reinterpret_cast<uint32_t*>(wsb);
+  ws.ml = reinterpret_cast<float*>(wsb + off_ml);
+  ws.o = reinterpret_cast<float*>(wsb + off_o);
+  k<<<dim3(unsigned(blocks)), dim3(kRowsThreads), 0, stream>>>(out, q, pool, num_pages, block_tables, max_pages,
+                                                                seq_lens, active, batch, max_len, scale_log2, ws, ap);
+  return ifn_launch_status();
+}
+
+}  // namespace ifn

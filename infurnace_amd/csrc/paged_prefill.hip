@@ -558,12 +558,13 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
       st_dev(ws.ml + (slot * kWave + lane) * 2 + 0, mfin);
       st_dev(ws.ml + (slot * kWave + lane) * 2 + 1, lfin);
     }
-    __builtin_amdgcn_s_waitcnt(0);  // this wave's stores are acknowledged
-    __syncthreads();                // ... and every other wave's
+    wait_all_mem();   // this wave's stores are acknowledged
+    __syncthreads();  // ... and every other wave's
     if (grp == 0 && lane == 0)
       s_ticket[g] = __hip_atomic_fetch_add(ws.count + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     if (s_ticket[g] != uint32_t(nsplit - 1)) return;
+    compiler_fence();  // the merge loads below stay behind the ticket
     float mo[kMaxSplit], lo[kMaxSplit];
     float mx = kNegBig;
 #pragma unroll
