@@ -105,8 +105,8 @@ size_t ifn_paged_decode_workspace_bytes(int32_t batch, int32_t num_q_heads, int3
  * Rows with active_mask[b] == 0 write nothing.  An active row with L == 0
  * writes zeros.  L is clamped to [0, max_pages_per_seq * block_size] and to
  * max_seq_len; a page id outside [0, num_pages) contributes no keys (no
- * out-of-bounds read).  max_seq_len is the host-side upper bound of seq_lens
- * that sizes the launch and the workspace.
+ * out-of-bounds read).  max_seq_len must be an upper bound of seq_lens: every
+ * row's length is clamped to it, so a smaller value truncates attention.
  * Page loads are streamed (non-temporal hint): each page is expected to be read
  * by one row of the batch.  Batches whose rows share pages go through
  * ifn_paged_decode_shared_prefix (shared_pages == 0 when the shared pages are
@@ -147,6 +147,57 @@ int ifn_paged_decode_append(void* out, const void* query, void* kv_pool_layer, i
                             int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
                             int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
                             size_t workspace_bytes, void* stream);
+
+/*
+ * Step plan of a decode batch.  Every layer of a decode step attends with the
+ * same block_tables, seq_lens, active_mask and (for the fused append)
+ * slot_mapping; the split of the batch's keys over the CUs depends on nothing
+ * else.  ifn_paged_decode_plan computes it once into `plan` (a device buffer
+ * of ifn_paged_decode_plan_bytes), and the *_planned entry points below then
+ * start each workgroup's page loads one round trip after launch instead of
+ * three.  A plan is valid for calls with exactly the inputs it was built
+ * from; it holds no pointers, so it may be built on one stream and used on
+ * another once ordered after it.  plan_bytes == 0 means these shapes decode
+ * without a plan (the planned entry points then ignore it).  slot_mapping may
+ * be NULL for a plan used only by ifn_paged_decode_planned; a plan used by
+ * ifn_paged_decode_append_planned must be built with the step's slots (else
+ * that call computes the split itself).
+ * Replaces: nothing in the reference (its decode step recomputes nothing per
+ * layer because its SDPA reads contiguous rows, model.py:196-200); this is
+ * the per-step half of paged_attention's decode (docs/architecture.md:246).
+ */
+size_t ifn_paged_decode_plan_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                   int32_t head_dim, int32_t block_size, int32_t max_pages_per_seq,
+                                   int32_t max_seq_len);
+int ifn_paged_decode_plan(void* plan, size_t plan_bytes, const int32_t* block_tables,
+                          int32_t max_pages_per_seq, const int32_t* seq_lens, const uint8_t* active_mask,
+                          const int32_t* slot_mapping, int64_t num_pages, int32_t batch,
+                          int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                          int32_t block_size, int32_t max_seq_len, void* stream);
+
+/*
+ * ifn_paged_decode and ifn_paged_decode_append with a step plan (NULL: none).
+ * Same arguments, results and workspace otherwise; the output is bit-identical
+ * to the unplanned call.  A plan built for other shapes or another batch size
+ * is detected and ignored; one built from other lengths or tables of the same
+ * shapes is not, and gives wrong results.
+ * Replaces: paged_attention (decode), docs/architecture.md:246, and store_kv
+ * then paged_attention (docs/architecture.md:245-246), as the unplanned calls.
+ */
+int ifn_paged_decode_planned(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                             const int32_t* block_tables, int32_t max_pages_per_seq,
+                             const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t block_size, int32_t max_seq_len, float scale, const void* plan,
+                             size_t plan_bytes, void* workspace, size_t workspace_bytes, void* stream);
+int ifn_paged_decode_append_planned(void* out, const void* query, void* kv_pool_layer, int64_t num_pages,
+                                    const int32_t* block_tables, int32_t max_pages_per_seq,
+                                    const int32_t* seq_lens, const uint8_t* active_mask,
+                                    const int32_t* slot_mapping, const void* new_k, const void* new_v,
+                                    int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                    int32_t head_dim, int32_t block_size, int32_t max_seq_len, float scale,
+                                    const void* plan, size_t plan_bytes, void* workspace,
+                                    size_t workspace_bytes, void* stream);
 
 /* Workspace bytes ifn_paged_decode_shared_prefix needs for these shapes. */
 size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num_q_heads,

@@ -218,13 +218,17 @@ int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t*
                 int32_t stride, int cus, hipStream_t stream);
 
 // Whole-row decode (paged_decode_rows.hip), used by the decode entry points when the token row
-// (num_kv_heads x head_dim fp16) is 2 KiB and its (head_dim, group) is compiled.
-bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d);
+// (num_kv_heads x head_dim fp16) is 2 KiB and its (head_dim, group) is compiled; and its step plan.
+bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t max_pages, int32_t max_len);
 size_t rows_decode_ws_bytes(int32_t batch, int32_t hq, int32_t d, int blocks);
+size_t rows_plan_bytes(int32_t batch, int blocks);
+int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
+                     const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
+                     int blocks, hipStream_t stream);
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
-                       const DecodeAppend& ap, bool cached, hipStream_t stream);
+                       const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream);
 
 }  // namespace ifn
 

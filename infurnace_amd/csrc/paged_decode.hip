@@ -766,7 +766,8 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
                         const int32_t* block_tables, int32_t max_pages_per_seq, const int32_t* seq_lens,
                         const uint8_t* active_mask, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                         int32_t head_dim, int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
-                        size_t workspace_bytes, void* stream, const DecodeAppend& ap, bool cached = false) {
+                        size_t workspace_bytes, void* stream, const DecodeAppend& ap, bool cached = false,
+                        const void* plan = nullptr, size_t plan_bytes = 0) {
   const bool append = ap.pool != nullptr;
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_tables == nullptr ||
       seq_lens == nullptr)
@@ -778,7 +779,7 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
     return IFN_ERR_INVALID_ARGUMENT;
   if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
-  const bool rows = rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim);
+  const bool rows = rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len);
   DecodeKernel k = rows ? nullptr
                         : pick_decode(head_dim, num_q_heads / num_kv_heads,
                                       append ? DecodeMode::kAppend
@@ -801,11 +802,17 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
   IFN_CHECK_ALIGN16(workspace);
   if (device_cu_count() < 1) return IFN_ERR_HIP;
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
-  if (rows)
+  if (rows) {
+    if (plan != nullptr) {  // the kernel reads this workgroup's record before checking the header
+      if (plan_bytes < rows_plan_bytes(batch, blocks)) return IFN_ERR_WORKSPACE;
+      IFN_CHECK_ALIGN16(plan);
+    }
     return rows_decode_launch(static_cast<f16*>(out), static_cast<const f16*>(query),
                               static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
                               seq_lens, active_mask, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
-                              scale * kLog2e, workspace, blocks, ap, cached, reinterpret_cast<hipStream_t>(stream));
+                              scale * kLog2e, workspace, blocks, ap, cached, static_cast<const int32_t*>(plan),
+                              reinterpret_cast<hipStream_t>(stream));
+  }
   DecodeWorkspace ws;
   uint8_t* wsb = static_cast<uint8_t*>(workspace);
   ws.count = reinterpret_cast<uint32_t*>(wsb);
@@ -846,6 +853,68 @@ extern "C" int ifn_paged_decode_append(void* out, const void* query, void* kv_po
                            workspace, workspace_bytes, stream,
                            ifn::DecodeAppend{static_cast<const ifn::f16*>(new_k), static_cast<const ifn::f16*>(new_v),
                                              slot_mapping, static_cast<ifn::f16*>(kv_pool_layer)});
+}
+
+extern "C" size_t ifn_paged_decode_plan_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                              int32_t head_dim, int32_t block_size, int32_t max_pages_per_seq,
+                                              int32_t max_seq_len) {
+  if (batch < 1 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 || block_size != ifn::kBlock ||
+      num_q_heads % num_kv_heads != 0 || max_pages_per_seq < 1 || max_seq_len < 0)
+    return 0;
+  if (!ifn::rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len))
+    return 0;
+  return ifn::rows_plan_bytes(batch, ifn::decode_blocks());
+}
+
+extern "C" int ifn_paged_decode_plan(void* plan, size_t plan_bytes, const int32_t* block_tables,
+                                     int32_t max_pages_per_seq, const int32_t* seq_lens, const uint8_t* active_mask,
+                                     const int32_t* slot_mapping, int64_t num_pages, int32_t batch,
+                                     int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                     int32_t max_seq_len, void* stream) {
+  using namespace ifn;
+  if (block_tables == nullptr || seq_lens == nullptr) return IFN_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || num_pages < 1 || max_pages_per_seq < 1 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 ||
+      max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
+  if (batch == 0) return IFN_OK;
+  if (!rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len))
+    return IFN_OK;  // these shapes decode without a plan; the planned entry points ignore it
+  const int blocks = decode_blocks();
+  if (plan == nullptr || plan_bytes < rows_plan_bytes(batch, blocks)) return IFN_ERR_WORKSPACE;
+  IFN_CHECK_ALIGN16(plan);
+  if (device_cu_count() < 1) return IFN_ERR_HIP;
+  return rows_plan_launch(static_cast<int32_t*>(plan), block_tables, max_pages_per_seq, seq_lens, active_mask,
+                          slot_mapping, num_pages, batch, max_seq_len, blocks, reinterpret_cast<hipStream_t>(stream));
+}
+
+extern "C" int ifn_paged_decode_planned(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                                        const int32_t* block_tables, int32_t max_pages_per_seq,
+                                        const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                                        int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t block_size, int32_t max_seq_len, float scale, const void* plan,
+                                        size_t plan_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+  return ifn::decode_entry(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                           active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
+                           workspace, workspace_bytes, stream, ifn::DecodeAppend{nullptr, nullptr, nullptr, nullptr},
+                           false, plan, plan_bytes);
+}
+
+extern "C" int ifn_paged_decode_append_planned(void* out, const void* query, void* kv_pool_layer, int64_t num_pages,
+                                               const int32_t* block_tables, int32_t max_pages_per_seq,
+                                               const int32_t* seq_lens, const uint8_t* active_mask,
+                                               const int32_t* slot_mapping, const void* new_k, const void* new_v,
+                                               int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                               int32_t head_dim, int32_t block_size, int32_t max_seq_len, float scale,
+                                               const void* plan, size_t plan_bytes, void* workspace,
+                                               size_t workspace_bytes, void* stream) {
+  if (kv_pool_layer == nullptr) return IFN_ERR_INVALID_ARGUMENT;
+  return ifn::decode_entry(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                           active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
+                           workspace, workspace_bytes, stream,
+                           ifn::DecodeAppend{static_cast<const ifn::f16*>(new_k), static_cast<const ifn::f16*>(new_v),
+                                             slot_mapping, static_cast<ifn::f16*>(kv_pool_layer)},
+                           false, plan, plan_bytes);
 }
 
 namespace ifn {

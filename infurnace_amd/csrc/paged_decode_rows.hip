@@ -11,9 +11,12 @@
 // instruction takes whole, contiguous token rows, so this kernel is organised around rows:
 //
 //  * Workgroup ranges over the flat token list.  The tokens of all rows, row after row, form one
-//    list of T tokens; workgroup w (one per CU, 8 waves) takes tokens [T w / N, T (w+1) / N), so
-//    ragged batches cost every CU the same bytes.  Workgroups are remapped so that each XCD
-//    streams a contiguous eighth of the list.  A range is cut into pieces at row boundaries.
+//    list; workgroup w (one per CU, 8 waves) takes positions [T w / N, T (w+1) / N), so ragged
+//    batches cost every CU the same bytes.  Every non-empty row is counted kRowStartCost
+//    positions longer than its keys (virtual positions in front of it): a range that ends one
+//    row and starts the next pays a second start-up and merge, and gets that many keys fewer.
+//    Workgroups are remapped so that each XCD streams a contiguous eighth of the list.  A range is
+//    cut into pieces at row boundaries.
 //  * Inside a piece the 8 waves interleave by token: wave w takes positions a + w + 8 i, so at
 //    any moment the workgroup reads 8 consecutive token rows of one page (16 KiB of K and 16 KiB
 //    of V, contiguous).  A wave reads a whole token row -- every kv head -- with two 16-byte loads
@@ -27,14 +30,19 @@
 //  * At the end of a piece the 8 waves merge log-sum-exp style through LDS, so one state per
 //    (row, workgroup) leaves the CU.  A row held by one workgroup is written directly; a row split
 //    over several workgroups is merged by the workgroup that arrives last (device-coherent
-//    partial stores, one ticket per row, taken once at the end of the range).
+//    16-byte state stores, one ticket per row, taken once at the end of the range).
+//  * Optional step plan (decode_plan_kernel): the split depends only on the lengths, the tables
+//    and the appended slots, which every layer of a decode step shares.  Built once per step, the
+//    plan holds the rows' offsets in the token list and, per range, its first pieces and first
+//    64 page ids, so a workgroup starts its first K/V loads one round trip after launch instead
+//    of three (lengths -> offsets -> page ids -> rows).
 #include "ifn_common.hpp"
 
 namespace ifn {
 
 constexpr int kRowsWaves = 8;
 constexpr int kRowsThreads = kRowsWaves * kWave;
-constexpr int kRowsMaxBatch = 4096;  // rows per call (LDS token-offset table)
+constexpr int kRowsMaxBatch = 4096;  // rows per call (LDS offset table)
 constexpr int kRowsBlock = 16;       // tokens per page compiled in
 constexpr int kRowsXcds = 8;         // MI355X: workgroups dispatched round-robin over 8 XCDs
 constexpr int kMergeBatch = 20;      // split states loaded per round trip of the final merge
@@ -42,6 +50,19 @@ constexpr int kMergeBatch = 20;      // split states loaded per round trip of th
 // next pays a second start-up, a second merge of its waves and possibly two split merges, so the
 // split counts each non-empty row as kRowStartCost tokens longer (virtual tokens in front of it).
 constexpr int kRowStartCost = 24;
+
+// Step plan (int32 words).  Header: magic, batch, ranges nr, virtual positions T, grid, whether
+// appended slots were given, the row-length cap, 0.  Then the rows' offsets cum[batch + 1], then one
+// record per workgroup range: [0] pieces of the range; [1 + 6 p ..] piece p < kPlanPieces: row,
+// first key a, end key e, first range of the row, ranges of the row, appended slot of the row;
+// [64 + i] page id i of the first piece's first window.
+constexpr int32_t kPlanMagic = 0x504c4e31;
+constexpr int kPlanHdr = 16;
+constexpr int kPlanRec = 128;
+constexpr int kPlanPieces = 3;
+constexpr int kPlanIds = 64;
+static inline __host__ __device__ int64_t plan_rec0(int32_t batch) { return (kPlanHdr + batch + 1 + 63) / 64 * 64; }
+static inline size_t plan_words(int32_t batch, int blocks) { return size_t(plan_rec0(batch) + int64_t(blocks) * kPlanRec); }
 
 // Workspace: [tickets: kTicketBytes][ml][o].  Slot = row + range index: the workgroups holding a
 // row are consecutive ranges, so (row, range) -> row + range is unique and below batch + ranges.
@@ -57,15 +78,162 @@ static inline size_t rows_ws_layout(int32_t batch, int32_t hq, int32_t d, int64_
   return off;
 }
 
+// Keys of row b (0 for inactive rows), clamped to cap; and the slot its appended token goes to
+// (-1 for none: inactive rows and slots outside the pool store nothing, as store_kv).
+__device__ __forceinline__ int row_keys(const int32_t* seq_lens, const uint8_t* active, int b, int cap) {
+  const int sl = seq_lens[b];
+  const int act = active != nullptr ? int(active[b]) : 1;
+  return act != 0 ? max(0, min(sl, cap)) : 0;
+}
+__device__ __forceinline__ int row_slot(const int32_t* slots, const uint8_t* active, int b, int64_t num_slots) {
+  const int64_t sl = slots[b];
+  const bool act = active == nullptr || active[b] != 0;
+  return act && sl >= 0 && sl < num_slots ? int(sl) : -1;
+}
+
+// Offsets of the rows in the split's virtual token list, into s_cum[0 .. batch] (all threads of the
+// workgroup call it; returns the total).  Row b occupies [s_cum[b], s_cum[b + 1]); its keys are the
+// last of those positions, after kRowStartCost virtual ones when it has any.
+__device__ __forceinline__ int build_offsets(int* s_cum, int* s_wsum, const int32_t* seq_lens,
+                                             const uint8_t* active, int batch, int cap) {
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, nwaves = blockDim.x / kWave;
+  int running = 0;
+  for (int base = 0; base < batch; base += blockDim.x) {
+    const int i = base + tid;
+    int len = i < batch ? row_keys(seq_lens, active, i, cap) : 0;
+    if (len > 0) len += kRowStartCost;
+    int x = len;
+#pragma unroll
+    for (int o = 1; o < kWave; o <<= 1) {
+      const int y = __shfl_up(x, o);
+      if (lane >= o) x += y;
+    }
+    if (lane == kWave - 1) s_wsum[wave] = x;
+    __syncthreads();
+    int wpre = 0, tot = 0;
+    for (int w = 0; w < nwaves; ++w) {
+      const int v = s_wsum[w];
+      wpre += w < wave ? v : 0;
+      tot += v;
+    }
+    if (i < batch) s_cum[i] = running + wpre + x - len;
+    running += tot;
+    __syncthreads();
+  }
+  if (tid == 0) s_cum[batch] = running;
+  __syncthreads();
+  return running;
+}
+
+// The row holding virtual position t (t < s_cum[batch]): the last b with s_cum[b] <= t, which skips
+// rows without keys.
+__device__ __forceinline__ int locate_row(const int* s_cum, int batch, int64_t t) {
+  int lo = 0, hi = batch - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (s_cum[mid] <= t) lo = mid; else hi = mid - 1;
+  }
+  return lo;
+}
+
+// A piece: keys [a, e) of row b, in range `first` .. first + nranges - 1 of the row's ranges, and
+// the row's appended slot.
+struct RowPiece {
+  int b, a, e, first, nranges, slot;
+};
+
+// Step plan: one workgroup writes the header, the offsets and every range's record.
+constexpr int kPlanThreads = 1024;
+__global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
+    int32_t* __restrict__ plan, const int32_t* __restrict__ block_tables, int32_t max_pages,
+    const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, const int32_t* __restrict__ slots,
+    int64_t num_pages, int32_t batch, int32_t max_len, int32_t nb) {
+  __shared__ int s_cum[kRowsMaxBatch + 1];
+  __shared__ int s_wsum[kPlanThreads / kWave];
+  __shared__ int s_p0[3][kPlanThreads];  // first piece of range r: row, a, e (rows < 0: none)
+  const int tid = threadIdx.x;
+  const int cap = min(max_pages * kRowsBlock, max_len);
+  const int T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap);
+  const int nr = int(min<int64_t>(nb, T));
+  if (tid == 0) {
+    plan[0] = kPlanMagic;
+    plan[1] = batch;
+    plan[2] = nr;
+    plan[3] = T;
+    plan[4] = nb;
+    plan[5] = slots != nullptr ? 1 : 0;
+    plan[6] = cap;
+    plan[7] = 0;
+  }
+  for (int i = tid; i <= batch; i += kPlanThreads) plan[kPlanHdr + i] = s_cum[i];
+  int32_t* recs = plan + plan_rec0(batch);
+  const int64_t num_slots = num_pages * kRowsBlock;
+  for (int r = tid; r < nb; r += kPlanThreads) {
+    int32_t* rec = recs + int64_t(r) * kPlanRec;
+    int n = 0;
+    int p0b = -1, p0a = 0, p0e = 0;
+    if (r < nr) {
+      const int64_t t0 = int64_t(T) * r / nr, t1 = int64_t(T) * (r + 1) / nr;
+      auto range_of = [&](int64_t t) -> int { return int(((t + 1) * nr - 1) / T); };
+      int b = locate_row(s_cum, batch, t0);
+      while (b < batch) {
+        const int cb = s_cum[b] + kRowStartCost;
+        const int len = s_cum[b + 1] - cb;
+        if (len > 0) {
+          if (cb >= t1) break;
+          const int a = int(max<int64_t>(t0, cb) - cb);
+          const int e = int(min<int64_t>(t1, int64_t(cb) + len) - cb);
+          if (a < e) {
+            if (n < kPlanPieces) {
+              int32_t* pc = rec + 1 + 6 * n;
+              const int first = range_of(cb);
+              pc[0] = b;
+              pc[1] = a;
+              pc[2] = e;
+              pc[3] = first;
+              pc[4] = range_of(int64_t(cb) + len - 1) - first + 1;
+              pc[5] = slots != nullptr ? row_slot(slots, active, b, num_slots) : -1;
+            }
+            if (n == 0) {
+              p0b = b;
+              p0a = a;
+              p0e = e;
+            }
+            ++n;
+          }
+          if (int64_t(cb) + len >= t1) break;
+        }
+        ++b;
+      }
+    }
+    rec[0] = n;
+    s_p0[0][r] = p0b;
+    s_p0[1][r] = p0a;
+    s_p0[2][r] = p0e;
+  }
+  __syncthreads();
+  for (int it = tid; it < nb * kPlanIds; it += kPlanThreads) {
+    const int r = it / kPlanIds, i = it % kPlanIds;
+    const int b = s_p0[0][r];
+    int id = 0;
+    if (b >= 0) {
+      const int pg0 = s_p0[1][r] / kRowsBlock;
+      const int npg = (s_p0[2][r] - 1) / kRowsBlock - pg0 + 1;
+      id = block_tables[int64_t(b) * max_pages + pg0 + min(i, npg - 1)];
+    }
+    recs[int64_t(r) * kPlanRec + 64 + i] = id;
+  }
+}
+
 // kAppend: the step's store_kv is fused in (ap); kStream: K/V row loads carry the non-temporal
 // hint (each row read once per launch; wrong when rows of the batch share pages).  S: tokens in
-// flight per wave.
+// flight per wave.  plan: a step plan for exactly these lengths, tables and slots, or null.
 template <int D, int G, int HKV, int S, bool kAppend, bool kStream>
 __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
     const int32_t* __restrict__ block_tables, int32_t max_pages, const int32_t* __restrict__ seq_lens,
     const uint8_t* __restrict__ active, int32_t batch, int32_t max_len, float scale_log2, DecodeWorkspace ws,
-    DecodeAppend ap) {
+    DecodeAppend ap, const int32_t* __restrict__ plan) {
   constexpr int LPH = kWave / HKV;  // lanes per kv head
   constexpr int ROW = HKV * D;      // fp16 elements per token row
   constexpr int HQ = HKV * G;
@@ -73,8 +241,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   constexpr int D4 = D / 4;
   static_assert(ROW == 2 * kWave * 8, "a token row is two 16-byte chunks per lane");
   static_assert(G % GR == 0, "merge rounds cover the group");
-  __shared__ int s_cum[kRowsMaxBatch + 1];            // tokens of the rows before b
-  __shared__ int s_slot[kAppend ? kRowsMaxBatch : 1];  // appended slot of row b, -1 if none
+  __shared__ int s_cum[kRowsMaxBatch + 1];  // rows' offsets in the virtual token list
   __shared__ int s_wsum[kRowsWaves];
   __shared__ float s_m[kRowsWaves][HQ];
   __shared__ float s_l[kRowsWaves][HQ];
@@ -86,113 +253,141 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const int lane = tid % kWave;
   const int cap = min(max_pages * kRowsBlock, max_len);
   const int64_t num_slots = num_pages * kRowsBlock;
-  auto row_len = [&](int b) -> int {  // keys of row b; inactive rows have none
-    const int sl = seq_lens[b];
-    const int act = active != nullptr ? int(active[b]) : 1;
-    return act != 0 ? max(0, min(sl, cap)) : 0;
-  };
-  auto append_slot = [&](int b) -> int {  // the slot row b appends to, -1 for none (store_kv's rule)
-    const int64_t sl = ap.slots[b];
-    const bool act = active == nullptr || active[b] != 0;
-    return act && sl >= 0 && sl < num_slots ? int(sl) : -1;
-  };
+  const int64_t nb = gridDim.x;
+  const int64_t blk = nb % kRowsXcds == 0 ? (blockIdx.x % kRowsXcds) * (nb / kRowsXcds) + blockIdx.x / kRowsXcds
+                                          : int64_t(blockIdx.x);
+
+  // Plan header, this range's record and its first page ids: one round trip, issued first.  The
+  // record is read before the header is checked; the entry point has checked that the buffer
+  // holds a record for every workgroup, so the read stays inside it.
+  bool planned = false;
+  int64_t T = 0;
+  int rec_n = 0;
+  int ids_pl = 0, cum_pf = 0;
+  const int32_t* rec = nullptr;
+  if (plan != nullptr) {
+    rec = plan + plan_rec0(batch) + blk * kPlanRec;
+    planned = plan[0] == kPlanMagic && plan[1] == batch && plan[4] == int(nb) && plan[6] == cap &&
+              (!kAppend || plan[5] != 0);
+    T = plan[3];
+    rec_n = rec[0];
+    ids_pl = rec[64 + lane];
+    cum_pf = plan[kPlanHdr + min(tid, batch)];
+  }
 
   // Fused append: 16-byte chunks of every appended K and V row, spread over the grid.  No wave of
   // this launch reads these slots (the attention takes the appended token from new_k / new_v).
-  // A thread's first chunk is loaded at launch and stored once the attention work is done.
+  // A thread's first chunk and its slot are loaded at launch; the chunk is stored once the
+  // attention work is done.
   constexpr int kAppChunks = ROW / 8;  // per row of K (and of V)
   const int64_t app_items = kAppend ? int64_t(batch) * 2 * kAppChunks : 0;
   auto app_src = [&](int64_t it) __attribute__((always_inline)) {
     const int b = int(it / (2 * kAppChunks)), rem = int(it % (2 * kAppChunks));
     return (rem / kAppChunks == 0 ? ap.new_k : ap.new_v) + int64_t(b) * ROW + (rem % kAppChunks) * 8;
   };
-  auto app_dst = [&](int64_t it) __attribute__((always_inline)) -> f16* {  // null: nothing to store
-    const int b = int(it / (2 * kAppChunks)), rem = int(it % (2 * kAppChunks));
-    const int slot = s_slot[b];
+  auto app_dst = [&](int64_t it, int slot) __attribute__((always_inline)) -> f16* {  // null: nothing to store
+    const int rem = int(it % (2 * kAppChunks));
     return slot < 0 ? nullptr : ap.pool + (int64_t(rem / kAppChunks) * num_slots + slot) * ROW + (rem % kAppChunks) * 8;
   };
   const int64_t app_first = int64_t(blockIdx.x) * kRowsThreads + tid;
   u32x4 app_data = u32x4{0u, 0u, 0u, 0u};
-  if constexpr (kAppend)
-    if (app_first < app_items) app_data = ld16(app_src(app_first));
-  auto flush_append = [&]() __attribute__((always_inline)) {
+  int app_slot = -1;
+  if constexpr (kAppend) {
+    if (app_first < app_items) {
+      app_data = ld16(app_src(app_first));
+      app_slot = row_slot(ap.slots, active, int(app_first / (2 * kAppChunks)), num_slots);
+    }
+  }
+  // Active rows with no keys get zeros (workgroup 0, at its end); their lengths are requested now.
+  int zero_len = 1, zero_live = 0;
+  if (blockIdx.x == 0 && tid < batch) {
+    zero_len = row_keys(seq_lens, active, tid, cap);
+    zero_live = active == nullptr || active[tid] != 0;
+  }
+  auto finish = [&]() __attribute__((always_inline)) {
     if constexpr (kAppend) {
       if (app_first < app_items) {
-        f16* d0 = app_dst(app_first);
+        f16* d0 = app_dst(app_first, app_slot);
         if (d0 != nullptr) st16(d0, app_data);
       }
       for (int64_t it = app_first + int64_t(gridDim.x) * kRowsThreads; it < app_items;
            it += int64_t(gridDim.x) * kRowsThreads) {
-        f16* d = app_dst(it);
+        f16* d = app_dst(it, row_slot(ap.slots, active, int(it / (2 * kAppChunks)), num_slots));
         if (d != nullptr) st16(d, ld16(app_src(it)));
+      }
+    }
+    if (blockIdx.x == 0) {
+      for (int b0 = 0; b0 < batch; b0 += kRowsThreads) {
+        const int b = b0 + tid;
+        bool z = false;
+        if (b < batch) z = b0 == 0 ? (zero_live && zero_len == 0)
+                                   : ((active == nullptr || active[b] != 0) && row_keys(seq_lens, active, b, cap) == 0);
+        uint64_t mask = __ballot(z);
+        while (mask != 0) {  // this wave's rows without keys, one at a time
+          const int j = __builtin_ctzll(mask);
+          mask &= mask - 1;
+          const int64_t row = b0 + wave * kWave + j;
+          for (int i = lane; i < HQ * D; i += kWave) out[row * HQ * D + i] = f16(0.f);
+        }
       }
     }
   };
 
-  // 1. Offsets of the rows in the split's (virtual) token list, in LDS (every workgroup builds its
-  // own copy): row b occupies [s_cum[b], s_cum[b + 1]), its keys the last len of those positions
-  // (kRowStartCost virtual positions in front of every non-empty row).
-  int running = 0;
-  for (int base = 0; base < batch; base += kRowsThreads) {
-    const int i = base + tid;
-    int len = 0;
-    if (i < batch) {
-      len = row_len(i);
-      if (len > 0) len += kRowStartCost;
-      if constexpr (kAppend) s_slot[i] = append_slot(i);
+  // Unplanned (or a plan for other shapes): the offsets are built here, before anything else.
+  // Planned: they go to LDS at the first merge barrier, for pieces the record does not describe.
+  if (!planned) T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap);
+  bool have_cum = !planned;
+  auto ensure_cum = [&]() __attribute__((always_inline)) {  // planned: s_cum valid after the next barrier
+    if (!have_cum) {
+      if (tid <= batch) s_cum[tid] = cum_pf;
+      for (int i = tid + kRowsThreads; i <= batch; i += kRowsThreads) s_cum[i] = plan[kPlanHdr + i];
+      have_cum = true;
     }
-    int x = len;
-#pragma unroll
-    for (int o = 1; o < kWave; o <<= 1) {
-      const int y = __shfl_up(x, o);
-      if (lane >= o) x += y;
-    }
-    if (lane == kWave - 1) s_wsum[wave] = x;
-    __syncthreads();
-    int wpre = 0, tot = 0;
-#pragma unroll
-    for (int w = 0; w < kRowsWaves; ++w) {
-      const int v = s_wsum[w];
-      wpre += w < wave ? v : 0;
-      tot += v;
-    }
-    if (i < batch) s_cum[i] = running + wpre + x - len;
-    running += tot;
-    __syncthreads();
-  }
-  if (tid == 0) s_cum[batch] = running;
-  __syncthreads();
-
-  // Active rows with no keys get zeros (workgroup 0, one wave per row).
-  if (blockIdx.x == 0) {
-    for (int b = wave; b < batch; b += kRowsWaves) {
-      const bool live = active == nullptr || active[b] != 0;
-      if (live && s_cum[b + 1] == s_cum[b])
-        for (int i = lane; i < HQ * D; i += kWave) out[int64_t(b) * HQ * D + i] = f16(0.f);
-    }
-  }
+  };
 
   // nr = min(workgroups, T) ranges, so that no range is empty (the split merge counts ranges).  A
   // range may still hold no key (only virtual positions); it then has no piece and takes no ticket.
-  const int64_t T = running;
-  const int64_t nb = gridDim.x;
   const int64_t nr = min(nb, T);
-  const int64_t blk = nb % kRowsXcds == 0 ? (blockIdx.x % kRowsXcds) * (nb / kRowsXcds) + blockIdx.x / kRowsXcds
-                                          : int64_t(blockIdx.x);
   if (blk >= nr) {
-    flush_append();
+    finish();
     return;
   }
   const int64_t t0 = T * blk / nr, t1 = T * (blk + 1) / nr;
-  // range holding flat token t: the largest r with T r / nr <= t
   auto range_of = [&](int64_t t) -> int64_t { return ((t + 1) * nr - 1) / T; };
-  auto locate = [&](int64_t t) -> int {  // the row holding flat token t (t < T)
-    int lo = 0, hi = batch - 1;
-    while (lo < hi) {
-      const int mid = (lo + hi + 1) >> 1;
-      if (s_cum[mid] <= t) lo = mid; else hi = mid - 1;
+  // The piece after row prev (prev < 0: the range's first piece); b >= batch: none.
+  auto next_piece = [&](int prev) -> RowPiece {
+    RowPiece P;
+    P.b = batch;
+    P.a = P.e = P.first = P.slot = 0;
+    P.nranges = 1;
+    int b = prev < 0 ? locate_row(s_cum, batch, t0) : prev + 1;
+    for (; b < batch; ++b) {
+      const int cb = s_cum[b] + kRowStartCost;
+      const int len = s_cum[b + 1] - cb;
+      if (len <= 0) continue;
+      if (cb >= t1) break;
+      P.a = int(max<int64_t>(t0, cb) - cb);
+      P.e = int(min<int64_t>(t1, int64_t(cb) + len) - cb);
+      if (P.a >= P.e) break;
+      P.b = b;
+      P.first = int(range_of(cb));
+      P.nranges = int(range_of(int64_t(cb) + len - 1)) - P.first + 1;
+      P.slot = kAppend ? row_slot(ap.slots, active, b, num_slots) : -1;
+      break;
     }
-    return __builtin_amdgcn_readfirstlane(lo);
+    P.b = __builtin_amdgcn_readfirstlane(P.b);
+    return P;
+  };
+  auto plan_piece = [&](int p) -> RowPiece {  // piece p < kPlanPieces of the record, clamped to the call
+    const int32_t* pc = rec + 1 + 6 * p;
+    RowPiece P;
+    P.b = min(max(pc[0], 0), batch - 1);
+    P.a = min(max(pc[1], 0), cap - 1);
+    P.e = min(max(pc[2], P.a + 1), cap);
+    P.first = min(max(pc[3], 0), int(nr) - 1);
+    P.nranges = min(max(pc[4], 1), int(nr) - P.first);
+    P.slot = pc[5];
+    return P;
   };
 
   // split partials: O [slot][HQ][D] and (m, l) [slot][HQ][2], slot < batch + gridDim.x
@@ -206,17 +401,14 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
 
   int pend_n = 0, pend_b0 = 0, pend_b1 = 0, pend_f0 = 0, pend_f1 = 0, pend_np0 = 0, pend_np1 = 0;
 
-  for (int64_t t = t0; t < t1;) {  // one piece (row segment) per iteration; uniform over the workgroup
-    const int b = locate(t);
-    const int cb = s_cum[b] + kRowStartCost;  // position of the row's first key
-    const int len = s_cum[b + 1] - cb;
-    const int a = int(max<int64_t>(t, cb) - cb);
-    const int e = int(min<int64_t>(t1, int64_t(cb) + len) - cb);
-    if (a >= e) {  // only virtual positions of this row in the range
-      t = int64_t(cb) + e;
-      continue;
-    }
-    const int slot_b = kAppend ? s_slot[b] : -1;
+  int prev = -1;
+  for (int pi = 0;; ++pi) {  // one piece (row segment) per iteration; uniform over the workgroup
+    if (planned && pi >= rec_n) break;
+    const bool from_plan = planned && pi < kPlanPieces;
+    const RowPiece P = from_plan ? plan_piece(pi) : next_piece(prev);
+    if (P.b >= batch) break;
+    const int b = P.b, a = P.a, e = P.e, slot_b = P.slot;
+    prev = b;
 
     // Query rows (b, hd * G + g), chunks col and col + LPH; the piece's page ids, one per lane.
     f16x8 qv[G][2];
@@ -229,7 +421,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     const int pg0 = a / kRowsBlock;
     const int npg = (e - 1) / kRowsBlock - pg0 + 1;
     const int32_t* bt = block_tables + int64_t(b) * max_pages + pg0;
-    int ids0 = bt[min(lane, npg - 1)];
+    int ids0 = pi == 0 && from_plan ? ids_pl : bt[min(lane, npg - 1)];
     int ids1 = bt[min(lane + kWave, npg - 1)];
     int cur_w = 0;
 
@@ -334,6 +526,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
 
     // Merge the 8 waves through LDS: (m, l) of every query head, then the accumulators in rounds of
     // GR heads per kv head.  One thread per 4 output dims combines the waves' states.
+    ensure_cum();
     if (col == 0) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -341,7 +534,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         s_l[wave][hd * G + g] = l[g];
       }
     }
-    const bool whole = a == 0 && e == len;   // this workgroup holds the whole row
+    const bool whole = P.nranges == 1;     // this workgroup holds the whole row
     const int64_t slot = int64_t(b) + blk;   // split-partial slot of (row b, this range)
 #pragma unroll
     for (int r = 0; r < G / GR; ++r) {
@@ -386,15 +579,13 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       __syncthreads();
     }
     if (!whole) {  // only the first and the last piece of a range can be split
-      const int first = int(range_of(cb)), last = int(range_of(int64_t(cb) + len - 1));
       if (pend_n == 0) {
-        pend_b0 = b; pend_f0 = first; pend_np0 = last - first + 1;
+        pend_b0 = b; pend_f0 = P.first; pend_np0 = P.nranges;
       } else {
-        pend_b1 = b; pend_f1 = first; pend_np1 = last - first + 1;
+        pend_b1 = b; pend_f1 = P.first; pend_np1 = P.nranges;
       }
       ++pend_n;
     }
-    t = int64_t(cb) + e;
   }
 
   if (pend_n > 0) {
@@ -459,11 +650,11 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       if (tid == 0) reset_ticket(ws.count + b);
     }
   }
-  flush_append();
+  finish();
 }
 
 typedef void (*RowsKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, const int32_t*,
-                           const uint8_t*, int32_t, int32_t, float, DecodeWorkspace, DecodeAppend);
+                           const uint8_t*, int32_t, int32_t, float, DecodeWorkspace, DecodeAppend, const int32_t*);
 
 constexpr int kRowsStages = 2;
 
@@ -481,8 +672,11 @@ static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream) {
   return nullptr;
 }
 
-bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d) {
-  return batch <= kRowsMaxBatch && hq % hkv == 0 && batch <= kMaxTickets &&
+bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t max_pages, int32_t max_len) {
+  // the virtual token list must fit int32: batch * (cap + kRowStartCost) < 2^31
+  const int64_t cap = std::min<int64_t>(int64_t(max_pages) * kRowsBlock, max_len);
+  return batch >= 1 && batch <= kRowsMaxBatch && hq % hkv == 0 && batch <= kMaxTickets &&
+         int64_t(batch) * (cap + kRowStartCost) < (int64_t(1) << 31) &&
          pick_rows(d, hq / hkv, hkv, false, true) != nullptr;
 }
 
@@ -491,10 +685,20 @@ size_t rows_decode_ws_bytes(int32_t batch, int32_t hq, int32_t d, int blocks) {
   return rows_ws_layout(batch, hq, d, blocks, &off_ml, &off_o);
 }
 
+size_t rows_plan_bytes(int32_t batch, int blocks) { return plan_words(batch, blocks) * sizeof(int32_t); }
+
+int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
+                     const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
+                     int blocks, hipStream_t stream) {
+  decode_plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, stream>>>(plan, block_tables, max_pages, seq_lens, active,
+                                                                  slots, num_pages, batch, max_len, blocks);
+  return ifn_launch_status();
+}
+
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
-                       const DecodeAppend& ap, bool cached, hipStream_t stream) {
+                       const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream) {
   RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   size_t off_ml, off_o;
@@ -505,7 +709,8 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
   ws.ml = reinterpret_cast<float*>(wsb + off_ml);
   ws.o = reinterpret_cast<float*>(wsb + off_o);
   k<<<dim3(unsigned(blocks)), dim3(kRowsThreads), 0, stream>>>(out, q, pool, num_pages, block_tables, max_pages,
-                                                                seq_lens, active, batch, max_len, scale_log2, ws, ap);
+                                                                seq_lens, active, batch, max_len, scale_log2, ws, ap,
+                                                                plan);
   return ifn_launch_status();
 }
 

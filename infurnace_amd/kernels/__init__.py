@@ -7,7 +7,8 @@ the C ABI of libinfurnace_hip.so to hand-written gfx950 HIP kernels.
 from ._common import KVStoreError, PagedAttentionError
 from .kv_prep import copy_pages, qk_norm_rope_append, rope_table, zero_pages
 from .kv_store import store_kv, store_kv_layers
-from .paged_attention import paged_attention, store_kv_and_decode, store_kv_and_prefill
+from .paged_attention import DecodePlan, decode_plan, paged_attention, store_kv_and_decode, store_kv_and_prefill
 
-__all__ = ["store_kv", "store_kv_layers", "paged_attention", "store_kv_and_decode", "store_kv_and_prefill", "qk_norm_rope_append", "rope_table", "zero_pages",
-           "copy_pages", "KVStoreError", "PagedAttentionError"]
+__all__ = ["store_kv", "store_kv_layers", "paged_attention", "store_kv_and_decode", "store_kv_and_prefill",
+           "decode_plan", "DecodePlan", "qk_norm_rope_append", "rope_table", "zero_pages", "copy_pages",
+           "KVStoreError", "PagedAttentionError"]

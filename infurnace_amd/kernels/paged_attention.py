@@ -28,7 +28,7 @@ from .. import _capi
 from ._common import PagedAttentionError, check_pool, current_stream, ptr
 
 __all__ = ["paged_attention", "store_kv_and_decode", "store_kv_and_prefill", "PagedAttentionError",
-           "workspace_for"]
+           "workspace_for", "DecodePlan", "decode_plan"]
 
 # One zero-initialised workspace per (device, stream): every kernel call leaves
 # the workspace's ticket counters at zero, so the buffer is reused as is.
@@ -48,6 +48,83 @@ def workspace_for(device: torch.device, stream: int, nbytes: int) -> torch.Tenso
     return ws
 
 
+class DecodePlan:
+    """The split of one decode step's keys over the CUs (``ifn_paged_decode_plan``).
+
+    Every layer of a decode step attends with the same block tables, lengths,
+    active mask and appended slots, and the decode kernel's split depends on
+    nothing else; a plan built once per step lets each layer's launch start its
+    page loads one round trip after launch.  It is valid only for calls with the
+    tensors it was built from, unchanged: the wrappers check that the same
+    tensors and shapes are passed (any layer of the same pool), not their
+    contents.
+    """
+
+    def __init__(self, buf, nbytes: int, key: tuple):
+        self.buf, self.nbytes, self.key = buf, nbytes, key
+
+    def ptr_for(self, key: tuple, need_slots: bool):
+        """The plan's device address for a call with ``key``; None when these shapes need no plan."""
+        if need_slots and self.key[1] is None:
+            raise PagedAttentionError("this DecodePlan was built without slot_mapping; the fused append needs it")
+        if key[0] != self.key[0] or key[2:] != self.key[2:] or (need_slots and key[1] != self.key[1]):
+            raise PagedAttentionError("this DecodePlan was built for other tensors or shapes")
+        return None if self.buf is None else self.buf.data_ptr()
+
+
+def _plan_key(query_shape, slot_mapping, pool_layer, block_tables, sequence_lengths, active_mask, max_seq_len):
+    """What a plan depends on, by tensor identity: shapes, the pool's page geometry, the tables,
+    lengths, mask, slots and the length cap."""
+    return (tuple(query_shape), None if slot_mapping is None else slot_mapping.data_ptr(),
+            tuple(pool_layer.shape), block_tables.data_ptr(), tuple(block_tables.shape),
+            sequence_lengths.data_ptr(), None if active_mask is None else active_mask.data_ptr(), int(max_seq_len))
+
+
+def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, sequence_lengths: torch.Tensor,
+                active_mask: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None, *,
+                layer: int = 0, block_size: int = 16, max_seq_len: int | None = None) -> DecodePlan:
+    """Build the step plan for decode calls with these tables, lengths, mask and (optionally) slots.
+
+    ``query_shape`` is the decode query's shape [B, Hq, D].  The plan is computed on the
+    current stream.  Pass it as ``plan=`` to ``paged_attention`` / ``store_kv_and_decode`` for
+    every layer of the step; with ``slot_mapping`` it also serves the fused append.  Shapes
+    that decode without a plan give an empty plan, which the calls accept and ignore.
+    """
+    pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
+    dev = pool_layer.device
+    if bs != block_size:
+        raise PagedAttentionError(f"kv_pool block_size {bs} != block_size argument {block_size}")
+    n, hq, qd = (int(x) for x in query_shape)
+    if qd != d or hq % hkv != 0:
+        raise PagedAttentionError(f"query [B, {hq}, {qd}] does not match kv heads {hkv} x {d}")
+    if not isinstance(block_tables, torch.Tensor) or block_tables.ndim != 2:
+        raise PagedAttentionError("block_tables must be a rank-2 [B, max_pages] int32 tensor")
+    max_pages = block_tables.shape[1]
+    _check("block_tables", block_tables, (n, max_pages), (torch.int32,), dev)
+    _check("sequence_lengths", sequence_lengths, (n,), (torch.int32,), dev)
+    if active_mask is not None:
+        _check("active_mask", active_mask, (n,), (torch.bool, torch.uint8), dev)
+    if slot_mapping is not None:
+        _check("slot_mapping", slot_mapping, (n,), (torch.int32,), dev)
+    if max_pages < 1:
+        raise PagedAttentionError("block_tables must have at least one column")
+    cap = max_pages * bs
+    msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
+    if msl < 0:
+        raise PagedAttentionError("max_seq_len must be non-negative")
+    key = _plan_key((n, hq, d), slot_mapping, pool_layer, block_tables, sequence_lengths, active_mask, msl)
+    if n == 0:
+        return DecodePlan(None, 0, key)
+    lib = _capi.lib()
+    nbytes = lib.ifn_paged_decode_plan_bytes(n, hq, hkv, d, bs, max_pages, msl)
+    if nbytes == 0:
+        return DecodePlan(None, 0, key)
+    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    _capi.call("ifn_paged_decode_plan", buf.data_ptr(), nbytes, ptr(block_tables), max_pages, ptr(sequence_lengths),
+               ptr(active_mask), ptr(slot_mapping), P, n, hq, hkv, d, bs, msl, current_stream(dev))
+    return DecodePlan(buf, nbytes, key)
+
+
 def _check(name: str, t, shape: tuple, dtypes: tuple, device) -> None:
     if not isinstance(t, torch.Tensor):
         raise PagedAttentionError(f"{name} must be a torch.Tensor")
@@ -65,14 +142,16 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
                     sequence_lengths: torch.Tensor | None, active_mask: torch.Tensor | None = None, *,
                     layer: int = 0, scale: float | None = None, query_start: int | None = None,
                     out: torch.Tensor | None = None, block_size: int = 16,
-                    max_seq_len: int | None = None, shared_prefix_pages: torch.Tensor | None = None) -> torch.Tensor:
+                    max_seq_len: int | None = None, shared_prefix_pages: torch.Tensor | None = None,
+                    plan: DecodePlan | None = None) -> torch.Tensor:
     """Paged GQA attention; returns ``out`` (allocated when None).
 
     Decode (``query_start is None``): ``query`` [B, Hq, D] fp16,
     ``block_tables`` int32 [B, max_pages], ``sequence_lengths`` int32 [B] on the
     device, ``active_mask`` bool/uint8 [B] or None.  ``max_seq_len`` is an
     optional host-side upper bound of ``sequence_lengths`` (default
-    max_pages * block_size) that sizes the launch.  ``shared_prefix_pages``
+    max_pages * block_size); every row's length is clamped to it, so a smaller
+    value truncates attention.  ``shared_prefix_pages``
     (int32 [S] on the device) declares that every row of at least
     S * block_size keys starts its table with these S pages (a prefix-cache
     hit); they are then read once for the whole batch instead of once per row.
@@ -80,6 +159,8 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
     pages (non-temporal loads, each page expected to be read by one row); an
     empty ``shared_prefix_pages`` declares rows that share pages outside a
     common leading run, and the decode then keeps pages in the caches.
+    ``plan`` (decode only, from ``decode_plan`` over the same tensors) is the
+    step's precomputed split; the result is bit-identical without it.
 
     Prefill (``query_start`` given): ``query`` [T, Hq, D] of one sequence,
     ``block_tables`` int32 [max_pages] or [1, max_pages]; ``sequence_lengths`` is
@@ -141,6 +222,13 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
             return out
         nbytes = lib.ifn_paged_decode_workspace_bytes(n, hq, hkv, d, bs, msl)
         ws = workspace_for(dev, stream, nbytes)
+        if plan is not None:
+            key = _plan_key((n, hq, d), None, pool_layer, block_tables, sequence_lengths, active_mask, msl)
+            pp = plan.ptr_for(key, False)
+            _capi.call("ifn_paged_decode_planned", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables),
+                       max_pages, ptr(sequence_lengths), ptr(active_mask), n, hq, hkv, d, bs, msl, float(scale),
+                       pp, plan.nbytes if pp else 0, ptr(ws), ws.numel(), stream)
+            return out
         _capi.call("ifn_paged_decode", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables),
                    max_pages, ptr(sequence_lengths), ptr(active_mask), n, hq, hkv, d, bs, msl,
                    float(scale), ptr(ws), ws.numel(), stream)
@@ -184,7 +272,7 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
                         sequence_lengths: torch.Tensor, active_mask: torch.Tensor | None,
                         slot_mapping: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor, *, layer: int = 0,
                         scale: float | None = None, out: torch.Tensor | None = None, block_size: int = 16,
-                        max_seq_len: int | None = None) -> torch.Tensor:
+                        max_seq_len: int | None = None, plan: DecodePlan | None = None) -> torch.Tensor:
     """One decode step's append and attention in one launch (``ifn_paged_decode_append``).
 
     Same result, in ``out`` and in the pool, as ``store_kv(kv_pool, slot_mapping, active_mask,
@@ -192,6 +280,7 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
     sequence_lengths, active_mask, layer=layer, ...)`` -- the store of model.py:191-196 and the
     attention of :196-200.  ``new_k``/``new_v`` are fp16 [B, Hkv, D], ``slot_mapping`` int32 [B].
     An appended slot must not be read by another row of the call (true of any paged KV state).
+    ``plan``: the step's ``decode_plan`` built with this ``slot_mapping``.
     """
     from .kv_store import _check_index, _check_rows
     if slot_mapping is None:
@@ -236,6 +325,13 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
     lib = _capi.lib()
     nbytes = lib.ifn_paged_decode_workspace_bytes(n, hq, hkv, d, bs, msl)
     ws = workspace_for(dev, stream, nbytes)
+    if plan is not None:
+        key = _plan_key((n, hq, d), sm, pool_layer, block_tables, sequence_lengths, active_mask, msl)
+        pp = plan.ptr_for(key, True)
+        _capi.call("ifn_paged_decode_append_planned", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables),
+                   max_pages, ptr(sequence_lengths), ptr(active_mask), ptr(sm), ptr(new_k), ptr(new_v), n, hq, hkv,
+                   d, bs, msl, float(scale), pp, plan.nbytes if pp else 0, ptr(ws), ws.numel(), stream)
+        return out
     _capi.call("ifn_paged_decode_append", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables), max_pages,
                ptr(sequence_lengths), ptr(active_mask), ptr(sm), ptr(new_k), ptr(new_v), n, hq, hkv, d, bs, msl,
                float(scale), ptr(ws), ws.numel(), stream)
