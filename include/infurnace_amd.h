@@ -199,6 +199,28 @@ int ifn_paged_decode_append_planned(void* out, const void* query, void* kv_pool_
                                     const void* plan, size_t plan_bytes, void* workspace,
                                     size_t workspace_bytes, void* stream);
 
+/*
+ * ifn_paged_decode without a workspace argument: for callers that cannot
+ * allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  It allocates nothing: the split-KV
+ * tickets and partial states live in a fixed device array of
+ * ifn_paged_decode_noalloc_max_bytes() bytes per GPU (16 MiB), held until
+ * the process ends.  Calls whose ifn_paged_decode_workspace_bytes exceed it
+ * return IFN_ERR_WORKSPACE.  The first call on a device resolves the array's
+ * address and zeroes its counters (a small kernel on `stream`, ordered before
+ * the decode).  Every call on a GPU shares that GPU's array, so calls that
+ * overlap on one GPU (two streams or host threads) race: serialise them.
+ * Output is bit-identical to ifn_paged_decode's.
+ * Replaces: nothing in the reference (no counterpart); it serves the callers
+ * that cannot allocate, with ifn_paged_decode's semantics.
+ */
+size_t ifn_paged_decode_noalloc_max_bytes(void);
+int ifn_paged_decode_noalloc(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                             const int32_t* block_tables, int32_t max_pages_per_seq,
+                             const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                             int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t block_size, int32_t max_seq_len, float scale, void* stream);
+
 /* Workspace bytes ifn_paged_decode_shared_prefix needs for these shapes. */
 size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num_q_heads,
                                                       int32_t num_kv_heads, int32_t head_dim,

@@ -46,6 +46,9 @@ SIGNATURES: dict[str, tuple] = {
                                                 _i32, _f32, _p, _sz, _p, _sz, _p]),
     "ifn_paged_decode_append_planned": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _p, _p, _p, _p, _i32, _i32,
                                                        _i32, _i32, _i32, _i32, _f32, _p, _sz, _p, _sz, _p]),
+    "ifn_paged_decode_noalloc_max_bytes": (_sz, []),
+    "ifn_paged_decode_noalloc": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _p, _i32, _i32, _i32, _i32,
+                                                _i32, _i32, _f32, _p]),
     "ifn_paged_decode_shared_prefix_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "ifn_paged_decode_shared_prefix": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _i32, _p, _p, _i32, _i32,
                                                       _i32, _i32, _i32, _i32, _f32, _p, _sz, _p]),
