@@ -9,7 +9,10 @@
  * reference's write-before-read rule (docs/architecture.md:249-250).
  *
  * The library never allocates device memory.  Scratch space is a
- * caller-provided workspace.  No C++ exception crosses this boundary: every
+ * caller-provided workspace.  Its first 256 KiB are split-KV tickets, whose
+ * last 4 bytes are an error flag: a kernel sets that uint32 to 1 when one of
+ * its bounded waits gave up (its result may then be wrong); only the caller
+ * reads and clears it.  No C++ exception crosses this boundary: every
  * entry point returns IFN_OK (0) or a negative IFN_ERR_* code, checked on the
  * host before any launch (shape, alignment and workspace checks) or after it
  * (hipGetLastError).  Entry points hold no mutable global state, so distinct

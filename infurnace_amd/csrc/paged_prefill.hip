@@ -457,21 +457,29 @@ __global__ __launch_bounds__((PrefillCfg<D, G>::kThreads)) void paged_prefill_ke
   int cur_flags = s0.flags;
   load_tile(1, s0);
   __syncthreads();
-  auto group_wait = [&](int target) __attribute__((always_inline)) {
+  // Returns false when the count did not arrive within the bound (never expected): the wave
+  // then skips that tile's arithmetic -- it does not multiply a tile that may not be stored --
+  // keeps counting its steps so that the rest of its group is not held up, and raises the
+  // workspace's error flag, which the caller's validate mode reports.
+  auto group_wait = [&](int target) __attribute__((always_inline)) -> bool {
     for (int spins = 0; spins < (1 << 20); ++spins) {
-      if (__hip_atomic_load(&s_grp_cnt[grp], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+      if (__hip_atomic_load(&s_grp_cnt[grp], __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) return true;
       __builtin_amdgcn_s_sleep(1);
     }
+    return false;
   };
+  bool wait_failed = false;
   for (int i = 0; i < iters; ++i) {
     const int fl = cur_flags;
-    if (i > 0) group_wait(G * i);  // every wave of the group has finished step i - 1
+    const bool ready = i == 0 || group_wait(G * i);  // every wave of the group has finished step i - 1
+    wait_failed |= !ready;
     if (has(i + 1)) store_tile(i + 1, (i + 1) & 1, s0);
     cur_flags = s0.flags;
     load_tile(i + 2, s0);
-    if (has(i)) compute_tile(i, i & 1, fl);
+    if (has(i) && ready) compute_tile(i, i & 1, fl);
     if (lane == 0) __hip_atomic_fetch_add(&s_grp_cnt[grp], 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
   }
+  if (wait_failed && lane == 0 && ws.count != nullptr) raise_error_flag(ws.count);
 
   __syncthreads();  // every group is done with the tile buffers, which the merge area reuses
   const float ltot = lsum + __shfl_xor(lsum, 32);
@@ -724,6 +732,9 @@ static int prefill_entry(void* out, const void* query, const void* kv_pool_layer
     ws.count = reinterpret_cast<uint32_t*>(wsb);
     ws.ml = reinterpret_cast<float*>(wsb + p.off_ml);
     ws.o = reinterpret_cast<float*>(wsb + p.off_o);
+  } else if (workspace != nullptr && workspace_bytes >= kTicketBytes) {
+    IFN_CHECK_ALIGN16(workspace);
+    ws.count = static_cast<uint32_t*>(workspace);  // no split: only the error flag is used
   }
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
   k<<<dim3(unsigned(p.n_qb * num_kv_heads * p.nsplit)), unsigned(threads), 0,

@@ -30,14 +30,19 @@ __all__ = ["qk_norm_rope_append", "rope_table", "zero_pages", "copy_pages"]
 def rope_table(max_positions: int, head_dim: int, base: float, device=None) -> torch.Tensor:
     """fp32 [max_positions, head_dim] rows ``[cos(p f_i) | sin(p f_i)]``, f_i = base^(-2i/D), i < D/2.
 
-    The layout of ``_precompute_rope`` (model.py:19-23).  The angles are computed in
-    float64 and rounded once to float32.
+    ``_precompute_rope`` (model.py:18-22) in its own order and precision: the exponents
+    2i/D, base^(2i/D), the inverse frequencies f_i and the angles p * f_i are float32 values,
+    each rounded once; cos and sin of those float32 angles are then rounded once to float32
+    (the reference's float32 cos/sin may differ from these by an ulp).
     """
     if max_positions < 1 or head_dim < 2 or head_dim % 2 or not base > 0:
         raise ValueError("rope_table needs max_positions >= 1, an even head_dim and base > 0")
-    inv = 1.0 / (base ** (np.arange(0, head_dim, 2, dtype=np.float64) / head_dim))
-    ang = np.arange(max_positions, dtype=np.float64)[:, None] * inv[None, :]
-    table = np.concatenate([np.cos(ang), np.sin(ang)], axis=1).astype(np.float32)
+    f32 = np.float32
+    expo = (np.arange(0, head_dim, 2, dtype=f32) / f32(head_dim)).astype(f32)
+    inv = (f32(1.0) / np.power(f32(base), expo).astype(f32)).astype(f32)
+    ang = (np.arange(max_positions, dtype=f32)[:, None] * inv[None, :]).astype(f32)
+    a64 = ang.astype(np.float64)
+    table = np.concatenate([np.cos(a64), np.sin(a64)], axis=1).astype(f32)
     return torch.from_numpy(table).to(device) if device is not None else torch.from_numpy(table)
 
 

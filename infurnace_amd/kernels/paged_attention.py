@@ -125,6 +125,17 @@ def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, 
     return DecodePlan(buf, nbytes, key)
 
 
+def check_error_flag(ws: torch.Tensor, what: str) -> None:
+    """Validate mode: synchronise, and raise if a kernel that used ``ws`` set its error flag (a
+    bounded wait gave up, so the result may be wrong); the flag is cleared first."""
+    torch.cuda.synchronize(ws.device)
+    off = _capi.WORKSPACE_ERROR_FLAG_OFFSET
+    flag = ws[off:off + 4]
+    if bool(flag.any()):
+        flag.zero_()
+        raise PagedAttentionError(f"{what}: a workgroup's bounded wait gave up; the result may be wrong")
+
+
 def _check(name: str, t, shape: tuple, dtypes: tuple, device) -> None:
     if not isinstance(t, torch.Tensor):
         raise PagedAttentionError(f"{name} must be a torch.Tensor")
@@ -143,7 +154,7 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
                     layer: int = 0, scale: float | None = None, query_start: int | None = None,
                     out: torch.Tensor | None = None, block_size: int = 16,
                     max_seq_len: int | None = None, shared_prefix_pages: torch.Tensor | None = None,
-                    plan: DecodePlan | None = None) -> torch.Tensor:
+                    plan: DecodePlan | None = None, validate: bool = False) -> torch.Tensor:
     """Paged GQA attention; returns ``out`` (allocated when None).
 
     Decode (``query_start is None``): ``query`` [B, Hq, D] fp16,
@@ -166,7 +177,8 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
     ``block_tables`` int32 [max_pages] or [1, max_pages]; ``sequence_lengths`` is
     unused on the device (keys = query_start + T) and, when it is a host value,
     must equal query_start + T.  ``active_mask`` of one False row makes the call
-    a no-op.
+    a no-op.  ``validate`` (prefill) synchronises after the launch and raises when
+    a workgroup's bounded wait gave up (the workspace's error flag).
     """
     pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
     dev = pool_layer.device
@@ -265,6 +277,8 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
     ws = workspace_for(dev, stream, nbytes)
     _capi.call("ifn_paged_prefill", ptr(out), ptr(query), ptr(pool_layer), P, ptr(table), max_pages,
                query_start, n, hq, hkv, d, bs, float(scale), ptr(ws), ws.numel(), stream)
+    if validate:
+        check_error_flag(ws, "paged_attention (prefill)")
     return out
 
 
@@ -340,7 +354,7 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
 
 def store_kv_and_prefill(query: torch.Tensor, kv_pool: torch.Tensor, block_table: torch.Tensor, new_k: torch.Tensor,
                          new_v: torch.Tensor, *, query_start: int, layer: int = 0, scale: float | None = None,
-                         out: torch.Tensor | None = None, block_size: int = 16) -> torch.Tensor:
+                         out: torch.Tensor | None = None, block_size: int = 16, validate: bool = False) -> torch.Tensor:
     """One prefill chunk's append and causal attention (``ifn_paged_prefill_append``).
 
     Same result, in ``out`` and in the pool, as ``store_kv`` of ``new_k``/``new_v`` [T, Hkv, D] at
@@ -390,5 +404,7 @@ def store_kv_and_prefill(query: torch.Tensor, kv_pool: torch.Tensor, block_table
     ws = workspace_for(dev, stream, nbytes)
     _capi.call("ifn_paged_prefill_append", ptr(out), ptr(query), ptr(pool_layer), P, ptr(table), max_pages,
                query_start, n, ptr(new_k), ptr(new_v), hq, hkv, d, bs, float(scale), ptr(ws), ws.numel(), stream)
+    if validate:
+        check_error_flag(ws, "store_kv_and_prefill")
     return out
 

@@ -20,6 +20,18 @@ this package's pool, tables and kernels:
 * ``clear_slot(slot)`` releases the slot's pages (zeroing them on request:
   buffers.py:67-81), which is what the engine calls on every terminal transition
   (src/infurnace/engine/engine.py:89,130,166);
+* pages referenced by submitted device work are in flight and do not return to
+  the free pool until that work has completed (docs/architecture.md:255-257;
+  the "delayed in-flight reclamation" of docs/roadmap.md:331-337,356-359): a
+  step marks the pages it reads or writes in flight when it begins, records an
+  event after each of its launches, and its pages are released once it is closed
+  (a later step began or a slot was cleared) and its last event has completed -- checked
+  without blocking at every ``begin_*``, ``clear_slot`` and ``reclaim()``, or
+  waited for by ``synchronize()``.  A page freed by ``clear_slot`` while in
+  flight is reused only after that; with ``zero=True`` it is zeroed when it is
+  released;
+* a decode step builds its step plan (``decode_plan``) once, at its first layer,
+  and every later layer reuses it;
 * a decode batch whose live rows start with the same pages (prefix-cache hits)
   reads those pages once for the batch (``paged_attention(...,
   shared_prefix_pages=...)``) when they are at least ``shared_prefix_min_pages``;
@@ -37,8 +49,9 @@ from typing import Sequence
 import numpy as np
 import torch
 
-from .cache import BlockPool, KVCacheError, KVManager, PagedKVCache, PrefixCache
-from .kernels import paged_attention, qk_norm_rope_append, store_kv, store_kv_and_decode, store_kv_and_prefill
+from .cache import BlockPool, KVCacheError, KVManager, PagedKVCache, PoolExhausted, PrefixCache
+from .kernels import (decode_plan, paged_attention, qk_norm_rope_append, store_kv, store_kv_and_decode,
+                      store_kv_and_prefill)
 
 __all__ = ["PagedKVRunner", "RunnerError"]
 
@@ -60,6 +73,22 @@ class _Step:
     max_len: int
     # int32 pages every live decode row starts with; empty: rows share pages elsewhere (cached page loads)
     shared_prefix: torch.Tensor | None = None
+    pages: np.ndarray | None = None   # page ids this step reads or writes (held in flight)
+    event: object | None = None       # recorded after the step's latest launch
+    closed: bool = False              # no further launch will be recorded
+    plan: object | None = None        # decode step plan, built at the first layer
+
+    def _launched(self) -> None:
+        """Record the step's completion event after a launch on the current stream."""
+        if self.event is None:
+            self.event = self.runner._event_factory()
+        self.event.record()
+
+    def _decode_plan(self, q: torch.Tensor):
+        if self.plan is None:
+            self.plan = decode_plan(q.shape, self.runner.cache.kv, self.block_tables, self.seq_lens, self.active,
+                                    self.slot_mapping, max_seq_len=self.max_len)
+        return self.plan
 
     def store_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                      out: torch.Tensor | None = None) -> torch.Tensor:
@@ -68,32 +97,42 @@ class _Step:
         A prefill chunk, and a decode step without a shared prefix, do both in one launch
         (``store_kv_and_prefill`` / ``store_kv_and_decode``).
         """
+        if self.closed:
+            raise RunnerError("this step is closed: a later step has begun")
         kv = self.runner.cache.kv
         if self.query_start is not None:
-            return store_kv_and_prefill(q, kv, self.block_tables, k, v, query_start=self.query_start, layer=layer,
-                                        out=out)
-        if self.shared_prefix is None:
-            return store_kv_and_decode(q, kv, self.block_tables, self.seq_lens, self.active, self.slot_mapping, k, v,
-                                       layer=layer, max_seq_len=self.max_len, out=out)
-        store_kv(kv, self.slot_mapping, self.active, k, v, layer=layer)
-        if self.query_start is not None:
-            return paged_attention(q, kv, self.block_tables, None, None, layer=layer, query_start=self.query_start,
-                                   out=out)
-        return paged_attention(q, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
-                               max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
+            o = store_kv_and_prefill(q, kv, self.block_tables, k, v, query_start=self.query_start, layer=layer,
+                                     out=out)
+        elif self.shared_prefix is None:
+            o = store_kv_and_decode(q, kv, self.block_tables, self.seq_lens, self.active, self.slot_mapping, k, v,
+                                    layer=layer, max_seq_len=self.max_len, out=out, plan=self._decode_plan(q))
+        else:
+            store_kv(kv, self.slot_mapping, self.active, k, v, layer=layer)
+            o = paged_attention(q, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
+                                max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
+        self._launched()
+        return o
 
     def prep_store_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, rope: torch.Tensor,
                           eps: float = 1e-6, out: torch.Tensor | None = None) -> torch.Tensor:
         """The same from fp32 projections: q/k RMSNorm + rotary, fp16 cast and append in one launch."""
+        if self.closed:
+            raise RunnerError("this step is closed: a later step has begun")
         kv = self.runner.cache.kv
         q16 = qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope, self.positions, self.slot_mapping,
                                   self.active, kv, layer=layer, eps=eps)
         if self.query_start is not None:
-            return paged_attention(q16, kv, self.block_tables, None, None, layer=layer,
-                                   query_start=self.query_start, out=out)
-        return paged_attention(q16, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
-                               max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
+            o = paged_attention(q16, kv, self.block_tables, None, None, layer=layer, query_start=self.query_start,
+                                out=out)
+        elif self.shared_prefix is None:
+            o = paged_attention(q16, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
+                                max_seq_len=self.max_len, out=out, plan=self._decode_plan(q16))
+        else:
+            o = paged_attention(q16, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
+                                max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
+        self._launched()
+        return o
 
 
 class PagedKVRunner:
@@ -102,7 +141,7 @@ class PagedKVRunner:
     def __init__(self, num_layers: int, num_slots: int, max_context: int, num_kv_heads: int, head_dim: int,
                  num_blocks: int, device: str | torch.device = "cuda", block_size: int = 16,
                  prefix_namespace=None, prefix_capacity_blocks: int | None = None,
-                 shared_prefix_min_pages: int = 64):
+                 shared_prefix_min_pages: int = 64, event_factory=None):
         if num_slots < 1 or max_context < 1:
             raise RunnerError("num_slots and max_context must be positive")
         self._num_slots, self._max_context = num_slots, max_context
@@ -119,6 +158,12 @@ class PagedKVRunner:
         # below this many common leading pages, decode re-reads them per row (from cache) instead
         # of paying the shared-prefix path's two extra launches
         self.shared_prefix_min_pages = max(1, int(shared_prefix_min_pages))
+        # completion events of submitted steps (an object with record() and query(); on a GPU a
+        # torch.cuda.Event recorded on the current stream)
+        self._event_factory = event_factory or (
+            (lambda: torch.cuda.Event()) if self.device.type == "cuda" else _CompletedEvent)
+        self._inflight: list[_Step] = []  # steps whose pages are held in flight
+        self._zero_on_release: set[int] = set()
 
     # Runner contract (runner.py:11-21)
     @property
@@ -164,15 +209,15 @@ class PagedKVRunner:
             raise RunnerError(f"slot {slot} holds {self.length(slot)} tokens; chunk starts at {start_position}")
         if start_position + num_tokens > self._max_context:
             raise RunnerError(f"chunk ends at {start_position + num_tokens} > max_context {self._max_context}")
+        self._close_steps()
         if slot not in self.mgr:
             self.mgr.add_sequence(slot)
-        try:
-            slots = self.mgr.append(slot, num_tokens)
-        except KVCacheError as e:
-            raise RunnerError(str(e)) from e
+        slots = self._reserve(lambda: self.mgr.append(slot, num_tokens))
         pos = np.arange(start_position, start_position + num_tokens, dtype=np.int32)
-        return _Step(self, self._dev(slots.astype(np.int32)), self._dev(self._table([slot])[0]), None, None,
-                     self._dev(pos), start_position, start_position + num_tokens)
+        table = self._table([slot])[0]
+        used = table[:-(-(start_position + num_tokens) // self.block_size)]
+        return self._submit(_Step(self, self._dev(slots.astype(np.int32)), self._dev(table), None, None,
+                                  self._dev(pos), start_position, start_position + num_tokens), used)
 
     def attach_prefix(self, slot: int, token_ids: Sequence[int]) -> int:
         """Start an empty slot from the longest cached prefix of ``token_ids`` (complete blocks).
@@ -224,10 +269,8 @@ class PagedKVRunner:
                 raise RunnerError(f"row {i}: position {positions[i]} is past max_context")
         if len({slots[i] for i in live}) != len(live):
             raise RunnerError("two active rows share a slot")
-        try:
-            new_slots = self.mgr.append_batch([slots[i] for i in live], [1] * len(live))
-        except KVCacheError as e:
-            raise RunnerError(str(e)) from e
+        self._close_steps()
+        new_slots = self._reserve(lambda: self.mgr.append_batch([slots[i] for i in live], [1] * len(live)))
         sm = np.full(len(slots), -1, np.int32)
         for j, i in enumerate(live):
             sm[i] = int(new_slots[j][0])
@@ -243,8 +286,11 @@ class PagedKVRunner:
             prefix = self._dev(np.zeros(0, np.int32))
         else:
             prefix = None
-        return _Step(self, self._dev(sm), self._dev(table), self._dev(lens), self._dev(act),
-                     self._dev(np.asarray(positions, np.int32)), None, int(lens.max()) if len(lens) else 0, prefix)
+        used = [table[i, :-(-int(lens[i]) // self.block_size)] for i in live]
+        return self._submit(_Step(self, self._dev(sm), self._dev(table), self._dev(lens), self._dev(act),
+                                  self._dev(np.asarray(positions, np.int32)), None,
+                                  int(lens.max()) if len(lens) else 0, prefix),
+                            np.concatenate(used) if used else np.zeros(0, np.int32))
 
     def _common_pages(self, table: np.ndarray, lens: np.ndarray) -> np.ndarray:
         """Leading page ids that every row of ``table`` holds at the same columns (at least two
@@ -267,11 +313,104 @@ class PagedKVRunner:
     # -- lifecycle --------------------------------------------------------------------------
 
     def clear_slot(self, slot: int, zero: bool = False) -> list[int]:
-        """Release the slot's pages (runner.py:38-43); ``zero`` also zeroes the freed pages."""
+        """Release the slot's pages (runner.py:38-43); ``zero`` also zeroes the freed pages.
+
+        Returns the pages that returned to the free pool now.  Pages that submitted work still
+        reads or writes return (and, with ``zero``, are zeroed) once that work has completed.
+        """
         self._check_slot(slot)
         if slot not in self.mgr:
             return []
+        for st in self._inflight:  # the engine clears slots between steps: no step takes more launches
+            st.closed = True
+        owned = self.mgr.blocks(slot)
         freed = self.mgr.free_sequence(slot)
-        if zero and freed:
-            self.cache.clear_pages(freed)
-        return freed
+        if zero:
+            if freed:
+                self.cache.clear_pages(freed)
+            held = set(owned) - set(freed)
+            self._zero_on_release.update(p for p in held if self.pool.refcount(p, "inflight") > 0)
+        return freed + self.reclaim()
+
+    # -- in-flight pages ----------------------------------------------------------------------
+
+    def _submit(self, step: _Step, pages: np.ndarray) -> _Step:
+        """Hold the step's pages in flight until its work has completed."""
+        ids = np.unique(np.asarray(pages, np.int64))
+        if self.pool.dummy_block is not None:
+            ids = ids[ids != self.pool.dummy_block]
+        step.pages = ids
+        if ids.size:
+            self.pool.mark_in_flight(ids)
+        self._inflight.append(step)
+        return step
+
+    def _close_steps(self) -> None:
+        """A new step begins: earlier steps take no further launches; release what has completed."""
+        for st in self._inflight:
+            st.closed = True
+        self.reclaim()
+
+    def _reserve(self, take):
+        """Run a page reservation (all or nothing).  When the pool is exhausted while submitted
+        steps still hold pages in flight, wait for them, release their pages and try once more;
+        an exhausted pool raises PoolExhausted, any other refusal RunnerError."""
+        try:
+            return take()
+        except PoolExhausted:
+            if not self._inflight:
+                raise
+            self.synchronize()
+        except KVCacheError as e:
+            raise RunnerError(str(e)) from e
+        try:
+            return take()
+        except KVCacheError as e:
+            raise RunnerError(str(e)) from e
+
+    def reclaim(self) -> list[int]:
+        """Release the pages of closed steps whose work has completed (no blocking); returns the
+        pages that returned to the free pool."""
+        released: list[int] = []
+        keep = []
+        for st in self._inflight:
+            if st.closed and (st.event is None or st.event.query()):
+                if st.pages is not None and st.pages.size:
+                    released += self.pool.release_in_flight(st.pages)
+            else:
+                keep.append(st)
+        self._inflight = keep
+        if released and self._zero_on_release:
+            z = [p for p in released if p in self._zero_on_release]
+            if z:
+                self._zero_on_release.difference_update(z)
+                self.cache.clear_pages(z)
+        return released
+
+    def synchronize(self) -> list[int]:
+        """Wait for every submitted step's work, close all steps and release their pages."""
+        for st in self._inflight:
+            st.closed = True
+            if st.event is not None:
+                st.event.synchronize()
+        return self.reclaim()
+
+    @property
+    def pages_in_flight(self) -> int:
+        """Distinct pages held by submitted, unreleased steps."""
+        if not self._inflight:
+            return 0
+        return int(np.unique(np.concatenate([st.pages for st in self._inflight if st.pages is not None])).size)
+
+
+class _CompletedEvent:
+    """Completion event for a runner without a GPU: work is complete as soon as it is recorded."""
+
+    def record(self, stream=None) -> None:
+        pass
+
+    def query(self) -> bool:
+        return True
+
+    def synchronize(self) -> None:
+        pass

@@ -127,6 +127,45 @@ def paged_attention(q, pool_layer, block_tables, seq_lens, active_mask=None, sca
     return o[:, 0] if decode else o
 
 
+def host_threads() -> int:
+    """Threads for the row-parallel oracle: the cores this process may run on, capped at the
+    host's thread budget (OMP_NUM_THREADS when set -- the CPU share of a one-GPU box -- else 16)."""
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    try:
+        cap = int(os.environ.get("OMP_NUM_THREADS") or 16)
+    except ValueError:
+        cap = 16
+    return max(1, min(n, cap))
+
+
+def paged_attention_rows(q, pool_layer, block_tables, seq_lens, active_mask=None, scale=None,
+                         threads: int | None = None) -> np.ndarray:
+    """``paged_attention`` with its rows split over host threads (the C call releases the GIL).
+
+    Each thread runs the same oracle on a contiguous block of rows, so the result is identical
+    to one ``paged_attention`` call on all rows.
+    """
+    import concurrent.futures as cf
+    q = _c(q, np.float16)
+    B = q.shape[0]
+    n = max(1, min(threads or host_threads(), B))
+    bounds = [B * i // n for i in range(n + 1)]
+    pool_layer = _c(pool_layer, np.float16)
+    bt, sl = _c(block_tables, np.int32), _c(seq_lens, np.int32)
+    am = None if active_mask is None else np.asarray(active_mask)
+
+    def run(i):
+        lo, hi = bounds[i], bounds[i + 1]
+        return paged_attention(q[lo:hi], pool_layer, bt[lo:hi], sl[lo:hi], None if am is None else am[lo:hi], scale)
+
+    with cf.ThreadPoolExecutor(max_workers=n) as ex:
+        parts = list(ex.map(run, range(n)))
+    return np.concatenate(parts, axis=0)
+
+
 def qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope_table, positions, slot_mapping,
                         active_mask, pool_layer: np.ndarray, eps: float = 1e-6) -> np.ndarray:
     """Pre-append step: returns q (fp16 [T, Hq, D]) after RMSNorm + rotary; stores k (normed,

@@ -52,7 +52,12 @@ def assert_attn_close(got: torch.Tensor, ref: np.ndarray, what: str = "") -> Non
 
 def oracle_decode(pool_layer: torch.Tensor, table: np.ndarray, lens: np.ndarray, q: torch.Tensor,
                   rows=None) -> np.ndarray:
+    """The oracle's decode of ``rows`` (all by default), over host threads; only the pages those rows
+    read are copied to the host (the whole pool when they read most of it)."""
     rows = np.arange(table.shape[0]) if rows is None else np.asarray(rows)
+    qh = q[torch.as_tensor(rows, device=q.device)].cpu().numpy()
+    used = -(-lens[rows].astype(np.int64) // 16)
+    if int(used.sum()) >= pool_layer.shape[1] // 2:
+        return oracle.paged_attention_rows(qh, pool_layer.cpu().numpy(), table[rows], lens[rows].astype(np.int32))
     sub, t2 = compact_for_oracle(pool_layer, table[rows], lens[rows])
-    return oracle.paged_attention(q[torch.as_tensor(rows, device=q.device)].cpu().numpy(), sub, t2,
-                                  lens[rows].astype(np.int32))
+    return oracle.paged_attention_rows(qh, sub, t2, lens[rows].astype(np.int32))

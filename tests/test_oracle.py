@@ -323,13 +323,112 @@ def test_prep_rotation_invariants():
     n0 = q0[..., :h].astype(np.float64) ** 2 + q0[..., h:].astype(np.float64) ** 2
     n1 = qp[..., :h].astype(np.float64) ** 2 + qp[..., h:].astype(np.float64) ** 2
     assert np.allclose(n0, n1, rtol=4e-3, atol=1e-4)
-    # rotations compose: rotating by a then by b (table rows) equals rotating by a + b
-    tab = _rope64(64, 128, 10000.0)
-    x = rng.standard_normal(128)
-    def rot(x, r):
-        c, s = r[:h], r[h:]
-        return np.concatenate([x[:h] * c - x[h:] * s, x[h:] * c + x[:h] * s])
-    assert np.allclose(rot(rot(x, tab[5]), tab[9]), rot(x, tab[14]), atol=1e-12)
+
+
+def test_prep_rotation_direction_closed_form():
+    """Unit vectors pin the rotation's direction (model.py:24-27: (x1 c - x2 s, x2 c + x1 s)):
+    e_i -> sqrt(D) (cos t_i at i, sin t_i at i + D/2) and e_{i+D/2} -> sqrt(D) (-sin t_i, cos t_i).
+    A transposed sign (x1 c + x2 s) or swapped halves fails."""
+    d, h = 64, 32
+    rope = _rope64(100, d, 1e4).astype(np.float32)
+    ones = np.ones(d, np.float32)
+    for i, p in ((0, 7), (5, 33), (31, 99)):
+        q = np.zeros((2, 1, d), np.float32)
+        q[0, 0, i] = 1.0
+        q[1, 0, h + i] = 1.0
+        k = np.zeros((2, 1, d), np.float32)
+        pool = np.zeros((2, 1, 16, 1, d), np.float16)
+        out = oracle.qk_norm_rope_append(q, k, k, ones, ones, rope, np.full(2, p, np.int32),
+                                         np.asarray([-1, -1], np.int32), None, pool, eps=0.0).astype(np.float64)
+        c, s_ = float(rope[p, i]), float(rope[p, h + i])
+        r = math.sqrt(d)
+        exp0 = np.zeros(d); exp0[i], exp0[h + i] = r * c, r * s_
+        exp1 = np.zeros(d); exp1[i], exp1[h + i] = -r * s_, r * c
+        assert np.allclose(out[0, 0], exp0, atol=r * 2e-3), (i, p)
+        assert np.allclose(out[1, 0], exp1, atol=r * 2e-3), (i, p)
+
+
+def test_rope_table_follows_the_reference_float32_order():
+    """rope_table against an independent float32 restatement of _precompute_rope (model.py:18-22)
+    in torch float32 ops, step by step, and against closed forms.
+
+    * inverse frequencies 1 / base^(2i/D): within 2 float32 ulps (float32 pow is
+      implementation-defined: numpy and torch differ by up to 2 ulps here);
+    * angles: the float32 products p * f_i of the table's own frequencies, exactly;
+    * cos / sin of those angles: within 2 float32 ulps of torch's float32 cos / sin;
+    * row 0 is [1 .. 1 | 0 .. 0]; column 0 has frequency 1 exactly, so it is cos(p) / sin(p) of the
+      exact integer p; the slowest column turns by base^(-(D-2)/D) per position (a table built on
+      arange(0, D) / D, on i / D or with the halves swapped fails one of these)."""
+    from infurnace_amd.kernels import rope_table
+    for d, base, n in ((128, 1e6, 40960), (64, 1e4, 4096)):
+        tab = rope_table(n, d, base).numpy().astype(np.float64)
+        h = d // 2
+        inv_t = (1.0 / (torch.tensor(base, dtype=torch.float32) **
+                        (torch.arange(0, d, 2, dtype=torch.float32) / d))).numpy()
+        # the table's frequencies, recovered from row 1 (angle = f_i exactly at p = 1)
+        f_tab = np.arctan2(tab[1, h:], tab[1, :h])
+        assert np.all(np.abs(f_tab - inv_t) <= 3 * np.spacing(inv_t.astype(np.float32)) + 1e-7 * inv_t)
+        f32 = np.float32
+        inv = (f32(1) / np.power(f32(base), (np.arange(0, d, 2, dtype=f32) / f32(d)).astype(f32)).astype(f32))
+        inv = inv.astype(f32)
+        assert np.all(np.abs(inv.view(np.int32).astype(np.int64) - inv_t.view(np.int32).astype(np.int64)) <= 2)
+        ang = torch.arange(n, dtype=torch.float32)[:, None] * torch.from_numpy(inv)[None, :]
+        ref = torch.cat([ang.cos(), ang.sin()], dim=1).numpy()
+        ulps = np.abs(tab.astype(np.float32).view(np.int32).astype(np.int64) - ref.view(np.int32).astype(np.int64))
+        assert ulps.max() <= 2, ulps.max()
+        assert np.array_equal(tab[0], np.concatenate([np.ones(h), np.zeros(h)]))
+        p = np.arange(n, dtype=np.float64)
+        assert np.array_equal(tab[:, 0], np.cos(p).astype(np.float32).astype(np.float64))
+        assert np.array_equal(tab[:, h], np.sin(p).astype(np.float32).astype(np.float64))
+        f_last = base ** (-(d - 2) / d)
+        assert abs(f_tab[-1] - f_last) <= 1e-6 * f_last
+
+
+def test_fp16_query_deviation_from_fp32_reference():
+    """The paged path takes fp16 queries and reads a chunk's own keys back from the fp16 pool; the
+    reference attends an fp32 query and, in a prefill chunk, its own fp32 K/V (model.py:105-125,
+    183-187).  This measures that deviation on config-1 (decode) and config-3 (prefill chunk)
+    shapes against a float64 restatement with the unrounded inputs; it stays inside the fp16
+    tolerance (atol 2e-3 / rtol 1e-2) with a large margin."""
+    rng = np.random.default_rng(90)
+    # config 1: decode, 16 q / 8 kv heads, 512 keys
+    pool = rng.standard_normal((2, 32, 16, 8, 128), dtype=np.float32).astype(np.float16)
+    table = rng.permutation(32).astype(np.int32)[None]
+    q32 = rng.standard_normal((1, 16, 128), dtype=np.float32)
+    got = oracle.paged_attention(q32.astype(np.float16), pool, table, np.asarray([512], np.int32)).astype(np.float64)
+    kk = pool[0][table[0]].reshape(512, 8, 128).astype(np.float64)
+    vv = pool[1][table[0]].reshape(512, 8, 128).astype(np.float64)
+    ref = np.zeros((16, 128))
+    for h in range(16):
+        s = kk[:, h // 2] @ q32[0, h].astype(np.float64) / math.sqrt(128)
+        p = np.exp(s - s.max())
+        ref[h] = p @ vv[:, h // 2] / p.sum()
+    e1 = np.abs(got[0] - ref)
+    assert np.all(e1 <= 2e-3 + 1e-2 * np.abs(ref)) and e1.max() < 1e-3, e1.max()
+    # config 3 shapes: a 128-query chunk at position 1920 over 2048 keys; its own K/V in fp32
+    T, start = 128, 1920
+    table = rng.permutation(128).astype(np.int32)[None]
+    pool = rng.standard_normal((2, 128, 16, 8, 128), dtype=np.float32).astype(np.float16)
+    k32 = rng.standard_normal((T, 8, 128), dtype=np.float32)
+    v32 = rng.standard_normal((T, 8, 128), dtype=np.float32)
+    slots = oracle.slot_mapping(table, np.zeros(T, np.int32), np.arange(start, start + T, dtype=np.int32))
+    oracle.store_kv(pool, slots, None, k32.astype(np.float16), v32.astype(np.float16))
+    q32 = rng.standard_normal((T, 16, 128), dtype=np.float32)
+    got = oracle.paged_attention(q32.astype(np.float16)[None], pool, table,
+                                 np.asarray([start + T], np.int32))[0].astype(np.float64)
+    kk = pool[0][table[0]].reshape(2048, 8, 128).astype(np.float64)
+    vv = pool[1][table[0]].reshape(2048, 8, 128).astype(np.float64)
+    kk[start:], vv[start:] = k32, v32  # the reference attends the chunk's own fp32 K/V
+    e3 = 0.0
+    for h in range(16):
+        s = (q32[:, h].astype(np.float64) @ kk[:, h // 2].T) / math.sqrt(128)
+        s[np.triu(np.ones((T, 2048), bool), k=start + 1)] = -np.inf
+        p = np.exp(s - s.max(axis=1, keepdims=True))
+        ref = (p @ vv[:, h // 2]) / p.sum(axis=1, keepdims=True)
+        err = np.abs(got[:, h] - ref)
+        assert np.all(err <= 2e-3 + 1e-2 * np.abs(ref)), (h, err.max())
+        e3 = max(e3, float(err.max()))
+    assert e3 < 1e-3, e3
 
 
 def test_prep_skips_inactive_bad_slots_and_positions():

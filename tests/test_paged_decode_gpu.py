@@ -176,7 +176,7 @@ def test_config2_append_then_decode_28_layers(dev):
 
 
 def test_config4_stress_full_size(dev):
-    """B=256, L=8192, 131072 pages (8.6 GB pool), 5% x8 tail: oracle on 6 rows, sanity on all."""
+    """B=256, L=8192, 131072 pages (8.6 GB pool), 5% x8 tail: every row against the oracle."""
     say("decode config4 full")
     w = workloads.config4()
     g = torch.Generator(device=dev).manual_seed(404)
@@ -186,9 +186,7 @@ def test_config4_stress_full_size(dev):
                           max_seq_len=8192)
     torch.cuda.synchronize()
     assert torch.isfinite(out.float()).all()
-    rows = [0, 1, 77, 128, 200, 255]
-    ref = oracle_decode(pool, w.block_tables, w.seq_lens, q, rows=rows)
-    assert_attn_close(out[rows], ref, "config4 sample")
+    assert_attn_close(out, oracle_decode(pool, w.block_tables, w.seq_lens, q), "config4 all rows")
     # every output is a convex combination of V rows: bounded by the row-wise V extremes
     vmax = pool[1].abs().amax().float()
     assert float(out.float().abs().max()) <= float(vmax) * (1 + 1e-3)
@@ -213,8 +211,7 @@ def test_config5_prefix_shared_with_churn(dev):
         pool[:, idx] = randn16((2, len(new), 16, 8, 128), g, dev)
         q = randn16((w.batch, 32, 128), g, dev)
         out = paged_attention(q, pool, to_dev(table, dev), to_dev(w.seq_lens, dev), None)
-        rows = [0, 31, 63]
-        assert_attn_close(out[rows], oracle_decode(pool, table, w.seq_lens, q, rows=rows), f"config5 step {step}")
+        assert_attn_close(out, oracle_decode(pool, table, w.seq_lens, q), f"config5 step {step}, all rows")
 
 
 def test_long_context_uses_many_partitions(dev):

@@ -61,23 +61,32 @@ def test_chunked_equals_unchunked_and_decode(dev):
 
 
 def test_config3_append_then_attend_all_chunks(dev):
-    """Config 3 on one layer: four 512-token chunks, each appended with store_kv then attended causally."""
+    """Config 3 on one layer: four 512-token chunks, each appended with store_kv then attended causally.
+
+    The oracle keeps its own host pool, written by its own store at the host-computed slots, so a
+    wrong store or slot on the GPU shows up both as a pool difference and in the attention.
+    """
     say("prefill config3")
     w = workloads.config3()
     g = torch.Generator(device=dev).manual_seed(303)
     pool = randn16((2, w.num_pages, 16, 8, 128), g, dev)
+    host_pool = pool.cpu().numpy()
     table = to_dev(w.block_table, dev)
     for c in range(4):
         start = c * w.chunk
         k = randn16((w.chunk, 8, 128), g, dev)
         v = randn16((w.chunk, 8, 128), g, dev)
         q = randn16((w.chunk, 16, 128), g, dev)
-        slots = to_dev(slot_mapping_for_positions(w.block_table, start, w.chunk), dev)
-        store_kv(pool, slots, None, k, v)
+        host_slots = oracle.slot_mapping(w.block_table[None], np.zeros(w.chunk, np.int32),
+                                         np.arange(start, start + w.chunk, dtype=np.int32))
+        assert np.array_equal(host_slots, slot_mapping_for_positions(w.block_table, start, w.chunk))
+        store_kv(pool, to_dev(host_slots, dev), None, k, v)
+        oracle.store_kv(host_pool, host_slots, None, k.cpu().numpy(), v.cpu().numpy())
         out = paged_attention(q, pool, table, None, None, query_start=start)
         total = start + w.chunk
-        sub, t2 = compact_for_oracle(pool, w.block_table[None], np.asarray([total]))
-        ref = oracle.paged_attention(q.cpu().numpy()[None], sub, t2, np.asarray([total], np.int32))[0]
+        assert np.array_equal(pool.cpu().numpy().view(np.uint16), host_pool.view(np.uint16)), f"chunk {c}: pool"
+        ref = oracle.paged_attention(q.cpu().numpy()[None], host_pool, w.block_table[None],
+                                     np.asarray([total], np.int32))[0]
         assert_attn_close(out, ref, f"chunk {c}")
 
 
@@ -134,3 +143,25 @@ def test_invalid_page_contributes_no_keys(dev):
     bad[2] = -1
     out = paged_attention(to_dev(q, dev), to_dev(pool, dev), to_dev(bad, dev), None, None, query_start=start)
     assert_attn_close(out, ref.astype(np.float32), "page id -1")
+
+
+def test_validate_reports_and_clears_the_error_flag(dev):
+    """Validate mode reads the workspace's error flag (set by a kernel whose bounded wait gave up),
+    raises, and clears it.  The flag is planted from the host: no kernel is made to time out."""
+    from infurnace_amd import _capi
+    from infurnace_amd.kernels import PagedAttentionError
+    from infurnace_amd.kernels.paged_attention import workspace_for
+    say("prefill validate / error flag")
+    rng = np.random.default_rng(26)
+    pool, table = _seq(rng, 1024, 16, 8, 128)
+    q = rng.standard_normal((256, 16, 128), dtype=np.float32).astype(np.float16)
+    P, T, Q = to_dev(pool, dev), to_dev(table, dev), to_dev(q, dev)
+    ok = paged_attention(Q, P, T, None, None, query_start=768, validate=True)
+    ws = workspace_for(dev, torch.cuda.current_stream(dev).cuda_stream, 0)
+    off = _capi.WORKSPACE_ERROR_FLAG_OFFSET
+    ws[off] = 1
+    with pytest.raises(PagedAttentionError):
+        paged_attention(Q, P, T, None, None, query_start=768, validate=True)
+    assert not bool(ws[off:off + 4].any())
+    again = paged_attention(Q, P, T, None, None, query_start=768, validate=True)
+    assert torch.equal(ok.view(torch.int16), again.view(torch.int16))

@@ -97,8 +97,11 @@ def test_engine_sequence_of_prefills_decodes_and_slot_reuse(dev):
     for _ in range(5):
         filled = decode([(0, True), (1, True), (2, False)])
     assert list(filled[0][:3]) == run.mgr.blocks(0)[:3]
-    freed = run.clear_slot(0, zero=True)
-    assert freed and all(torch.all(run.cache.kv[:, :, p] == 0) for p in freed)
+    owned = run.mgr.blocks(0)
+    freed = run.clear_slot(0, zero=True)   # pages the last step still uses come back once it completes
+    freed += run.synchronize()
+    assert sorted(freed) == sorted(owned)
+    assert all(torch.all(run.cache.kv[:, :, p] == 0) for p in freed)
     ref.clear(0)
     prefill(0, 0, 10)          # the slot is reused from position 0
     for _ in range(3):

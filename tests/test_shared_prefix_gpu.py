@@ -118,8 +118,7 @@ def test_config5_full_size_with_churn(dev):
         q = randn16((w.batch, 32, 128), g, dev)
         tdev, ldev = to_dev(table, dev), to_dev(w.seq_lens, dev)
         out = paged_attention(q, pool, tdev, ldev, None, shared_prefix_pages=prefix)
-        rows = [0, 17, 31, 63]
-        assert_attn_close(out[rows], oracle_decode(pool, table, w.seq_lens, q, rows=rows), f"config5 step {step}")
+        assert_attn_close(out, oracle_decode(pool, table, w.seq_lens, q), f"config5 step {step}, all rows")
         plain = paged_attention(q, pool, tdev, ldev, None)
         assert_attn_close(out, plain.cpu().numpy(), f"config5 step {step} vs ifn_paged_decode")
 
