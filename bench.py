@@ -3,23 +3,27 @@
 
 Workload (config 2): Qwen3-0.6B ragged batched decode over all 28 layers, fp16,
 batch 32, context lengths U[128, 4096], 16-token pages in a 16384-page pool per
-layer.  One step = for each of the 28 layers: store_kv (one new token per
-sequence) then paged decode attention, launched back to back on one stream
-through the C ABI (no Python validation inside the timed region).
+layer.  One step = the step plan (one launch: the split of the batch's keys over
+the CUs, shared by all layers), then for each of the 28 layers store_kv (one new
+token per sequence) and paged decode attention, launched back to back on one
+stream through the C ABI (no Python validation inside the timed region).
 
 Reported:
   value            paged-decode attention HBM GB/s = algorithmic decode bytes /
-                   decode kernel time, both summed over the K timed steps; the
-                   kernel time comes from HIP events recorded on the launch stream
-                   around every decode launch
+                   (decode kernel time + the step plan's time / 28), summed over
+                   the K timed steps; the times come from HIP events recorded on the
+                   launch stream around every launch
   kv_append_us_per_layer   the same events around every store_kv launch
-  roofline         the decode kernel against 8 TB/s HBM; traffic (HBM bytes per
-                   launch from rocprofv3 FETCH_SIZE/WRITE_SIZE) is read from the
-                   committed profile summary when it exists
+  roofline         the decode kernel against 8 TB/s HBM (its own launches); traffic
+                   (HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE) is read
+                   from the committed profile summary when it exists
   append_batched   the bandwidth-sized append (28 layers x 2048 tokens, one
                    launch) against 8 TB/s
-  cpu_baseline     the CPU oracle (plain C port of the same algorithm, one core)
-                   on a bounded sample of the same decode workload
+  config1          the CPU-runnable case: one token's append + decode, µs per call
+  cpu_baseline     the CPU oracle (plain C port of the same algorithm) on all the
+                   host cores this process may use (one thread per block of rows),
+                   on a bounded sample of the same decode workload; the one-thread
+                   figure beside it
 """
 from __future__ import annotations
 
@@ -92,26 +96,43 @@ def _compact(pool_layer, table, lens, bs=16):
 
 
 def run_cpu_baseline(w, pool_layer, q, seconds: float) -> dict:
+    """The oracle on config-2 decode rows of one layer: all rows per pass, rows split over the host
+    threads (one block of rows each), repeated for about ``seconds``; then the same on one thread
+    for about a third of that."""
     import oracle
     sub, t2 = _compact(pool_layer, w.block_tables, w.seq_lens)
     qn = q.cpu().numpy()
-    rows = 0
-    nbytes = 0
-    t0 = time.perf_counter()
-    while True:
-        for b in range(w.batch):
-            oracle.paged_attention(qn[b:b + 1], sub, t2[b:b + 1], w.seq_lens[b:b + 1])
-            rows += 1
-            nbytes += int(w.seq_lens[b]) * 2 * w.num_kv_heads * w.head_dim * 2 + 2 * w.num_q_heads * w.head_dim * 2
-            if time.perf_counter() - t0 >= seconds:
-                break
-        if time.perf_counter() - t0 >= seconds:
-            break
-    dt = time.perf_counter() - t0
-    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": 1, "kind": "port",
-            "sample": f"CPU oracle (oracle/ifn_oracle.c, scalar C, 1 thread) on {rows} config-2 decode rows "
-                      f"of layer 0 ({nbytes / 1e6:.1f} MB algorithmic) in {dt:.1f} s",
-            "cpu_model": _cpu_model()}
+    tok = 2 * w.num_kv_heads * w.head_dim * 2
+    row_bytes = [int(L) * tok + 2 * w.num_q_heads * w.head_dim * 2 for L in w.seq_lens]
+    threads = oracle.host_threads()
+
+    def timed(fn, budget):
+        passes, t0 = 0, time.perf_counter()
+        while True:
+            fn()
+            passes += 1
+            if time.perf_counter() - t0 >= budget:
+                return passes, time.perf_counter() - t0
+
+    passes, dt = timed(lambda: oracle.paged_attention_rows(qn, sub, t2, w.seq_lens, threads=threads), seconds)
+    nbytes = passes * sum(row_bytes)
+    rows1, bytes1, t0 = 0, 0, time.perf_counter()
+    while time.perf_counter() - t0 < seconds / 3:
+        b = rows1 % w.batch
+        oracle.paged_attention(qn[b:b + 1], sub, t2[b:b + 1], w.seq_lens[b:b + 1])
+        rows1 += 1
+        bytes1 += row_bytes[b]
+    dt1 = time.perf_counter() - t0
+    try:
+        affinity = len(os.sched_getaffinity(0))
+    except AttributeError:
+        affinity = os.cpu_count() or 1
+    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"CPU oracle (oracle/ifn_oracle.c, scalar C) on all 32 config-2 decode rows of layer 0, "
+                      f"{passes} passes ({nbytes / 1e6:.1f} MB algorithmic) in {dt:.1f} s, rows split over "
+                      f"{threads} threads",
+            "single_thread_GB/s": round(bytes1 / dt1 / 1e9, 4),
+            "affinity_cores": affinity, "cpu_model": _cpu_model()}
 
 
 def _cpu_model() -> str:
@@ -339,6 +360,166 @@ def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> di
     return res
 
 
+def run_config1(lib, hip, dev, stream, reps: int = 200) -> dict:
+    """Config 1 (the CPU-runnable case): one token's append at position 511 and single-row decode over
+    512 tokens, timed as two launches (ifn_store_kv + ifn_paged_decode) and as one fused launch
+    (ifn_paged_decode_append); µs per call from HIP events, median over ``reps`` calls."""
+    import torch
+    c = workloads_mod().config1()
+    pool = torch.from_numpy(c["pool"]).to(dev)
+    P = pool.shape[1]
+    bt = torch.from_numpy(c["block_tables"]).to(dev)
+    sl = torch.from_numpy(c["seq_lens"]).to(dev)
+    slots = torch.from_numpy(c["slot_mapping"]).to(dev)
+    q, k, v = (torch.from_numpy(c[n]).to(dev) for n in ("q", "new_k", "new_v"))
+    out = torch.empty_like(q)
+    ws_bytes = lib.ifn_paged_decode_workspace_bytes(1, 16, 8, 128, 16, 512)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    scale = float(c["scale"])
+
+    def two():
+        rc = lib.ifn_store_kv(pool.data_ptr(), P, slots.data_ptr(), None, k.data_ptr(), v.data_ptr(), 1, 8, 128, 16,
+                              stream)
+        return rc | lib.ifn_paged_decode(out.data_ptr(), q.data_ptr(), pool.data_ptr(), P, bt.data_ptr(), 32,
+                                         sl.data_ptr(), None, 1, 16, 8, 128, 16, 512, scale, ws.data_ptr(), ws_bytes,
+                                         stream)
+
+    def fused():
+        return lib.ifn_paged_decode_append(out.data_ptr(), q.data_ptr(), pool.data_ptr(), P, bt.data_ptr(), 32,
+                                           sl.data_ptr(), None, slots.data_ptr(), k.data_ptr(), v.data_ptr(), 1, 16,
+                                           8, 128, 16, 512, scale, ws.data_ptr(), ws_bytes, stream)
+
+    res = {"workload": "config 1: B=1, context 512, 64-page pool, one layer (append at 511 + decode)"}
+    for name, fn in (("two_launch", two), ("fused", fused)):
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        evs = hip.create(2 * reps)
+        t0 = time.perf_counter()
+        for r in range(reps):
+            hip.hip.hipEventRecord(evs[2 * r], stream)
+            rc = fn()
+            hip.hip.hipEventRecord(evs[2 * r + 1], stream)
+            if rc:
+                raise RuntimeError(f"config 1 {name}: launch failed: {rc}")
+        torch.cuda.synchronize()
+        wall_us = (time.perf_counter() - t0) / reps * 1e6
+        res[f"{name}_us"] = round(float(np.median([hip.elapsed_ms(evs[2 * r], evs[2 * r + 1])
+                                                   for r in range(reps)])) * 1e3, 2)
+        res[f"{name}_host_us_per_call"] = round(wall_us, 2)  # launch rate through ctypes, back to back
+        hip.destroy(evs)
+    return res
+
+
+def workloads_mod():
+    from infurnace_amd import workloads
+    return workloads
+
+
+def run_config5_churn(lib, hip, dev, g, stream, steps: int) -> dict:
+    """Config 5 as serving runs it: each step first churns 10% of the private pages (KVManager.replace_blocks
+    frees them and takes fresh ones), uploads the new block tables, rewrites the fresh pages of all 36 layers
+    (one ifn_store_kv_layers launch over their 16 slots each), then for each layer appends one token per row
+    (ifn_store_kv) and decodes through the shared-prefix entry point.
+
+    The pages come from a BlockPool handing out ids in the workload's seeded order, so the first step's
+    tables are the workload's own.  Decode µs per layer (HIP events around every decode launch) and whole
+    step ms (host clock, churn bookkeeping included) are reported separately."""
+    import torch
+    from infurnace_amd.cache import BlockPool, KVManager
+    w = workloads_mod().config5()
+    L, B, hq, hkv, d, P = w.num_layers, w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.num_pages
+    sp = w.shared_prefix_pages
+    perm = np.concatenate([w.block_tables[0, :sp], w.block_tables[:, sp:].reshape(-1), w.extra["free_ids"]])
+    bpool = BlockPool(P, 16, reserve_dummy=False, order=perm)
+    mgr = KVManager(bpool, max_pages_per_seq=w.max_pages)
+    prefix = bpool.allocate(sp)
+    for b in range(B):
+        mgr.add_sequence(b, prefix_blocks=prefix, prefix_len=sp * 16)
+        mgr.append(b, int(w.seq_lens[b]) - sp * 16)
+    rows = list(range(B))
+    table = mgr.block_tables(rows, max_pages=w.max_pages)
+    assert np.array_equal(table, w.block_tables), "config 5: the pool's order does not reproduce the tables"
+
+    pool = torch.empty((L, 2, P, 16, hkv, d), dtype=torch.float16, device=dev)
+    for layer in range(L):
+        pool[layer].normal_(generator=g)
+    q = torch.randn((L, B, hq, d), generator=g, device=dev, dtype=torch.float16)
+    nk = torch.randn((L, B, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    n_fresh = max(len(c) for c in w.extra["churn"])
+    rk = torch.randn((L, n_fresh * 16, hkv, d), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty((B, hq, d), dtype=torch.float16, device=dev)
+    bt = torch.from_numpy(table).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    slots = torch.empty(B, dtype=torch.int32, device=dev)
+    fresh_slots = torch.empty(n_fresh * 16, dtype=torch.int32, device=dev)
+    prefix_d = torch.as_tensor(np.asarray(prefix, np.int32), device=dev)
+    max_len = int(w.seq_lens.max())
+    ws_bytes = lib.ifn_paged_decode_shared_prefix_workspace_bytes(B, hq, hkv, d, 16, sp)
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    lb = pool[0].numel() * 2
+    scale = 1.0 / np.sqrt(d)
+    pos = w.seq_lens.astype(np.int64) - 1
+
+    def step(s_, evs=None, base=0):
+        # churn: free 10% of the private pages and take fresh ones (host bookkeeping)
+        ch = w.extra["churn"][s_ % len(w.extra["churn"])]
+        fresh = []
+        for b in np.unique(ch[:, 0]):
+            fresh += mgr.replace_blocks(int(b), ch[ch[:, 0] == b, 1].tolist())
+        tab = mgr.block_tables(rows, max_pages=w.max_pages)
+        app = (tab[np.arange(B), pos // 16].astype(np.int64) * 16 + pos % 16).astype(np.int32)
+        fs = (np.repeat(np.asarray(fresh, np.int64) * 16, 16) + np.tile(np.arange(16), len(fresh))).astype(np.int32)
+        # uploads on the launch stream (pinned staging keeps them asynchronous and stream-ordered)
+        bt.copy_(torch.from_numpy(tab).pin_memory(), non_blocking=True)
+        slots.copy_(torch.from_numpy(app).pin_memory(), non_blocking=True)
+        fresh_slots[:len(fs)].copy_(torch.from_numpy(fs).pin_memory(), non_blocking=True)
+        # rewrite the fresh pages of every layer: one launch, 16 slots per page
+        rc = lib.ifn_store_kv_layers(pool.data_ptr(), L, P, fresh_slots.data_ptr(), None, rk.data_ptr(),
+                                     rk.data_ptr(), len(fs), hkv, d, 16, stream)
+        for layer in range(L):
+            rc |= lib.ifn_store_kv(pool.data_ptr() + layer * lb, P, slots.data_ptr(), None, nk[layer].data_ptr(),
+                                   nk[layer].data_ptr(), B, hkv, d, 16, stream)
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 2 * layer], stream)
+            rc |= lib.ifn_paged_decode_shared_prefix(
+                out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P, prefix_d.data_ptr(), sp,
+                bt.data_ptr(), w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, ws.data_ptr(),
+                ws_bytes, stream)
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 2 * layer + 1], stream)
+        if rc:
+            raise RuntimeError(f"config 5 step {s_}: launch failed: {rc}")
+        return len(fresh)
+
+    step(0)
+    torch.cuda.synchronize()
+    evs = hip.create(2 * L * steps)
+    t0 = time.perf_counter()
+    churned = [step(1 + s_, evs, 2 * L * s_) for s_ in range(steps)]
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    us = float(np.mean([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(L * steps)])) * 1e3
+    hip.destroy(evs)
+    bpool.check_invariants()
+    # the roofline counts each physical page once, for the tables the timed steps used
+    w_now = workloads_mod().DecodeWorkload(w.name, L, hq, hkv, d, P, w.seq_lens,
+                                           mgr.block_tables(rows, max_pages=w.max_pages), w.seed,
+                                           shared_prefix_pages=sp)
+    uniq = w_now.decode_bytes(unique=True)
+    logical = w_now.decode_bytes()
+    del pool, rk
+    gbps = uniq / (us / 1e6) / 1e9
+    return {"workload": w.name + ", 36 layers, 10% private-page churn per step", "steps_timed": steps,
+            "entry": "ifn_paged_decode_shared_prefix", "pages_churned_per_step": int(np.mean(churned)),
+            "decode_us_per_layer": round(us, 2), "bytes_per_layer": uniq, "GB/s": round(gbps, 1),
+            "frac": round(gbps / HBM_PEAK_GBPS, 4), "logical_bytes_per_layer": logical,
+            "effective_GB/s": round(logical / (us / 1e6) / 1e9, 1),
+            "ms_per_step": round(wall / steps * 1e3, 3),
+            "step": "churn (replace_blocks) + table upload + fresh-page rewrite (store_kv_layers) + 36 x "
+                    "(store_kv + shared-prefix decode)"}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=int(os.environ.get("WORLD_SIZE", "1")))
@@ -388,24 +569,38 @@ def main() -> int:
     scale = 1.0 / np.sqrt(d)
 
     layer_bytes = pool[0].numel() * 2
+    # the step plan: the split of the batch's keys over the CUs, shared by every layer of the step
+    plan_bytes = lib.ifn_paged_decode_plan_bytes(B, hq, hkv, d, 16, w.max_pages, max_len)
+    plan = torch.zeros(max(plan_bytes, 256), dtype=torch.uint8, device=dev)
+    plan_args = (plan.data_ptr(), plan_bytes, bt.data_ptr(), w.max_pages, sl.data_ptr(), None, slots.data_ptr(), P,
+                 B, hq, hkv, d, 16, max_len, stream)
     store_args = [(pool.data_ptr() + i * layer_bytes, P, slots.data_ptr(), None, nk[i].data_ptr(), nv[i].data_ptr(),
                    B, hkv, d, 16, stream) for i in range(L)]
     dec_args = [(out[i].data_ptr(), q[i].data_ptr(), pool.data_ptr() + i * layer_bytes, P, bt.data_ptr(),
-                 w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, ws.data_ptr(), ws_bytes,
-                 stream) for i in range(L)]
-    store_fn, dec_fn = lib.ifn_store_kv, lib.ifn_paged_decode
+                 w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, plan.data_ptr(), plan_bytes,
+                 ws.data_ptr(), ws_bytes, stream) for i in range(L)]
+    plan_fn, store_fn, dec_fn = lib.ifn_paged_decode_plan, lib.ifn_store_kv, lib.ifn_paged_decode_planned
     hip = HipEvents()
+    E = 2 + 3 * L  # events per step: the plan, then store_kv and decode per layer
 
     def step(evs=None, base=0):
+        if evs is not None:
+            hip.hip.hipEventRecord(evs[base], stream)
+        rc = plan_fn(*plan_args)
+        if evs is not None:
+            hip.hip.hipEventRecord(evs[base + 1], stream)
+        if rc:
+            raise RuntimeError(f"plan launch failed: {_capi.status_string(rc)}")
         for i in range(L):
+            b = base + 2 + 3 * i
             if evs is not None:
-                hip.hip.hipEventRecord(evs[base + 3 * i], stream)
+                hip.hip.hipEventRecord(evs[b], stream)
             rc = store_fn(*store_args[i])
             if evs is not None:
-                hip.hip.hipEventRecord(evs[base + 3 * i + 1], stream)
+                hip.hip.hipEventRecord(evs[b + 1], stream)
             rc |= dec_fn(*dec_args[i])
             if evs is not None:
-                hip.hip.hipEventRecord(evs[base + 3 * i + 2], stream)
+                hip.hip.hipEventRecord(evs[b + 2], stream)
             if rc:
                 raise RuntimeError(f"launch failed in layer {i}: {_capi.status_string(rc)}")
 
@@ -413,50 +608,78 @@ def main() -> int:
         step()
     torch.cuda.synchronize()
     K = args.steps
-    evs = hip.create(3 * L * K)
+    evs = hip.create(E * K)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for s in range(K):
-        step(evs, 3 * L * s)
+    for s_ in range(K):
+        step(evs, E * s_)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    dec_ms = [hip.elapsed_ms(evs[3 * j + 1], evs[3 * j + 2]) for j in range(L * K)]
-    app_ms = [hip.elapsed_ms(evs[3 * j], evs[3 * j + 1]) for j in range(L * K)]
+    plan_ms = [hip.elapsed_ms(evs[E * s_], evs[E * s_ + 1]) for s_ in range(K)]
+    dec_ms = [hip.elapsed_ms(evs[E * s_ + 2 + 3 * i + 1], evs[E * s_ + 2 + 3 * i + 2]) for s_ in range(K)
+              for i in range(L)]
+    app_ms = [hip.elapsed_ms(evs[E * s_ + 2 + 3 * i], evs[E * s_ + 2 + 3 * i + 1]) for s_ in range(K)
+              for i in range(L)]
     hip.destroy(evs)
     print(f"[bench] timed {K} steps x {L} layers in {wall:.3f} s", file=sys.stderr, flush=True)
 
-    # The same step with the append fused into the decode launch (ifn_paged_decode_append): one
-    # launch per layer instead of two, same output and pool bytes.
+    # The same decode launches without a plan (each launch splits the batch itself), for comparison.
+    unplanned_args = [a[:15] + a[17:] for a in dec_args]
+    uevs = hip.create(2 * L * 2)
+    for r in range(2):
+        for i in range(L):
+            hip.hip.hipEventRecord(uevs[2 * (r * L + i)], stream)
+            rc = lib.ifn_paged_decode(*unplanned_args[i])
+            hip.hip.hipEventRecord(uevs[2 * (r * L + i) + 1], stream)
+            if rc:
+                raise RuntimeError(_capi.status_string(rc))
+    torch.cuda.synchronize()
+    unplanned_us = float(np.mean([hip.elapsed_ms(uevs[2 * j], uevs[2 * j + 1]) for j in range(L, 2 * L)])) * 1e3
+    hip.destroy(uevs)
+
+    # The same step with the append fused into the decode launch (ifn_paged_decode_append_planned): one
+    # launch per layer after the plan, same output and pool bytes.
     fused_args = [(out[i].data_ptr(), q[i].data_ptr(), pool.data_ptr() + i * layer_bytes, P, bt.data_ptr(),
                    w.max_pages, sl.data_ptr(), None, slots.data_ptr(), nk[i].data_ptr(), nv[i].data_ptr(), B, hq,
-                   hkv, d, 16, max_len, scale, ws.data_ptr(), ws_bytes, stream) for i in range(L)]
-    fused_fn = lib.ifn_paged_decode_append
+                   hkv, d, 16, max_len, scale, plan.data_ptr(), plan_bytes, ws.data_ptr(), ws_bytes, stream)
+                  for i in range(L)]
+    fused_fn = lib.ifn_paged_decode_append_planned
+    EF = 2 + 2 * L
 
     def fused_step(evs=None, base=0):
+        if evs is not None:
+            hip.hip.hipEventRecord(evs[base], stream)
+        rc = plan_fn(*plan_args)
+        if evs is not None:
+            hip.hip.hipEventRecord(evs[base + 1], stream)
         for i in range(L):
             if evs is not None:
-                hip.hip.hipEventRecord(evs[base + 2 * i], stream)
-            rc = fused_fn(*fused_args[i])
+                hip.hip.hipEventRecord(evs[base + 2 + 2 * i], stream)
+            rc |= fused_fn(*fused_args[i])
             if evs is not None:
-                hip.hip.hipEventRecord(evs[base + 2 * i + 1], stream)
+                hip.hip.hipEventRecord(evs[base + 3 + 2 * i], stream)
             if rc:
                 raise RuntimeError(f"fused launch failed in layer {i}: {_capi.status_string(rc)}")
 
     for _ in range(args.warmup):
         fused_step()
     torch.cuda.synchronize()
-    fevs = hip.create(2 * L * K)
+    fevs = hip.create(EF * K)
     t0 = time.perf_counter()
     for s_ in range(K):
-        fused_step(fevs, 2 * L * s_)
+        fused_step(fevs, EF * s_)
     torch.cuda.synchronize()
     fused_wall = time.perf_counter() - t0
-    fused_ms = [hip.elapsed_ms(fevs[2 * j], fevs[2 * j + 1]) for j in range(L * K)]
+    fused_ms = [hip.elapsed_ms(fevs[EF * s_ + 2 + 2 * i], fevs[EF * s_ + 3 + 2 * i]) for s_ in range(K)
+                for i in range(L)]
     hip.destroy(fevs)
 
     dec_bytes = w.decode_bytes()
-    dec_s = float(np.mean(dec_ms)) / 1e3
-    gbps = dec_bytes / dec_s / 1e9
+    dec_s = float(np.mean(dec_ms)) / 1e3            # the decode kernel, per launch
+    plan_s = float(np.mean(plan_ms)) / 1e3          # the step plan, once per step
+    layer_s = dec_s + plan_s / L                    # a layer's share of the step's decode work
+    gbps = dec_bytes / layer_s / 1e9
+    kernel_gbps = dec_bytes / dec_s / 1e9
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         try:
@@ -507,11 +730,15 @@ def main() -> int:
         print("[bench] config 4 (8.6 GB per layer) ...", file=sys.stderr, flush=True)
         extra["config4"] = run_decode_config(lib, hip, dev, g, stream, workloads.config4(), layers=1, reps=10)
         torch.cuda.empty_cache()
-        print("[bench] config 5 (Qwen3-8B shapes, shared prefix) ...", file=sys.stderr, flush=True)
-        extra["config5"] = run_decode_config(lib, hip, dev, g, stream, workloads.config5(), layers=36, reps=3)
+        print("[bench] config 5 (Qwen3-8B shapes, shared prefix, page churn) ...", file=sys.stderr, flush=True)
+        extra["config5"] = run_config5_churn(lib, hip, dev, g, stream, steps=4)
+        torch.cuda.empty_cache()
+        extra["config5"]["no_churn"] = run_decode_config(lib, hip, dev, g, stream, workloads.config5(), layers=36,
+                                                         reps=3)
         torch.cuda.empty_cache()
     else:
         cpu_pool = pool[0]
+    config1 = run_config1(lib, hip, dev, stream)
 
     if args.profile_pass:
         src = torch.empty(1 << 29, dtype=torch.float16, device=dev).normal_(generator=g)
@@ -543,22 +770,28 @@ def main() -> int:
                    "pages_per_layer": P, "context_tokens": int(w.seq_lens.sum()), "layers": L, "seed": w.seed},
         "decode_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
         "decode_us_per_layer": round(dec_s * 1e6, 3),
+        "plan_us_per_step": round(plan_s * 1e6, 3),
+        "decode_kernel_GB/s": round(kernel_gbps, 2),
+        "unplanned_decode_us_per_layer": round(unplanned_us, 3),
         "decode_bytes_per_layer": dec_bytes,
         "kv_append_us_per_layer": round(float(np.mean(app_ms)) * 1e3, 3),
-        "fused_step": {"entry": "ifn_paged_decode_append (store_kv + paged decode in one launch per layer)",
+        "fused_step": {"entry": "ifn_paged_decode_append_planned (store_kv + paged decode in one launch per "
+                                "layer, after the step plan)",
                        "us_per_layer": round(float(np.mean(fused_ms)) * 1e3, 3),
                        "two_launch_us_per_layer": round((float(np.mean(app_ms)) + float(np.mean(dec_ms))) * 1e3, 3),
                        # what the append adds to a decode launch when fused into it
                        "append_marginal_us_per_layer": round((float(np.mean(fused_ms)) - float(np.mean(dec_ms))) * 1e3,
                                                              3),
                        "ms_per_step": round(fused_wall / K * 1e3, 4)},
-        "roofline": {"bound": "hbm", "achieved": round(gbps, 2), "peak": HBM_PEAK_GBPS, "unit": "GB/s",
-                     "frac": round(gbps / HBM_PEAK_GBPS, 4), "traffic": traffic},
+        "roofline": {"bound": "hbm", "kernel": "decode_rows_kernel", "achieved": round(kernel_gbps, 2),
+                     "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
+                     "traffic": traffic},
         "append_batched": {"workload": "store_kv_layers, 28 layers x 2048 tokens (config 3 prompt), one launch",
                            "us": round(a_ms * 1e3, 2), "bytes": a_bytes, "GB/s": round(a_gbps, 2),
                            "frac": round(a_gbps / HBM_PEAK_GBPS, 4)},
         "prefill": prefill,
         "pre_append": pre_append,
+        "config1": config1,
         "config4": extra.get("config4"),
         "config5": extra.get("config5"),
         "cpu_baseline": cpu,
