@@ -50,6 +50,15 @@ constexpr int kMergeBatch = 20;      // split states loaded per round trip of th
 // next pays a second start-up, a second merge of its waves and possibly two split merges, so the
 // split counts each non-empty row as kRowStartCost tokens longer (virtual tokens in front of it).
 constexpr int kRowStartCost = 24;
+// Fewest virtual positions per range.  A row split over n ranges is merged by one workgroup that
+// reads n partial states (Hq x D floats each), so short batches are split over fewer workgroups:
+// one row of 512 keys takes 17 ranges of about 32 positions instead of one range per CU.
+constexpr int kMinRangePositions = 32;
+
+// Ranges of a call: one per workgroup, at most, and none empty of positions.
+__device__ __forceinline__ int64_t range_count(int64_t nb, int64_t T) {
+  return min(nb, (T + kMinRangePositions - 1) / kMinRangePositions);
+}
 
 // Step plan (int32 words).  Header: magic, batch, ranges nr, virtual positions T, grid, whether
 // appended slots were given, the row-length cap, 0.  Then the rows' offsets cum[batch + 1], then one
@@ -154,7 +163,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   const int tid = threadIdx.x;
   const int cap = min(max_pages * kRowsBlock, max_len);
   const int T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap);
-  const int nr = int(min<int64_t>(nb, T));
+  const int nr = int(range_count(nb, T));
   if (tid == 0) {
     plan[0] = kPlanMagic;
     plan[1] = batch;
@@ -345,9 +354,9 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     }
   };
 
-  // nr = min(workgroups, T) ranges, so that no range is empty (the split merge counts ranges).  A
+  // nr <= min(workgroups, T) ranges, so that no range is empty (the split merge counts ranges).  A
   // range may still hold no key (only virtual positions); it then has no piece and takes no ticket.
-  const int64_t nr = min(nb, T);
+  const int64_t nr = range_count(nb, T);
   if (blk >= nr) {
     finish();
     return;
