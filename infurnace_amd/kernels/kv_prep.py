@@ -23,6 +23,7 @@ import torch
 
 from .. import _capi
 from ._common import KVStoreError, check_pool, current_stream, ptr
+from ._carrier import accepts_carriers
 
 __all__ = ["qk_norm_rope_append", "rope_table", "zero_pages", "copy_pages"]
 
@@ -66,6 +67,7 @@ def _i32(name: str, t, n: int, device, dtypes=(torch.int32,)) -> torch.Tensor:
     return t
 
 
+@accepts_carriers
 def qk_norm_rope_append(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_weight: torch.Tensor,
                         k_norm_weight: torch.Tensor, rope: torch.Tensor, positions: torch.Tensor,
                         slot_mapping: torch.Tensor, active_mask: torch.Tensor | None, kv_pool: torch.Tensor, *,
@@ -118,6 +120,7 @@ def _full_pool(kv_pool) -> tuple:
     return kv_pool.shape
 
 
+@accepts_carriers
 def zero_pages(kv_pool: torch.Tensor, page_ids: torch.Tensor) -> None:
     """Zero K and V of every listed page in every layer (ids outside the pool are skipped)."""
     L, _, P, bs, hkv, d = _full_pool(kv_pool)
@@ -127,6 +130,7 @@ def zero_pages(kv_pool: torch.Tensor, page_ids: torch.Tensor) -> None:
                current_stream(kv_pool.device))
 
 
+@accepts_carriers
 def copy_pages(kv_pool: torch.Tensor, src_ids: torch.Tensor, dst_ids: torch.Tensor) -> None:
     """Copy page src_ids[i] to dst_ids[i] in every layer.  Destinations must be distinct and
     disjoint from the sources (checked here on the host)."""

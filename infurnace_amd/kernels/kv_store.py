@@ -23,6 +23,7 @@ import torch
 
 from .. import _capi
 from ._common import KVStoreError, check_pool, current_stream, ptr
+from ._carrier import accepts_carriers
 
 __all__ = ["store_kv", "store_kv_layers", "KVStoreError"]
 
@@ -67,6 +68,7 @@ def _debug_validate(slot_mapping: torch.Tensor, active_mask, num_slots: int) -> 
         raise KVStoreError("two active rows map to the same slot")
 
 
+@accepts_carriers
 def store_kv(kv_pool: torch.Tensor, slot_mapping: torch.Tensor, active_mask: torch.Tensor | None,
              new_k: torch.Tensor, new_v: torch.Tensor, *, layer: int = 0, validate: bool = False) -> None:
     """Append ``new_k``/``new_v`` [T, Hkv, D] fp16 into ``kv_pool`` in place.
@@ -93,6 +95,7 @@ def store_kv(kv_pool: torch.Tensor, slot_mapping: torch.Tensor, active_mask: tor
                T, hkv, d, bs, current_stream(dev))
 
 
+@accepts_carriers
 def store_kv_layers(kv_pool: torch.Tensor, slot_mapping: torch.Tensor, active_mask: torch.Tensor | None,
                     new_k: torch.Tensor, new_v: torch.Tensor, *, validate: bool = False) -> None:
     """Append one token batch into every layer with a single launch.

@@ -26,6 +26,7 @@ import torch
 
 from .. import _capi
 from ._common import PagedAttentionError, check_pool, current_stream, ptr
+from ._carrier import accepts_carriers
 
 __all__ = ["paged_attention", "store_kv_and_decode", "store_kv_and_prefill", "PagedAttentionError",
            "workspace_for", "DecodePlan", "decode_plan"]
@@ -80,6 +81,7 @@ def _plan_key(query_shape, slot_mapping, pool_layer, block_tables, sequence_leng
             sequence_lengths.data_ptr(), None if active_mask is None else active_mask.data_ptr(), int(max_seq_len))
 
 
+@accepts_carriers
 def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, sequence_lengths: torch.Tensor,
                 active_mask: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None, *,
                 layer: int = 0, block_size: int = 16, max_seq_len: int | None = None) -> DecodePlan:
@@ -149,6 +151,7 @@ def _check(name: str, t, shape: tuple, dtypes: tuple, device) -> None:
         raise PagedAttentionError(f"{name} must be contiguous")
 
 
+@accepts_carriers
 def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: torch.Tensor,
                     sequence_lengths: torch.Tensor | None, active_mask: torch.Tensor | None = None, *,
                     layer: int = 0, scale: float | None = None, query_start: int | None = None,
@@ -282,6 +285,7 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
     return out
 
 
+@accepts_carriers
 def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: torch.Tensor,
                         sequence_lengths: torch.Tensor, active_mask: torch.Tensor | None,
                         slot_mapping: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor, *, layer: int = 0,
@@ -352,6 +356,7 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
     return out
 
 
+@accepts_carriers
 def store_kv_and_prefill(query: torch.Tensor, kv_pool: torch.Tensor, block_table: torch.Tensor, new_k: torch.Tensor,
                          new_v: torch.Tensor, *, query_start: int, layer: int = 0, scale: float | None = None,
                          out: torch.Tensor | None = None, block_size: int = 16, validate: bool = False) -> torch.Tensor:
