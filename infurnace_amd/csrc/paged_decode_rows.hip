@@ -55,6 +55,15 @@ constexpr int kRowStartCost = 24;
 // one row of 512 keys takes 17 ranges of about 32 positions instead of one range per CU.
 constexpr int kMinRangePositions = 32;
 
+// floor(num / den) for 0 <= num < 2^52 and den > 0: a double quotient (off by less than one)
+// corrected by one step -- a few instructions instead of the 64-bit integer division routine.
+__device__ __forceinline__ int64_t div_floor(int64_t num, int64_t den) {
+  int64_t q = int64_t(double(num) / double(den));
+  if (q * den > num) --q;
+  else if ((q + 1) * den <= num) ++q;
+  return q;
+}
+
 // Ranges of a call: one per workgroup, at most, and none empty of positions.
 __device__ __forceinline__ int64_t range_count(int64_t nb, int64_t T) {
   return min(nb, (T + kMinRangePositions - 1) / kMinRangePositions);
@@ -160,8 +169,12 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   __shared__ int s_cum[kRowsMaxBatch + 1];
   __shared__ int s_wsum[kPlanThreads / kWave];
   __shared__ int s_p0[3][kPlanThreads];  // first piece of range r: row, a, e (rows < 0: none)
+  __shared__ int s_slot[kRowsMaxBatch];   // appended slot of each row (-1: none)
   const int tid = threadIdx.x;
   const int cap = min(max_pages * kRowsBlock, max_len);
+  const int64_t num_slots = num_pages * kRowsBlock;
+  if (slots != nullptr)  // loaded beside the lengths; build_offsets' barriers publish them
+    for (int i = tid; i < batch; i += kPlanThreads) s_slot[i] = row_slot(slots, active, i, num_slots);
   const int T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap);
   const int nr = int(range_count(nb, T));
   if (tid == 0) {
@@ -176,14 +189,13 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   }
   for (int i = tid; i <= batch; i += kPlanThreads) plan[kPlanHdr + i] = s_cum[i];
   int32_t* recs = plan + plan_rec0(batch);
-  const int64_t num_slots = num_pages * kRowsBlock;
   for (int r = tid; r < nb; r += kPlanThreads) {
     int32_t* rec = recs + int64_t(r) * kPlanRec;
     int n = 0;
     int p0b = -1, p0a = 0, p0e = 0;
     if (r < nr) {
-      const int64_t t0 = int64_t(T) * r / nr, t1 = int64_t(T) * (r + 1) / nr;
-      auto range_of = [&](int64_t t) -> int { return int(((t + 1) * nr - 1) / T); };
+      const int64_t t0 = div_floor(int64_t(T) * r, nr), t1 = div_floor(int64_t(T) * (r + 1), nr);
+      auto range_of = [&](int64_t t) -> int { return int(div_floor((t + 1) * nr - 1, T)); };
       int b = locate_row(s_cum, batch, t0);
       while (b < batch) {
         const int cb = s_cum[b] + kRowStartCost;
@@ -201,7 +213,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
               pc[2] = e;
               pc[3] = first;
               pc[4] = range_of(int64_t(cb) + len - 1) - first + 1;
-              pc[5] = slots != nullptr ? row_slot(slots, active, b, num_slots) : -1;
+              pc[5] = slots != nullptr ? s_slot[b] : -1;
             }
             if (n == 0) {
               p0b = b;
@@ -221,16 +233,28 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
     s_p0[2][r] = p0e;
   }
   __syncthreads();
-  for (int it = tid; it < nb * kPlanIds; it += kPlanThreads) {
-    const int r = it / kPlanIds, i = it % kPlanIds;
-    const int b = s_p0[0][r];
-    int id = 0;
-    if (b >= 0) {
-      const int pg0 = s_p0[1][r] / kRowsBlock;
-      const int npg = (s_p0[2][r] - 1) / kRowsBlock - pg0 + 1;
-      id = block_tables[int64_t(b) * max_pages + pg0 + min(i, npg - 1)];
+  // The first window's page ids.  Wave w takes ranges w, w + 16, ...: lane i loads id i of a
+  // range (one coalesced 256-byte load per range), and all of a wave's loads are issued before
+  // its first store.
+  constexpr int kPlanWaves = kPlanThreads / kWave;
+  constexpr int kIdBatch = 16;
+  static_assert(kPlanIds == kWave, "one id per lane");
+  const int wave = tid / kWave, lane = tid % kWave;
+  for (int r0 = wave; r0 < nb; r0 += kPlanWaves * kIdBatch) {
+    int id[kIdBatch];
+#pragma unroll
+    for (int k = 0; k < kIdBatch; ++k) {
+      const int r = min(r0 + k * kPlanWaves, nb - 1);
+      const int b = s_p0[0][r];
+      const int pg0 = b >= 0 ? s_p0[1][r] / kRowsBlock : 0;
+      const int npg = b >= 0 ? (s_p0[2][r] - 1) / kRowsBlock - pg0 + 1 : 1;
+      id[k] = block_tables[int64_t(max(b, 0)) * max_pages + pg0 + min(lane, npg - 1)];
     }
-    recs[int64_t(r) * kPlanRec + 64 + i] = id;
+#pragma unroll
+    for (int k = 0; k < kIdBatch; ++k) {
+      const int r = r0 + k * kPlanWaves;
+      if (r < nb) recs[int64_t(r) * kPlanRec + 64 + lane] = s_p0[0][r] >= 0 ? id[k] : 0;
+    }
   }
 }
 
@@ -361,8 +385,8 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     finish();
     return;
   }
-  const int64_t t0 = T * blk / nr, t1 = T * (blk + 1) / nr;
-  auto range_of = [&](int64_t t) -> int64_t { return ((t + 1) * nr - 1) / T; };
+  const int64_t t0 = div_floor(T * blk, nr), t1 = div_floor(T * (blk + 1), nr);
+  auto range_of = [&](int64_t t) -> int64_t { return div_floor((t + 1) * nr - 1, T); };
   // The piece after row prev (prev < 0: the range's first piece); b >= batch: none.
   auto next_piece = [&](int prev) -> RowPiece {
     RowPiece P;
@@ -625,6 +649,17 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         for (int j0 = 0; j0 < np; j0 += GL) {
           const int cnt = min(GL, np - j0);
           const f32x2 ml = ld_dev2(r_ml, uint32_t(((slot0 + j0 + min(gj, cnt - 1)) * HQ + qh) * 2 * 4));
+          // The first kMergeBatch O slices go out with the (m, l) loads: their addresses do not
+          // depend on the weights, so a row of up to kMergeBatch states costs one round trip.  Only
+          // the cnt states that exist are loaded (cnt is uniform): the merging CU's own bandwidth
+          // bounds this step, at Hq * D * 4 bytes per state.
+          f32x4 oj[kMergeBatch];
+#pragma unroll
+          for (int u = 0; u < kMergeBatch; ++u) {
+            oj[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+            if (u < cnt) oj[u] = ld_dev4(r_o, uint32_t(((slot0 + j0 + u) * HQ + qh) * D * 4 + d4 * 16));
+          }
+          __builtin_amdgcn_sched_barrier(0);
           const float mj = gj < cnt ? ml[0] : kNegBig;
           float gm = mj;
 #pragma unroll
@@ -639,10 +674,11 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
           for (int o = 1; o < GL; o <<= 1) ls += __shfl_xor(ls, o);
           L = fmaf(L, sc, ls);
           for (int u0 = 0; u0 < cnt; u0 += kMergeBatch) {
-            f32x4 oj[kMergeBatch];
+            if (u0 > 0) {
 #pragma unroll
-            for (int u = 0; u < kMergeBatch; ++u)
-              oj[u] = ld_dev4(r_o, uint32_t(((slot0 + j0 + min(u0 + u, cnt - 1)) * HQ + qh) * D * 4 + d4 * 16));
+              for (int u = 0; u < kMergeBatch; ++u)
+                if (u0 + u < cnt) oj[u] = ld_dev4(r_o, uint32_t(((slot0 + j0 + u0 + u) * HQ + qh) * D * 4 + d4 * 16));
+            }
 #pragma unroll
             for (int u = 0; u < kMergeBatch; ++u) {
               const float w = __shfl(wj, gbase + min(u0 + u, cnt - 1));
