@@ -279,6 +279,69 @@ def run_pre_append(lib, hip, dev, g, stream) -> dict:
             "frac": round(gbps / HBM_PEAK_GBPS, 4)}
 
 
+def run_prep_step(lib, hip, dev, g, stream, w, pool, plan, plan_bytes, ws, ws_bytes, steps: int) -> dict:
+    """Config 2's decode step from fp32 projections: per layer either the pre-append
+    (ifn_qk_norm_rope_append, 32 tokens) then the planned decode, or both in one launch
+    (ifn_paged_decode_prep_append).  Same plan, pool and workspace as the headline step; HIP events
+    around every launch."""
+    import torch
+    from infurnace_amd.kernels import rope_table
+    L, B, hq, hkv, d, P = w.num_layers, w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.num_pages
+    q32 = torch.randn((L, B, hq, d), generator=g, device=dev)
+    k32 = torch.randn((L, B, hkv, d), generator=g, device=dev)
+    v32 = torch.randn((L, B, hkv, d), generator=g, device=dev)
+    nw = torch.ones(d, device=dev) + 0.1 * torch.randn(d, generator=g, device=dev)
+    max_len = int(w.seq_lens.max())
+    rope = rope_table(max_len, d, 1e6, device=dev)
+    pos = torch.from_numpy((w.seq_lens - 1).astype(np.int32)).to(dev)
+    bt = torch.from_numpy(w.block_tables).to(dev)
+    sl = torch.from_numpy(w.seq_lens).to(dev)
+    slots = torch.from_numpy(w.append_slots).to(dev)
+    q16 = torch.empty((B, hq, d), dtype=torch.float16, device=dev)
+    out = torch.empty((B, hq, d), dtype=torch.float16, device=dev)
+    lb = pool[0].numel() * 2
+    scale = 1.0 / np.sqrt(d)
+
+    def two(i):
+        rc = lib.ifn_qk_norm_rope_append(q16.data_ptr(), q32[i].data_ptr(), k32[i].data_ptr(), v32[i].data_ptr(),
+                                         nw.data_ptr(), nw.data_ptr(), rope.data_ptr(), max_len, pos.data_ptr(),
+                                         slots.data_ptr(), None, pool.data_ptr() + i * lb, P, B, hq, hkv, d, 16, 1e-6,
+                                         stream)
+        return rc | lib.ifn_paged_decode_planned(out.data_ptr(), q16.data_ptr(), pool.data_ptr() + i * lb, P,
+                                                 bt.data_ptr(), w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16,
+                                                 max_len, scale, plan.data_ptr(), plan_bytes, ws.data_ptr(), ws_bytes,
+                                                 stream)
+
+    def one(i):
+        return lib.ifn_paged_decode_prep_append(out.data_ptr(), q32[i].data_ptr(), k32[i].data_ptr(),
+                                                v32[i].data_ptr(), nw.data_ptr(), nw.data_ptr(), rope.data_ptr(),
+                                                max_len, pos.data_ptr(), slots.data_ptr(), pool.data_ptr() + i * lb, P,
+                                                bt.data_ptr(), w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16,
+                                                max_len, scale, 1e-6, plan.data_ptr(), plan_bytes, ws.data_ptr(),
+                                                ws_bytes, stream)
+
+    res = {}
+    for name, fn in (("two_launch", two), ("fused", one)):
+        for i in range(L):
+            if fn(i):
+                raise RuntimeError(f"prep step ({name}) launch failed")
+        torch.cuda.synchronize()
+        evs = hip.create(2 * L * steps)
+        for s_ in range(steps):
+            for i in range(L):
+                hip.hip.hipEventRecord(evs[2 * (s_ * L + i)], stream)
+                fn(i)
+                hip.hip.hipEventRecord(evs[2 * (s_ * L + i) + 1], stream)
+        torch.cuda.synchronize()
+        res[name] = float(np.mean([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(L * steps)])) * 1e3
+        hip.destroy(evs)
+    return {"workload": "config 2 decode step from fp32 projections: q/k RMSNorm + rotary + fp16 cast + append, "
+                        "then planned decode, per layer",
+            "entry": "ifn_paged_decode_prep_append (one launch per layer, after the step plan)",
+            "us_per_layer": round(res["fused"], 3), "two_launch_us_per_layer": round(res["two_launch"], 3),
+            "layers": L, "steps": steps}
+
+
 def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> dict:
     """Decode leg for a second or third workload (configs 4 and 5): `layers` distinct layer pools,
     store_kv (one token per row) then decode per layer; HIP events around every decode launch.
@@ -673,6 +736,7 @@ def main() -> int:
     fused_ms = [hip.elapsed_ms(fevs[EF * s_ + 2 + 2 * i], fevs[EF * s_ + 3 + 2 * i]) for s_ in range(K)
                 for i in range(L)]
     hip.destroy(fevs)
+    prep_step = run_prep_step(lib, hip, dev, g, stream, w, pool, plan, plan_bytes, ws, ws_bytes, steps=4)
 
     dec_bytes = w.decode_bytes()
     dec_s = float(np.mean(dec_ms)) / 1e3            # the decode kernel, per launch
@@ -786,6 +850,7 @@ def main() -> int:
         "roofline": {"bound": "hbm", "kernel": "decode_rows_kernel", "achieved": round(kernel_gbps, 2),
                      "peak": HBM_PEAK_GBPS, "unit": "GB/s", "frac": round(kernel_gbps / HBM_PEAK_GBPS, 4),
                      "traffic": traffic},
+        "prep_step": prep_step,
         "append_batched": {"workload": "store_kv_layers, 28 layers x 2048 tokens (config 3 prompt), one launch",
                            "us": round(a_ms * 1e3, 2), "bytes": a_bytes, "GB/s": round(a_gbps, 2),
                            "frac": round(a_gbps / HBM_PEAK_GBPS, 4)},

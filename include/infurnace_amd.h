@@ -325,6 +325,38 @@ int ifn_qk_norm_rope_append(void* q_out, const float* q, const float* k, const f
                             int32_t head_dim, int32_t block_size, float eps, void* stream);
 
 /*
+ * One decode step of one layer from the fp32 projections, in one launch:
+ * the pre-append of ifn_qk_norm_rope_append (q/k RMSNorm and rotary at
+ * positions[b], k/v cast to fp16 and stored at slot_mapping[b]) and the
+ * attention of ifn_paged_decode_planned over the result.  q: fp32
+ * [batch][num_q_heads][head_dim]; k, v: fp32 [batch][num_kv_heads][head_dim];
+ * the other arguments as in those two calls (plan may be NULL; a plan must
+ * be built with slot_mapping).  `out` and the pool are bit-identical to
+ * ifn_qk_norm_rope_append(...) followed by ifn_paged_decode_planned(...) on
+ * the normalised fp16 query; the fp16 query itself is not written.  The
+ * attention takes row b's appended token from the prepared k/v, at position
+ * positions[b] when slot_mapping[b] is that position's slot in the row's
+ * table (the decode step's invariant); the slot must not be read by any other
+ * row or position of the call.  All float arrays 16-byte aligned; head_dim a
+ * multiple of 8.  Shapes whose token row (num_kv_heads x head_dim fp16) is
+ * not 2 KiB, or head_dim > 128, return IFN_ERR_UNSUPPORTED (run the two calls
+ * instead).
+ * Replaces: model.py:183-200 (norm, rope, cast, store and SDPA of a decode
+ * step) as docs/architecture.md:245-246's store_kv then paged_attention.
+ */
+int ifn_paged_decode_prep_append(void* out, const float* q, const float* k, const float* v,
+                                 const float* q_norm_weight, const float* k_norm_weight,
+                                 const float* rope_table, int32_t max_positions,
+                                 const int32_t* positions, const int32_t* slot_mapping,
+                                 void* kv_pool_layer, int64_t num_pages, const int32_t* block_tables,
+                                 int32_t max_pages_per_seq, const int32_t* seq_lens,
+                                 const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
+                                 int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                 int32_t max_seq_len, float scale, float eps, const void* plan,
+                                 size_t plan_bytes, void* workspace, size_t workspace_bytes,
+                                 void* stream);
+
+/*
  * Zero the K and V of each listed page in every layer of the full pool
  * [num_layers][2][num_pages][block_size][num_kv_heads][head_dim].  Ids outside
  * [0, num_pages) are skipped.

@@ -63,6 +63,9 @@ SIGNATURES: dict[str, tuple] = {
                                                 _i32, _f32, _p, _sz, _p]),
     "ifn_qk_norm_rope_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _p, _i64,
                                                _i32, _i32, _i32, _i32, _i32, _f32, _p]),
+    "ifn_paged_decode_prep_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i64, _p, _i32,
+                                                    _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _p,
+                                                    _sz, _p, _sz, _p]),
     "ifn_zero_pages": (ctypes.c_int, [_p, _i32, _i64, _p, _i32, _i32, _i32, _i32, _p]),
     "ifn_copy_pages": (ctypes.c_int, [_p, _i32, _i64, _p, _p, _i32, _i32, _i32, _i32, _p]),
 }

@@ -198,6 +198,44 @@ struct DecodeAppend {
   f16* pool;                // the layer's pool (the same memory the kernel reads)
 };
 
+// ---- q/k RMSNorm and half-split rotary (model.py:11-13, :24-27) ---------------------------------
+// One definition of the arithmetic for the pre-append kernel and the decode kernel that fuses it,
+// with every operation rounded on its own (no contraction into fma), so that both produce the same
+// bits.  The sum of squares of a head is formed over the rotary pairs (x_i, x_{i + D/2}),
+// i < D/2, as the butterfly i ^ 1, i ^ 2, i ^ 4, ... of the pair sums.
+__device__ __forceinline__ float pair_sq(float x1, float x2) {
+#pragma clang fp contract(off)
+  return x1 * x1 + x2 * x2;
+}
+// 1 / sqrt(sum / D + eps), correctly rounded divide and square root.
+__device__ __forceinline__ float rms_inv(float ss, int d, float eps) { return 1.0f / sqrtf(ss / float(d) + eps); }
+// Normalise the pair with weights (w1, w2), then rotate it by the angle whose cos / sin are (c, s):
+// a = x1 rs w1, b = x2 rs w2 -> (a c - b s, b c + a s).
+__device__ __forceinline__ void norm_rope_pair(float& x1, float& x2, float rs, float w1, float w2, float c,
+                                               float s) {
+#pragma clang fp contract(off)
+  const float a = x1 * rs * w1;
+  const float b = x2 * rs * w2;
+  x1 = a * c - b * s;
+  x2 = b * c + a * s;
+}
+
+// Fused pre-append (decode): the step's fp32 projections are normalised, rotated and cast to fp16
+// inside the decode launch, as ifn_qk_norm_rope_append would do before it.  Row b's query heads are
+// q[b], its new K/V row k[b] / v[b]; its rotary position positions[b] selects the table row
+// [cos | sin] (a position outside [0, max_pos) gives a zero query and stores nothing).
+struct DecodePrep {
+  const float* q;         // [batch][Hq][D]
+  const float* k;         // [batch][Hkv][D]
+  const float* v;         // [batch][Hkv][D]
+  const float* q_norm_w;  // [D]
+  const float* k_norm_w;  // [D]
+  const float* rope;      // [max_pos][D]: cos of the D/2 angles, then their sin
+  const int32_t* positions;  // [batch]
+  int32_t max_pos;
+  float eps;
+};
+
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Number of CUs of the current device (queried once per device; 0 when there is none).
@@ -233,10 +271,13 @@ size_t rows_plan_bytes(int32_t batch, int blocks);
 int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
                      const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
                      int blocks, hipStream_t stream);
+// prep (non-null): the fused pre-append variant; ap then carries the slots and the pool, and q is unused.
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
-                       const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream);
+                       const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
+                       const DecodePrep* prep = nullptr);
+bool rows_prep_supported(int32_t hq, int32_t hkv, int32_t d);
 
 }  // namespace ifn
 

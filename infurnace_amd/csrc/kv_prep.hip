@@ -74,19 +74,17 @@ __global__ __launch_bounds__(kPrepThreads) void qk_norm_rope_append_kernel(
       if (r >= rows) break;
       const int kind = r < hq ? 0 : (r < hq + hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v
       if (kind != 2) {
+        // lane l holds the pairs l, l + 64, ...: their sums, then the butterfly over the lanes
         float ss = 0.f;
 #pragma unroll
         for (int j = 0; j < kMaxPairs; ++j)
-          if (lane + kWave * j < half) ss += x1[rr][j] * x1[rr][j] + x2[rr][j] * x2[rr][j];
+          if (lane + kWave * j < half) ss += pair_sq(x1[rr][j], x2[rr][j]);
         ss = wave_sum(ss);
-        const float rs = 1.0f / sqrtf(ss / float(D) + eps);
+        const float rs = rms_inv(ss, D, eps);
 #pragma unroll
-        for (int j = 0; j < kMaxPairs; ++j) {
-          const float a = x1[rr][j] * rs * (kind == 0 ? wq1[j] : wk1[j]);
-          const float b = x2[rr][j] * rs * (kind == 0 ? wq2[j] : wk2[j]);
-          x1[rr][j] = a * c[j] - b * sn[j];
-          x2[rr][j] = b * c[j] + a * sn[j];
-        }
+        for (int j = 0; j < kMaxPairs; ++j)
+          norm_rope_pair(x1[rr][j], x2[rr][j], rs, kind == 0 ? wq1[j] : wk1[j], kind == 0 ? wq2[j] : wk2[j], c[j],
+                         sn[j]);
       }
       f16* dst;
       if (kind == 0) {

@@ -767,12 +767,12 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
                         const uint8_t* active_mask, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                         int32_t head_dim, int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
                         size_t workspace_bytes, void* stream, const DecodeAppend& ap, bool cached = false,
-                        const void* plan = nullptr, size_t plan_bytes = 0) {
+                        const void* plan = nullptr, size_t plan_bytes = 0, const DecodePrep* prep = nullptr) {
   const bool append = ap.pool != nullptr;
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_tables == nullptr ||
       seq_lens == nullptr)
     return IFN_ERR_INVALID_ARGUMENT;
-  if (append && (ap.new_k == nullptr || ap.new_v == nullptr || ap.slots == nullptr))
+  if (append && (ap.slots == nullptr || (prep == nullptr && (ap.new_k == nullptr || ap.new_v == nullptr))))
     return IFN_ERR_INVALID_ARGUMENT;
   if (batch < 0 || num_pages < 1 || max_pages_per_seq < 1 || num_q_heads < 1 ||
       num_kv_heads < 1 || head_dim < 1 || max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
@@ -785,10 +785,12 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
                                       append ? DecodeMode::kAppend
                                              : (cached ? DecodeMode::kPlainCached : DecodeMode::kPlain));
   if (!rows && k == nullptr) return IFN_ERR_UNSUPPORTED;
+  if (prep != nullptr && (!rows || !rows_prep_supported(num_q_heads, num_kv_heads, head_dim)))
+    return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);
-  if (append) {
+  if (append && prep == nullptr) {
     IFN_CHECK_ALIGN16(ap.new_k);
     IFN_CHECK_ALIGN16(ap.new_v);
   }
@@ -811,7 +813,7 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
                               static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
                               seq_lens, active_mask, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
                               scale * kLog2e, workspace, blocks, ap, cached, static_cast<const int32_t*>(plan),
-                              reinterpret_cast<hipStream_t>(stream));
+                              reinterpret_cast<hipStream_t>(stream), prep);
   }
   DecodeWorkspace ws;
   uint8_t* wsb = static_cast<uint8_t*>(workspace);
@@ -915,6 +917,35 @@ extern "C" int ifn_paged_decode_append_planned(void* out, const void* query, voi
                            ifn::DecodeAppend{static_cast<const ifn::f16*>(new_k), static_cast<const ifn::f16*>(new_v),
                                              slot_mapping, static_cast<ifn::f16*>(kv_pool_layer)},
                            false, plan, plan_bytes);
+}
+
+extern "C" int ifn_paged_decode_prep_append(void* out, const float* q, const float* k, const float* v,
+                                            const float* q_norm_weight, const float* k_norm_weight,
+                                            const float* rope_table, int32_t max_positions,
+                                            const int32_t* positions, const int32_t* slot_mapping,
+                                            void* kv_pool_layer, int64_t num_pages, const int32_t* block_tables,
+                                            int32_t max_pages_per_seq, const int32_t* seq_lens,
+                                            const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
+                                            int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                            int32_t max_seq_len, float scale, float eps, const void* plan,
+                                            size_t plan_bytes, void* workspace, size_t workspace_bytes,
+                                            void* stream) {
+  using namespace ifn;
+  if (q == nullptr || k == nullptr || v == nullptr || q_norm_weight == nullptr || k_norm_weight == nullptr ||
+      rope_table == nullptr || positions == nullptr || slot_mapping == nullptr || kv_pool_layer == nullptr)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (max_positions < 1 || !(eps >= 0.f) || head_dim % 8 != 0) return IFN_ERR_INVALID_ARGUMENT;
+  IFN_CHECK_ALIGN16(k);
+  IFN_CHECK_ALIGN16(v);
+  IFN_CHECK_ALIGN16(q_norm_weight);
+  IFN_CHECK_ALIGN16(k_norm_weight);
+  IFN_CHECK_ALIGN16(rope_table);
+  const DecodePrep pp{q, k, v, q_norm_weight, k_norm_weight, rope_table, positions, max_positions, eps};
+  // the fp32 query stands in for the fp16 one, which this variant does not read
+  return decode_entry(out, q, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens, active_mask,
+                      batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale, workspace,
+                      workspace_bytes, stream, DecodeAppend{nullptr, nullptr, slot_mapping, static_cast<f16*>(kv_pool_layer)},
+                      false, plan, plan_bytes, &pp);
 }
 
 namespace ifn {

@@ -258,28 +258,81 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   }
 }
 
+// A wave's two 8-dim halves of a token row's head: lane (hd, col) holds dims 8 col .. 8 col + 7 and
+// D/2 + 8 col .. D/2 + 8 col + 7 of head hd -- exactly the rotary pairs (i, i + D/2) of its 8 dims,
+// since 8 x (lanes per head) = D/2 for a 2 KiB row.  Loads the fp32 values of one head row.
+template <int D>
+__device__ __forceinline__ void load_pairs(const float* row, int col, float (&x1)[8], float (&x2)[8]) {
+  const f32x4 a0 = *reinterpret_cast<const f32x4*>(row + 8 * col);
+  const f32x4 a1 = *reinterpret_cast<const f32x4*>(row + 8 * col + 4);
+  const f32x4 b0 = *reinterpret_cast<const f32x4*>(row + D / 2 + 8 * col);
+  const f32x4 b1 = *reinterpret_cast<const f32x4*>(row + D / 2 + 8 * col + 4);
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x1[j] = a0[j];
+    x1[4 + j] = a1[j];
+    x2[j] = b0[j];
+    x2[4 + j] = b1[j];
+  }
+}
+
+// RMSNorm + rotary of one head held as load_pairs leaves it (LPH lanes per head), in the rounding
+// and summation order of the pre-append kernel: pair i = 8 col + j of the head sits in register j
+// of lane col, so the butterfly over pairs (i ^ 1, i ^ 2, i ^ 4, then i ^ 8, ...) is a tree over
+// the registers followed by the DPP sum over the head's lanes.  Pairs i >= D/2 of a 64-lane
+// butterfly would add zeros, which leave the sum unchanged.
+template <int D, int LPH>
+__device__ __forceinline__ void norm_rope_head(float (&x1)[8], float (&x2)[8], const float (&w1)[8],
+                                               const float (&w2)[8], const float (&c)[8], const float (&s)[8],
+                                               float eps) {
+  float p[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) p[j] = pair_sq(x1[j], x2[j]);
+  const float s01 = p[0] + p[1], s23 = p[2] + p[3], s45 = p[4] + p[5], s67 = p[6] + p[7];
+  float ss = (s01 + s23) + (s45 + s67);
+  ss = sum_lanes<LPH>(ss);
+  const float rs = rms_inv(ss, D, eps);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) norm_rope_pair(x1[j], x2[j], rs, w1[j], w2[j], c[j], s[j]);
+}
+
+__device__ __forceinline__ u32x4 pack_h8(const float (&x)[8]) {
+  return __builtin_bit_cast(u32x4, f16x8{f16(x[0]), f16(x[1]), f16(x[2]), f16(x[3]), f16(x[4]), f16(x[5]),
+                                         f16(x[6]), f16(x[7])});
+}
+
 // kAppend: the step's store_kv is fused in (ap); kStream: K/V row loads carry the non-temporal
 // hint (each row read once per launch; wrong when rows of the batch share pages).  S: tokens in
 // flight per wave.  plan: a step plan for exactly these lengths, tables and slots, or null.
-template <int D, int G, int HKV, int S, bool kAppend, bool kStream>
+// kPrep: the pre-append is fused in as well (pp): the query rows and the appended K/V rows come
+// from fp32 projections, normalised, rotated and cast here (q is unused; ap.slots / ap.pool
+// give the store's slots and pool, ap.new_k / ap.new_v are unused).
+template <int D, int G, int HKV, int S, bool kAppend, bool kStream, bool kPrep = false>
 __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
     const int32_t* __restrict__ block_tables, int32_t max_pages, const int32_t* __restrict__ seq_lens,
     const uint8_t* __restrict__ active, int32_t batch, int32_t max_len, float scale_log2, DecodeWorkspace ws,
-    DecodeAppend ap, const int32_t* __restrict__ plan) {
+    DecodeAppend ap, const int32_t* __restrict__ plan, DecodePrep pp) {
   constexpr int LPH = kWave / HKV;  // lanes per kv head
   constexpr int ROW = HKV * D;      // fp16 elements per token row
   constexpr int HQ = HKV * G;
   constexpr int GR = G < 2 ? G : 2;  // query heads per kv head merged per LDS round
   constexpr int D4 = D / 4;
+  constexpr bool kApp = kAppend || kPrep;  // the step's appended rows are stored by this launch
   static_assert(ROW == 2 * kWave * 8, "a token row is two 16-byte chunks per lane");
   static_assert(G % GR == 0, "merge rounds cover the group");
+  static_assert(!(kAppend && kPrep), "one append mode");
+  static_assert(!kPrep || (8 * LPH == D / 2), "a lane's two chunks are rotary partners");
   __shared__ int s_cum[kRowsMaxBatch + 1];  // rows' offsets in the virtual token list
   __shared__ int s_wsum[kRowsWaves];
   __shared__ float s_m[kRowsWaves][HQ];
   __shared__ float s_l[kRowsWaves][HQ];
   __shared__ f32x4 s_acc[kRowsWaves][HKV * GR][D4];
   __shared__ uint32_t s_ticket[2];
+  // kPrep: the appended token's fp16 K and V rows, prepared at the start of its piece
+  __shared__ __attribute__((aligned(16))) f16 s_app[kPrep ? 2 : 1][kPrep ? ROW : 8];
+  // kPrep: the piece's fp16 query, head g of every kv head in the layout of a token row
+  __shared__ __attribute__((aligned(16))) f16 s_q[kPrep ? G : 1][kPrep ? ROW : 8];
 
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
@@ -301,7 +354,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   if (plan != nullptr) {
     rec = plan + plan_rec0(batch) + blk * kPlanRec;
     planned = plan[0] == kPlanMagic && plan[1] == batch && plan[4] == int(nb) && plan[6] == cap &&
-              (!kAppend || plan[5] != 0);
+              (!kApp || plan[5] != 0);
     T = plan[3];
     rec_n = rec[0];
     ids_pl = rec[64 + lane];
@@ -337,7 +390,48 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     zero_len = row_keys(seq_lens, active, tid, cap);
     zero_live = active == nullptr || active[tid] != 0;
   }
+  // kPrep: this wave's first item of the fallback store below, looked up at launch so that the end
+  // of the kernel does not wait on it.
+  const int64_t fb_first = int64_t(blockIdx.x) + int64_t(gridDim.x) * (kRowsWaves - 1 - wave);
+  const int64_t fb_step = int64_t(gridDim.x) * kRowsWaves;
+  auto fb_item = [&](int64_t it, int& pos, int& slot) __attribute__((always_inline)) -> bool {
+    const int b = int(it >> 1);
+    pos = pp.positions[b];
+    slot = row_slot(ap.slots, active, b, num_slots);
+    return slot >= 0 && pos >= 0 && pos < pp.max_pos && pos >= row_keys(seq_lens, active, b, cap);
+  };
+  int fb_pos0 = 0, fb_slot0 = -1;
+  bool fb_need0 = false;
+  if constexpr (kPrep) {
+    if (fb_first < 2 * int64_t(batch)) fb_need0 = fb_item(fb_first, fb_pos0, fb_slot0);
+  }
   auto finish = [&]() __attribute__((always_inline)) {
+    if constexpr (kPrep) {
+      // The appended rows the attention did not take (their position is not among the row's keys:
+      // rows without keys, or a position past them), normalised and rotated (K) or cast (V) and
+      // stored as the pre-append kernel stores them; the others were stored by the wave that
+      // prepared them for the attention.  A position outside the table, an inactive row or a slot
+      // outside the pool stores nothing.  Item i = (row i / 2, K or V) goes to workgroup i % grid,
+      // wave 7 - (i / grid) % 8, once the workgroup's attention work is done.
+      const int hd = lane / LPH, col = lane % LPH;
+      for (int64_t it = fb_first; it < 2 * int64_t(batch); it += fb_step) {
+        const int b = int(it >> 1), kind = int(it & 1);
+        int pos = fb_pos0, slot = fb_slot0;
+        const bool need = it == fb_first ? fb_need0 : fb_item(it, pos, slot);
+        if (!need) continue;
+        float x1[8], x2[8];
+        load_pairs<D>((kind == 0 ? pp.k : pp.v) + int64_t(b) * ROW + hd * D, col, x1, x2);
+        if (kind == 0) {
+          float w1[8], w2[8], c[8], sn[8];
+          load_pairs<D>(pp.k_norm_w, col, w1, w2);
+          load_pairs<D>(pp.rope + int64_t(pos) * D, col, c, sn);
+          norm_rope_head<D, LPH>(x1, x2, w1, w2, c, sn, pp.eps);
+        }
+        f16* dst = ap.pool + (int64_t(kind) * num_slots + slot) * ROW + hd * D + 8 * col;
+        st16(dst, pack_h8(x1));
+        st16(dst + D / 2, pack_h8(x2));
+      }
+    }
     if constexpr (kAppend) {
       if (app_first < app_items) {
         f16* d0 = app_dst(app_first, app_slot);
@@ -405,7 +499,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       P.b = b;
       P.first = int(range_of(cb));
       P.nranges = int(range_of(int64_t(cb) + len - 1)) - P.first + 1;
-      P.slot = kAppend ? row_slot(ap.slots, active, b, num_slots) : -1;
+      P.slot = kApp ? row_slot(ap.slots, active, b, num_slots) : -1;
       break;
     }
     P.b = __builtin_amdgcn_readfirstlane(P.b);
@@ -445,12 +539,68 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
 
     // Query rows (b, hd * G + g), chunks col and col + LPH; the piece's page ids, one per lane.
     f16x8 qv[G][2];
-    const f16* qrow = q + (int64_t(b) * HQ + hd * G) * D;
+    // kPrep: the query comes from the fp32 projection (RMSNorm, rotary at the row's position, fp16;
+    // zero when the position is outside the table), as the pre-append kernel writes it: wave g < G
+    // prepares query head g of every kv head.  When the row's appended token (at its position) is
+    // in this piece, wave G prepares its fp16 K row (normalised, rotated) and wave G + 1 its V row
+    // (cast), to LDS -- where the wave that consumes the token reads them in place of the pool row --
+    // and to the pool at the row's slot (the step's store of that row).  Each wave holds at most one
+    // fp32 row, its weights and the rotary row.  The fp32 loads are issued here and the arithmetic
+    // runs once the ring's first request is out, so the two round trips overlap; the workgroup then
+    // exchanges the results through LDS at one barrier.
+    int app_pos = -1;  // position of the row's appended token when it is in this piece (uniform)
+    int app_page = -1;  // page id of the appended token's position
+    bool pos_ok = false, k_maker = false, v_maker = false;
+    const bool q_maker = kPrep && wave < G;
+    float pc[8], psn[8], pw1[8], pw2[8], px1[8], px2[8];
+    if constexpr (kPrep) {
+      const int pos = pp.positions[b];
+      pos_ok = pos >= 0 && pos < pp.max_pos;
+      if (pos_ok && slot_b >= 0 && pos >= a && pos < e) {
+        app_pos = pos;
+        k_maker = wave == G;
+        v_maker = wave == G + 1;
+        app_page = block_tables[int64_t(b) * max_pages + pos / kRowsBlock];  // read when the token comes up
+      }
+      if (q_maker || k_maker) {
+        load_pairs<D>(pp.rope + int64_t(pos_ok ? pos : 0) * D, col, pc, psn);
+        load_pairs<D>(q_maker ? pp.q_norm_w : pp.k_norm_w, col, pw1, pw2);
+      }
+      if (q_maker || k_maker || v_maker)
+        load_pairs<D>(q_maker ? pp.q + (int64_t(b) * HQ + hd * G + wave) * D
+                              : (k_maker ? pp.k : pp.v) + int64_t(b) * ROW + hd * D,
+                      col, px1, px2);
+    } else {
+      const f16* qrow = q + (int64_t(b) * HQ + hd * G) * D;
 #pragma unroll
-    for (int g = 0; g < G; ++g) {
-      qv[g][0] = as_h8(ld16(qrow + g * D + 8 * col));
-      qv[g][1] = as_h8(ld16(qrow + g * D + 8 * (col + LPH)));
+      for (int g = 0; g < G; ++g) {
+        qv[g][0] = as_h8(ld16(qrow + g * D + 8 * col));
+        qv[g][1] = as_h8(ld16(qrow + g * D + 8 * (col + LPH)));
+      }
     }
+    // kPrep, after the ring's first request (every wave of the workgroup calls it)
+    auto prep_compute = [&]() __attribute__((always_inline)) {
+      if (q_maker || k_maker) norm_rope_head<D, LPH>(px1, px2, pw1, pw2, pc, psn, pp.eps);
+      const u32x4 h0 = pack_h8(px1), h1 = pack_h8(px2);
+      if (q_maker) {
+        *reinterpret_cast<u32x4*>(&s_q[wave][off0]) = pos_ok ? h0 : u32x4{0u, 0u, 0u, 0u};
+        *reinterpret_cast<u32x4*>(&s_q[wave][off1]) = pos_ok ? h1 : u32x4{0u, 0u, 0u, 0u};
+      }
+      if (k_maker || v_maker) {
+        const int kv = v_maker ? 1 : 0;
+        *reinterpret_cast<u32x4*>(&s_app[kv][off0]) = h0;
+        *reinterpret_cast<u32x4*>(&s_app[kv][off1]) = h1;
+        f16* dst = ap.pool + (int64_t(kv) * num_slots + slot_b) * ROW;
+        st16(dst + off0, h0);
+        st16(dst + off1, h1);
+      }
+      __syncthreads();
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        qv[g][0] = *reinterpret_cast<const f16x8*>(&s_q[g][off0]);
+        qv[g][1] = *reinterpret_cast<const f16x8*>(&s_q[g][off1]);
+      }
+    };
     const int pg0 = a / kRowsBlock;
     const int npg = (e - 1) / kRowsBlock - pg0 + 1;
     const int32_t* bt = block_tables + int64_t(b) * max_pages + pg0;
@@ -535,26 +685,61 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     // The scheduling barriers keep the loads ahead of the arithmetic.
     u32x4 kb_[S][2], vb_[S][2];
     bool okb[S];
-    if (nw > 0) {
+    // This wave's tokens i0 .. i1 - 1 through the ring; with_prep: the piece's preparation (kPrep)
+    // runs on every wave between the first requests and the first token.
+    auto ring = [&](int i0, int i1, bool with_prep) __attribute__((always_inline)) {
+      if (i1 > i0) {
 #pragma unroll
-      for (int s = 0; s < S - 1; ++s) issue(min(s, nw - 1), kb_[s], vb_[s], okb[s]);
-      int i = 0;
-      for (; i + S <= nw; i += S) {
-#pragma unroll
-        for (int s = 0; s < S; ++s) {
-          shift(i + s);
-          const int sn = (s + S - 1) % S;
-          issue(min(i + s + S - 1, nw - 1), kb_[sn], vb_[sn], okb[sn]);
+        for (int s = 0; s < S - 1; ++s) issue(min(i0 + s, i1 - 1), kb_[s], vb_[s], okb[s]);
+      }
+      if constexpr (kPrep) {
+        if (with_prep) {
           __builtin_amdgcn_sched_barrier(0);
-          consume(kb_[s], vb_[s], okb[s]);
+          prep_compute();
         }
       }
+      if (i1 > i0) {
+        int i = i0;
+        for (; i + S <= i1; i += S) {
 #pragma unroll
-      for (int s = 0; s < S - 1; ++s)
-        if (i + s < nw) {
-          shift(i + s);
-          consume(kb_[s], vb_[s], okb[s]);
+          for (int s = 0; s < S; ++s) {
+            shift(i + s);
+            const int sn = (s + S - 1) % S;
+            issue(min(i + s + S - 1, i1 - 1), kb_[sn], vb_[sn], okb[sn]);
+            __builtin_amdgcn_sched_barrier(0);
+            consume(kb_[s], vb_[s], okb[s]);
+          }
         }
+#pragma unroll
+        for (int s = 0; s < S - 1; ++s)
+          if (i + s < i1) {
+            shift(i + s);
+            consume(kb_[s], vb_[s], okb[s]);
+          }
+      }
+    };
+    // kPrep: the wave that holds the row's appended token takes the ring up to it, the token itself
+    // (from LDS when its slot is that position's slot in the table, as the step writes it; else the
+    // pool row, as the two-launch step would read it), then the rest of its tokens.
+    const int i_app = kPrep && app_pos >= 0 && (app_pos - a) % kRowsWaves == wave ? (app_pos - a) / kRowsWaves : nw;
+    ring(0, i_app, true);
+    if constexpr (kPrep) {
+      if (i_app < nw) {
+        shift(i_app);
+        const int phys = app_page;
+        bool ok = phys >= 0 && int64_t(phys) < num_pages;
+        u32x4 kr[2], vr[2];
+        if (ok && int64_t(phys) * kRowsBlock + app_pos % kRowsBlock == slot_b) {
+          kr[0] = *reinterpret_cast<const u32x4*>(&s_app[0][off0]);
+          kr[1] = *reinterpret_cast<const u32x4*>(&s_app[0][off1]);
+          vr[0] = *reinterpret_cast<const u32x4*>(&s_app[1][off0]);
+          vr[1] = *reinterpret_cast<const u32x4*>(&s_app[1][off1]);
+        } else {
+          issue(i_app, kr, vr, ok);
+        }
+        consume(kr, vr, ok);
+        ring(i_app + 1, nw, false);
+      }
     }
 
     // Merge the 8 waves through LDS: (m, l) of every query head, then the accumulators in rounds of
@@ -699,13 +884,23 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
 }
 
 typedef void (*RowsKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, const int32_t*,
-                           const uint8_t*, int32_t, int32_t, float, DecodeWorkspace, DecodeAppend, const int32_t*);
+                           const uint8_t*, int32_t, int32_t, float, DecodeWorkspace, DecodeAppend, const int32_t*,
+                           DecodePrep);
 
 constexpr int kRowsStages = 2;
 
-static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream) {
+// The fused pre-append variant, compiled where head_dim <= 128: there the pre-append kernel holds
+// one rotary pair per lane, and the variant follows that summation order.
+template <int D, int G, int HKV>
+static RowsKernel prep_rows() {
+  if constexpr (D <= 128) return decode_rows_kernel<D, G, HKV, kRowsStages, false, true, true>;
+  else return nullptr;
+}
+
+static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream, bool prep = false) {
 #define IFN_ROWS_CASE(DD, GG, HH)                                                                  \
   if (d == DD && g == GG && hkv == HH) {                                                           \
+    if (prep) return prep_rows<DD, GG, HH>();                                                      \
     if (append) return decode_rows_kernel<DD, GG, HH, kRowsStages, true, true>;                    \
     return stream ? decode_rows_kernel<DD, GG, HH, kRowsStages, false, true>                       \
                   : decode_rows_kernel<DD, GG, HH, kRowsStages, false, false>;                     \
@@ -715,6 +910,10 @@ static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream) {
   IFN_ROWS_CASE(256, 1, 4) IFN_ROWS_CASE(256, 2, 4)
 #undef IFN_ROWS_CASE
   return nullptr;
+}
+
+bool rows_prep_supported(int32_t hq, int32_t hkv, int32_t d) {
+  return hkv >= 1 && hq % hkv == 0 && pick_rows(d, hq / hkv, hkv, false, true, true) != nullptr;
 }
 
 bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t max_pages, int32_t max_len) {
@@ -743,8 +942,9 @@ int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pag
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
-                       const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream) {
-  RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached);
+                       const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
+                       const DecodePrep* prep) {
+  RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached, prep != nullptr);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   size_t off_ml, off_o;
   rows_ws_layout(batch, hq, d, blocks, &off_ml, &off_o);
@@ -753,9 +953,10 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
   ws.count = reinterpret_cast<uint32_t*>(wsb);
   ws.ml = reinterpret_cast<float*>(wsb + off_ml);
   ws.o = reinterpret_cast<float*>(wsb + off_o);
+  const DecodePrep pp = prep != nullptr ? *prep : DecodePrep{};
   k<<<dim3(unsigned(blocks)), dim3(kRowsThreads), 0, stream>>>(out, q, pool, num_pages, block_tables, max_pages,
                                                                 seq_lens, active, batch, max_len, scale_log2, ws, ap,
-                                                                plan);
+                                                                plan, pp);
   return ifn_launch_status();
 }
 

@@ -22,10 +22,10 @@ import numpy as np
 import torch
 
 from .. import _capi
-from ._common import KVStoreError, check_pool, current_stream, ptr
+from ._common import KVStoreError, PagedAttentionError, check_pool, current_stream, ptr
 from ._carrier import accepts_carriers
 
-__all__ = ["qk_norm_rope_append", "rope_table", "zero_pages", "copy_pages"]
+__all__ = ["qk_norm_rope_append", "qk_norm_rope_store_and_decode", "rope_table", "zero_pages", "copy_pages"]
 
 
 def rope_table(max_positions: int, head_dim: int, base: float, device=None) -> torch.Tensor:
@@ -143,3 +143,93 @@ def copy_pages(kv_pool: torch.Tensor, src_ids: torch.Tensor, dst_ids: torch.Tens
         raise KVStoreError("copy_pages destinations must be distinct and not among the sources")
     _capi.call("ifn_copy_pages", ptr(kv_pool), L, P, ptr(src), ptr(dst), n, hkv, d, bs,
                current_stream(kv_pool.device))
+
+
+@accepts_carriers
+def qk_norm_rope_store_and_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_weight: torch.Tensor,
+                                  k_norm_weight: torch.Tensor, rope: torch.Tensor, positions: torch.Tensor,
+                                  slot_mapping: torch.Tensor, active_mask: torch.Tensor | None,
+                                  kv_pool: torch.Tensor, block_tables: torch.Tensor,
+                                  sequence_lengths: torch.Tensor, *, layer: int = 0, eps: float = 1e-6,
+                                  scale: float | None = None, out: torch.Tensor | None = None,
+                                  block_size: int = 16, max_seq_len: int | None = None, plan=None) -> torch.Tensor:
+    """A decode step of one layer from fp32 projections: pre-append and attention in one launch.
+
+    ``ifn_paged_decode_prep_append``: the same ``out`` and pool as ``qk_norm_rope_append(q, k, v,
+    ..., positions, slot_mapping, active_mask, kv_pool, layer=layer, eps=eps)`` followed by
+    ``paged_attention(q16, kv_pool, block_tables, sequence_lengths, active_mask, ...)`` -- the
+    norm / rope / cast / store of model.py:183-196 and the attention of :196-200.  q fp32
+    [B, Hq, D], k / v fp32 [B, Hkv, D]; ``plan`` a ``decode_plan`` built with ``slot_mapping``.
+    Row b's appended token is at ``positions[b]`` and ``slot_mapping[b]`` is that position's slot
+    in the row's table (the decode step's invariant).  Shapes the fused kernel does not cover
+    (token row other than 2 KiB, head_dim > 128) run the two launches instead.
+    """
+    from .paged_attention import _check, _plan_key, paged_attention, workspace_for
+    from .kv_store import _check_index
+    pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
+    dev = pool_layer.device
+    if bs != block_size:
+        raise PagedAttentionError(f"kv_pool block_size {bs} != block_size argument {block_size}")
+    if not isinstance(q, torch.Tensor) or q.ndim != 3:
+        raise PagedAttentionError("q must be a rank-3 [B, Hq, D] tensor")
+    n, hq = q.shape[0], q.shape[1]
+    if hq % hkv:
+        raise PagedAttentionError(f"num_q_heads {hq} is not a multiple of num_kv_heads {hkv}")
+    _f32("q", q, (n, hq, d), dev)
+    _f32("k", k, (n, hkv, d), dev)
+    _f32("v", v, (n, hkv, d), dev)
+    _f32("q_norm_weight", q_norm_weight, (d,), dev)
+    _f32("k_norm_weight", k_norm_weight, (d,), dev)
+    if not isinstance(rope, torch.Tensor) or rope.ndim != 2:
+        raise KVStoreError("rope must be the rank-2 table of rope_table()")
+    _f32("rope", rope, (rope.shape[0], d), dev)
+    _i32("positions", positions, n, dev)
+    sm = _check_index("slot_mapping", slot_mapping, n, dev, (torch.int32,))
+    if sm is None:
+        raise PagedAttentionError("qk_norm_rope_store_and_decode needs a slot_mapping")
+    if active_mask is not None:
+        _i32("active_mask", active_mask, n, dev, (torch.bool, torch.uint8))
+    if not isinstance(block_tables, torch.Tensor) or block_tables.ndim != 2:
+        raise PagedAttentionError("block_tables must be a rank-2 [B, max_pages] int32 tensor")
+    max_pages = block_tables.shape[1]
+    _check("block_tables", block_tables, (n, max_pages), (torch.int32,), dev)
+    _check("sequence_lengths", sequence_lengths, (n,), (torch.int32,), dev)
+    if max_pages < 1:
+        raise PagedAttentionError("block_tables must have at least one column")
+    if not (eps >= 0 and math.isfinite(eps)):
+        raise KVStoreError("eps must be a finite non-negative number")
+    if out is None:
+        out = torch.zeros((n, hq, d), dtype=torch.float16, device=dev) if active_mask is not None else \
+            torch.empty((n, hq, d), dtype=torch.float16, device=dev)
+    else:
+        _check("out", out, (n, hq, d), (torch.float16,), dev)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if not scale > 0:
+        raise PagedAttentionError(f"scale must be positive, got {scale}")
+    cap = max_pages * bs
+    msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
+    if msl < 0:
+        raise PagedAttentionError("max_seq_len must be non-negative")
+    if n == 0:
+        return out
+    stream = current_stream(dev)
+    lib = _capi.lib()
+    nbytes = lib.ifn_paged_decode_workspace_bytes(n, hq, hkv, d, bs, msl)
+    ws = workspace_for(dev, stream, nbytes)
+    pp, pbytes = None, 0
+    if plan is not None:
+        key = _plan_key((n, hq, d), sm, pool_layer, block_tables, sequence_lengths, active_mask, msl)
+        pp = plan.ptr_for(key, True)
+        pbytes = plan.nbytes if pp else 0
+    status = lib.ifn_paged_decode_prep_append(
+        ptr(out), ptr(q), ptr(k), ptr(v), ptr(q_norm_weight), ptr(k_norm_weight), ptr(rope), rope.shape[0],
+        ptr(positions), ptr(sm), ptr(pool_layer), P, ptr(block_tables), max_pages, ptr(sequence_lengths),
+        ptr(active_mask), n, hq, hkv, d, bs, msl, float(scale), float(eps), pp, pbytes, ptr(ws), ws.numel(), stream)
+    if status == _capi.IFN_ERR_UNSUPPORTED:
+        q16 = qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope, positions, sm, active_mask, kv_pool,
+                                  layer=layer, eps=eps)
+        return paged_attention(q16, kv_pool, block_tables, sequence_lengths, active_mask, layer=layer, scale=scale,
+                               out=out, block_size=block_size, max_seq_len=max_seq_len, plan=plan)
+    _capi.check("ifn_paged_decode_prep_append", status)
+    return out

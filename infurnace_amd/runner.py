@@ -50,8 +50,8 @@ import numpy as np
 import torch
 
 from .cache import BlockPool, KVCacheError, KVManager, PagedKVCache, PoolExhausted, PrefixCache
-from .kernels import (decode_plan, paged_attention, qk_norm_rope_append, store_kv, store_kv_and_decode,
-                      store_kv_and_prefill)
+from .kernels import (decode_plan, paged_attention, qk_norm_rope_append, qk_norm_rope_store_and_decode, store_kv,
+                      store_kv_and_decode, store_kv_and_prefill)
 
 __all__ = ["PagedKVRunner", "RunnerError"]
 
@@ -116,10 +116,21 @@ class _Step:
     def prep_store_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
                           q_norm_weight: torch.Tensor, k_norm_weight: torch.Tensor, rope: torch.Tensor,
                           eps: float = 1e-6, out: torch.Tensor | None = None) -> torch.Tensor:
-        """The same from fp32 projections: q/k RMSNorm + rotary, fp16 cast and append in one launch."""
+        """The same from fp32 projections: q/k RMSNorm + rotary, fp16 cast and append.
+
+        A decode step without a shared prefix does all of it and the attention in one launch
+        (``qk_norm_rope_store_and_decode``); otherwise the pre-append is its own launch.
+        """
         if self.closed:
             raise RunnerError("this step is closed: a later step has begun")
         kv = self.runner.cache.kv
+        if self.query_start is None and self.shared_prefix is None:
+            o = qk_norm_rope_store_and_decode(q, k, v, q_norm_weight, k_norm_weight, rope, self.positions,
+                                              self.slot_mapping, self.active, kv, self.block_tables, self.seq_lens,
+                                              layer=layer, eps=eps, max_seq_len=self.max_len, out=out,
+                                              plan=self._decode_plan(q))
+            self._launched()
+            return o
         q16 = qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope, self.positions, self.slot_mapping,
                                   self.active, kv, layer=layer, eps=eps)
         if self.query_start is not None:
