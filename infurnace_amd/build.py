@@ -35,9 +35,18 @@ DEVICE_FLAGS = [
 ]
 
 
+# Per-source extras. The prefill kernel rescales its fp32 accumulators with VALU work inside the
+# key loop; with the accumulators in AGPRs the compiler copies all of them to VGPRs and back every
+# iteration, so its MFMAs are selected in the VGPR form (it fits 256 VGPRs without spilling).
+FILE_FLAGS = {
+    "paged_prefill_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form"],
+}
+
+
 def _compile(src: str) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    cmd = [HIPCC, *DEVICE_FLAGS, "-c", src, "-o", obj]
+    extra = FILE_FLAGS.get(os.path.basename(src), [])
+    cmd = [HIPCC, *DEVICE_FLAGS, *extra, "-c", src, "-o", obj]
     r = subprocess.run(cmd, capture_output=True, text=True)
     # the only accepted diagnostic noise is the host pass not knowing the gfx feature
     noise = "'-packed-fp32-ops' is not a recognized feature for this target (ignoring feature)"
@@ -62,6 +71,13 @@ def build(jobs: int = 8) -> str:
     tmp = LIB_PATH + ".tmp"
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp, *objs]
     subprocess.run(cmd, check=True)
+    # A kernel whose host-side launch stub was not emitted links as an undefined symbol and only fails
+    # when the library is loaded; refuse such a library here.
+    nm = subprocess.run(["nm", "-u", tmp], capture_output=True, text=True)
+    missing = [ln.split()[-1] for ln in nm.stdout.splitlines() if "_ZN3ifn" in ln]
+    if missing:
+        os.remove(tmp)
+        raise RuntimeError(f"{len(missing)} undefined library symbols, e.g. {missing[0]}")
     os.replace(tmp, LIB_PATH)
     return LIB_PATH
 

@@ -236,6 +236,25 @@ struct DecodePrep {
   float eps;
 };
 
+// Key-split workspace of the prefill kernels: tickets (zero between calls), then the splits'
+// partial states (m in log2 units, l) and unnormalised outputs.
+struct PrefillWorkspace {
+  uint32_t* count;  // one ticket per (query block, kv head[, head]); every call returns them to zero
+  float* ml;
+  float* o;
+};
+
+// Fused prefill append: the chunk's new_k / new_v [T][Hkv][D] are stored into the pool at the
+// table's slots for positions query_start .. query_start + T - 1, and the attention takes the
+// chunk's keys and values from new_k / new_v, so the stores need no ordering against the reads.
+// Requires query_start % 32 == 0 (a key tile is then wholly before the chunk or wholly in it)
+// and T * Hkv * D * 2 < 2^31 bytes (one buffer resource).
+struct PrefillAppend {
+  const f16* new_k;
+  const f16* new_v;
+  f16* pool;  // the layer's pool (the memory the kernel reads)
+};
+
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Number of CUs of the current device (queried once per device; 0 when there is none).
@@ -262,6 +281,15 @@ int prefix_pass_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_
 int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
                 int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
                 int32_t stride, int cus, hipStream_t stream);
+
+// Chunked prefill with 64 query rows per wavefront (paged_prefill_wide.hip): the entry points'
+// kernel for the (head_dim, group) it compiles; the key-split workspace it needs.
+bool wide_prefill_supported(int32_t hq, int32_t hkv, int32_t d);
+size_t wide_prefill_ws_bytes(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus);
+int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* table,
+                        int32_t query_start, int32_t T, int32_t hq, int32_t hkv, int32_t d, float scale_log2,
+                        void* workspace, size_t workspace_bytes, const PrefillAppend& ap, int cus,
+                        hipStream_t stream);
 
 // Whole-row decode (paged_decode_rows.hip), used by the decode entry points when the token row
 // (num_kv_heads x head_dim fp16) is 2 KiB and its (head_dim, group) is compiled; and its step plan.

@@ -49,11 +49,6 @@ namespace ifn {
 constexpr int kPBlock = 16;  // tokens per page compiled in
 constexpr int kMaxSplit = 16;  // workgroups per (query block, kv head) at most
 
-struct PrefillWorkspace {
-  uint32_t* count;  // [query block][kv head][G] tickets, zero between calls
-  float* ml;        // [pair][split][64 lanes][2]   (m in log2 units, l)
-  float* o;         // [pair][split][D/32][16][64 lanes] unnormalised outputs
-};
 
 // Shared-prefix mode: every query row sees keys [0, key_len) (no causal mask) and each key split
 // writes its result unnormalised, as the state (m, l, O), for a later merge:
@@ -67,16 +62,6 @@ struct PrefixOut {
   int32_t stride;
 };
 
-// Fused append (kAppend variant): the chunk's new_k / new_v [T][Hkv][D] are stored into the pool at
-// the table's slots for positions query_start .. query_start + T - 1, and the attention takes the
-// chunk's keys and values from new_k / new_v, so the stores need no ordering against the reads.
-// Requires query_start % 32 == 0 (a key tile is then wholly before the chunk or wholly in it)
-// and T * Hkv * D * 2 < 2^31 bytes (one buffer resource).
-struct PrefillAppend {
-  const f16* new_k;
-  const f16* new_v;
-  f16* pool;  // the layer's pool (the memory the kernel reads)
-};
 
 // The chunk's K and V rows -> the pool at table[pos / 16] * 16 + pos % 16, pos = query_start + t:
 // 16-byte chunks, item it of `items` per thread in a grid-stride loop.  Rows whose page id is
@@ -677,6 +662,8 @@ extern "C" size_t ifn_paged_prefill_workspace_bytes(int32_t num_q_tokens, int32_
     return 0;
   int cus = ifn::device_cu_count();
   if (cus < 1) cus = 256;
+  if (ifn::wide_prefill_supported(num_q_heads, num_kv_heads, head_dim))
+    return ifn::wide_prefill_ws_bytes(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim, cus);
   return ifn::plan_prefill(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim, cus).bytes;
 }
 
@@ -722,6 +709,12 @@ static int prefill_entry(void* out, const void* query, const void* kv_pool_layer
     ap = PrefillAppend{nullptr, nullptr, nullptr};
     k = pick_prefill(head_dim, num_q_heads / num_kv_heads, &threads, false);
   }
+  if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
+  if (wide_prefill_supported(num_q_heads, num_kv_heads, head_dim))
+    return wide_prefill_launch(static_cast<f16*>(out), static_cast<const f16*>(query),
+                               static_cast<const f16*>(kv_pool_layer), num_pages, block_table, query_start,
+                               num_q_tokens, num_q_heads, num_kv_heads, head_dim, scale * kLog2e, workspace,
+                               workspace_bytes, ap, cus, reinterpret_cast<hipStream_t>(stream));
   const PrefillPlan p = plan_prefill(num_q_tokens, query_start, num_q_heads, num_kv_heads, head_dim, cus);
   if (p.n_qb * num_kv_heads * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
   PrefillWorkspace ws{nullptr, nullptr, nullptr};
@@ -736,7 +729,6 @@ static int prefill_entry(void* out, const void* query, const void* kv_pool_layer
     IFN_CHECK_ALIGN16(workspace);
     ws.count = static_cast<uint32_t*>(workspace);  // no split: only the error flag is used
   }
-  if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
   k<<<dim3(unsigned(p.n_qb * num_kv_heads * p.nsplit)), unsigned(threads), 0,
       reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),

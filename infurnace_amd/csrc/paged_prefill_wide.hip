@@ -1,0 +1,641 @@
+// Causal chunked-prefill paged attention with 64 query rows per wavefront (gfx950 MFMA fp16).
+//
+// Same operation and entry points as paged_prefill.hip (docs/architecture.md:246; contiguous
+// semantics src/infurnace/executor/tinygrad/model.py:116-132: query row i sits at
+// start_position + i and sees keys with key_pos <= query_pos), organised so that every K and V
+// fragment feeds two MFMA chains and K never passes through LDS:
+//
+//  * Rows.  A workgroup serves one (query block, kv head): 64 rows = 64 / G queries x the G query
+//    heads of the kv head.  Its 4 waves (one per SIMD, up to 512 registers each) are 4 key groups:
+//    wave k takes the 32-key tiles t = k, k + 4, ... (interleaved, so the causal diagonal costs
+//    every group the same) and keeps all 64 rows in registers as two 32-row MFMA tiles.  When
+//    (query blocks x kv heads) cannot cover the CUs, up to kWMaxSplit workgroups share a block's
+//    tiles and the last to finish merges their partials through the workspace.
+//  * Scores, transposed: S^T = K . Q^T with v_mfma_f32_32x32x16_f16.  The A operand (32 keys x 16
+//    dims) is one key row per lane, loaded straight from the pool into registers: MFMA K-step s
+//    takes dims D/2 * half + 8 s .. + 7, a permutation of the head dims applied to both operands,
+//    so a lane's K-steps read 128 contiguous bytes of its key row.  The B operand (the queries) is
+//    held for the whole kernel.  Each K fragment feeds both row tiles.
+//  * O^T += V^T . P^T: the probabilities stay in registers (a lane's 16 scores of a 32-key tile are
+//    the B operands of two K = 16 steps); V goes to the wave's own LDS tile as it is in the pool,
+//    [key][dim], and the A operand comes from transposing LDS reads (ds_read_b64_tr_b16).  Each V^T
+//    fragment feeds both row tiles.
+//  * Pipeline: tile i + 1's K and tile i + 2's V are in flight while tile i is multiplied; every
+//    load addresses a real row (an invalid page reads page 0), so each iteration waits for a fixed
+//    number of loads.  Keys past the end or in an invalid page are masked and their V rows zeroed.
+//  * Online softmax in base 2, per lane and row tile (one lane ^ 32 exchange per tile), with the
+//    lazy rescale of the running maximum (slack 2^8).
+//  * Epilogue: the 4 key groups merge log-sum-exp style through LDS, each wave finishing its own
+//    (dim tile, row tile) blocks; then the key-split merge and the fp16 stores.
+#include "ifn_common.hpp"
+
+namespace ifn {
+
+constexpr int kWBlock = 16;    // tokens per page compiled in
+constexpr int kWTile = 32;     // keys per tile
+constexpr int kWGroups = 4;    // waves (key groups) per workgroup
+constexpr int kWThreads = kWGroups * kWave;
+constexpr int kWMaxSplit = 16;
+constexpr int kWRows = 64;     // query rows per workgroup
+
+template <int D, int G>
+struct WideCfg {
+  static constexpr int kQw = kWRows / G;             // queries per workgroup
+  static constexpr int kKSteps = D / 16;             // MFMA K-steps over the head dims
+  static constexpr int kDT = D / 32;                 // 32-dim output tiles
+  static constexpr int kBlocks = 2 * kDT;            // output blocks: (dim tile, row tile)
+  static constexpr int kOwned = kBlocks / kWGroups;  // blocks each wave finishes
+  // V tile in LDS: two page halves of 16 key rows, row stride kVS halves (the 4 rows a 16-lane
+  // group reads in a transposing load sit on disjoint banks), each half padded to whole 64-slot
+  // (1 KiB) DMA instructions.
+  static constexpr int kVS = D + 16;
+  static constexpr int kRowSlots = kVS / 8;          // 16-byte slots per LDS row
+  static constexpr int kHalfSlots = (16 * kRowSlots + kWave - 1) / kWave * kWave;
+  static constexpr int kHalfInstr = kHalfSlots / kWave;  // DMA instructions per page half
+  static constexpr int kVBufBytes = 2 * kHalfSlots * 16;
+  static constexpr int kVBufs = 3;                   // V tiles in LDS per wave: i, i + 1, i + 2
+  static constexpr int kTileBytes = kWGroups * kVBufs * kVBufBytes;
+  static constexpr int kMlFloats = kWGroups * 2 * 32 * 2;
+  static constexpr int kMergeBytes = kMlFloats * 4 + kWGroups * kBlocks * 16 * kWave * 4;
+  static constexpr int kLdsBytes = kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes;
+  // VMEM instructions that may still be outstanding when a tile's V is read: the V DMA of the tile
+  // two ahead and the K loads of the next (see the main loop).
+  static constexpr int kVWait = 2 * kHalfInstr + kKSteps;
+  static_assert(kQw * G == kWRows, "64 rows per workgroup");
+  static_assert(kBlocks % kWGroups == 0, "every wave finishes the same number of blocks");
+  static_assert(kVWait < 64, "vmcnt range");
+};
+
+struct WidePlan {
+  int64_t n_qb;
+  int nsplit;
+  size_t off_ml, off_o, bytes;
+};
+
+// Key split: enough workgroups to cover the CUs when (query blocks x kv heads) alone does not,
+// provided every split still gets at least two tiles per key group.
+static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
+  WidePlan p;
+  const int g = hq / hkv;
+  p.n_qb = (int64_t(T) + kWRows / g - 1) / (kWRows / g);
+  const int64_t units = p.n_qb * hkv;
+  const int64_t max_tiles = (int64_t(query_start) + T + kWTile - 1) / kWTile;
+  int ns = 1;
+  while (ns < kWMaxSplit && units * ns * 2 <= cus && max_tiles >= int64_t(2 * ns) * 2 * kWGroups) ns *= 2;
+  if (units > kMaxTickets) ns = 1;
+  p.nsplit = ns;
+  const size_t slots = size_t(units) * ns;
+  p.off_ml = kTicketBytes;
+  p.off_o = p.off_ml + align256(slots * kWRows * 2 * sizeof(float));
+  p.bytes = ns > 1 ? p.off_o + align256(slots * kWRows * size_t(d) * sizeof(float)) : 256;
+  return p;
+}
+
+// The chunk's K and V rows -> the pool at table[pos / 16] * 16 + pos % 16, pos = query_start + t
+// (16-byte chunks, grid-stride; rows whose page id is outside the pool are skipped).
+__device__ __forceinline__ void wide_store_chunk(f16* __restrict__ pool, int64_t num_pages,
+                                                 const int32_t* __restrict__ table, int32_t query_start, int32_t T,
+                                                 int32_t hkv, int32_t d, const f16* __restrict__ new_k,
+                                                 const f16* __restrict__ new_v, int64_t first, int64_t step) {
+  const int chunks = hkv * d / 8;
+  const int64_t tok_stride = int64_t(hkv) * d;
+  const int64_t items = int64_t(T) * 2 * chunks;
+  for (int64_t it = first; it < items; it += step) {
+    const int t = int(it / (2 * chunks));
+    const int rem = int(it % (2 * chunks));
+    const int kv = rem / chunks, c = rem % chunks;
+    const int pos = query_start + t;
+    const int page = table[pos / kWBlock];
+    if (page < 0 || int64_t(page) >= num_pages) continue;
+    const f16* src = (kv == 0 ? new_k : new_v) + int64_t(t) * tok_stride + c * 8;
+    f16* dst = pool + (int64_t(kv) * num_pages * kWBlock + int64_t(page) * kWBlock + pos % kWBlock) * tok_stride + c * 8;
+    *reinterpret_cast<u32x4*>(dst) = ld16(src);
+  }
+}
+
+// 16-byte buffer load of each lane straight into LDS at lds + 16 * lane (buffer_load_dwordx4 ... lds);
+// an offset past the resource's end writes zeros.  (Device compilation only, like the asm below: the
+// host pass does not know the builtin and would drop the kernels' launch stubs.)
+__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, __attribute__((address_space(3))) void* lds,
+                                      uint32_t off) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, off, 0, 0, 0);
+#endif
+}
+
+// Transposing LDS read (ds_read_b64_tr_b16) issued through inline asm.  The V tiles arrive by DMA
+// (buffer_load ... lds), which the compiler orders against LDS reads only per LDS object -- it would
+// wait for the newest DMA into any of the three buffers before every read.  The kernel waits for
+// the right DMA itself (vmcnt) and for these reads with wait_lds below.
+__device__ __forceinline__ u32x2 ds_read_tr16(const void* p) {
+  u32x2 r = u32x2{0u, 0u};
+#if defined(__HIP_DEVICE_COMPILE__)
+  const uint32_t a = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
+  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
+#endif
+  return r;
+}
+// Waits for every outstanding LDS access of the wave; the values passed through it are the ones the
+// reads above return, so nothing that uses them is scheduled before the wait.
+__device__ __forceinline__ void wait_lds(u32x2 (&r)[8]) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt lgkmcnt(0)"
+               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+#endif
+}
+
+// No instruction: the values must exist at this point (and the scheduler treats it as a boundary).
+__device__ __forceinline__ void pin_regs(f16x8& a, f16x8& b, f16x8& c, f16x8& d) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+#endif
+}
+
+template <int D, int G, bool kAppend>
+__global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
+    f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
+    const int32_t* __restrict__ table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb,
+    int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap) {
+  using C = WideCfg<D, G>;
+  constexpr int kKS = C::kKSteps;
+  constexpr int kDT = C::kDT;
+  constexpr int kQw = C::kQw;
+  // Workgroup i runs on XCD i % 8: kv head = i % Hkv keeps each head's K/V in one XCD's L2 (for
+  // Hkv = 8); query blocks go longest key range first.
+  const int kvh = int(blockIdx.x) % num_kv_heads;
+  const int split = (int(blockIdx.x) / num_kv_heads) % nsplit;
+  const int qb = n_qb - 1 - int(blockIdx.x) / (num_kv_heads * nsplit);
+  const int tid = threadIdx.x;
+  const int grp = __builtin_amdgcn_readfirstlane(tid / kWave);  // key group = wave
+  const int lane = tid % kWave;
+  const int col = lane % 32, half = lane / 32;
+  const int hq = num_kv_heads * G;
+  const int total = query_start + T;
+  const int q0 = qb * kQw;
+  const int key_end = min(total, query_start + q0 + kQw);  // keys some row of the block sees
+  const int min_pos = query_start + q0;                    // the block's first query position
+  const int n_tiles = int(ceil_div(key_end, kWTile));
+  auto tile_of = [&](int i) { return (i * nsplit + split) * kWGroups + grp; };
+  const int first = split * kWGroups + grp;
+  const int iters = n_tiles > first ? int(ceil_div(n_tiles - first, kWGroups * nsplit)) : 0;
+
+  // This lane's row in each row tile: row = 32 rt + col = g * kQw + query offset.
+  int my_q[2], my_pos[2], my_head[2];
+  bool q_ok[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) {
+    const int rho = 32 * rt + col;
+    my_q[rt] = q0 + rho % kQw;
+    my_head[rt] = kvh * G + rho / kQw;
+    my_pos[rt] = query_start + my_q[rt];
+    q_ok[rt] = my_q[rt] < T;
+  }
+  // Q^T as the B operand, K-step s = dims D/2 * half + 8 s .. + 7
+  f16x8 qreg[2][kKS];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int s = 0; s < kKS; ++s)
+      qreg[rt][s] = q_ok[rt] ? as_h8(ld16(q + (int64_t(my_q[rt]) * hq + my_head[rt]) * D + (D / 2) * half + 8 * s))
+                             : f16x8{};
+
+  __shared__ __attribute__((aligned(16))) unsigned char smem[C::kLdsBytes];
+
+  const int64_t tok_stride = int64_t(num_kv_heads) * D;
+  const int64_t v_off = num_pages * kWBlock * tok_stride;
+  const int64_t page_elems = int64_t(kWBlock) * tok_stride;
+  const f16* head_pool = pool + int64_t(kvh) * D;
+
+  if constexpr (kAppend)
+    wide_store_chunk(ap.pool, num_pages, table, query_start, T, num_kv_heads, D, ap.new_k, ap.new_v,
+                     int64_t(blockIdx.x) * kWThreads + tid, int64_t(gridDim.x) * kWThreads);
+
+  // Page ids: a tile of 32 keys spans two pages.  Lane l of a window holds page 2 * tile + (l & 1) of
+  // the wave's (l / 2)-th tile of that window (32 tiles), read with v_readlane.  The K and the V
+  // loads run one tile apart, each through its own window, so neither reloads a window twice.
+  const int seq_pages = int(ceil_div(total, kWBlock));
+  struct Window {
+    int ids, w;
+  };
+  Window win_k{-1, -1}, win_v{-1, -1};
+  auto tile_pages = [&](Window& wn, int i, int& pa, int& pb) __attribute__((always_inline)) {
+    if ((i >> 5) != wn.w) {
+      wn.w = i >> 5;
+      const int pg = 2 * tile_of(32 * wn.w + lane / 2) + (lane & 1);
+      const int id = table[min(pg, seq_pages - 1)];
+      wn.ids = pg < seq_pages ? id : -1;
+      asm volatile("" ::"v"(wn.ids));  // the window load completes here, not at every readlane
+    }
+    pa = __builtin_amdgcn_readlane(wn.ids, 2 * (i & 31));
+    pb = __builtin_amdgcn_readlane(wn.ids, 2 * (i & 31) + 1);
+  };
+  // Tile flags (uniform): bit 0/1 = first/second page valid, bit 2 = every key of the tile is
+  // visible to every row of the block (no mask, no zero fill).
+  auto tile_flags = [&](int i, int pa, int pb) __attribute__((always_inline)) -> int {
+    const int kt = tile_of(i) * kWTile;
+    const int oka = pa >= 0 && int64_t(pa) < num_pages, okb = pb >= 0 && int64_t(pb) < num_pages;
+    const int full = oka && okb && kt + kWTile <= total && kt + kWTile - 1 <= min_pos;
+    return oka | (okb << 1) | (full << 2);
+  };
+
+  // Fused append: buffer resources over the chunk's rows (T rows; past them a load reads zero).
+  const int rsrc_bytes = kAppend ? T * int(tok_stride) * 2 : 0;
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_k), 0, rsrc_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_v), 0, rsrc_bytes, 0x00020000);
+
+  // K: this lane's key row (col) of the tile, dims D/2 * half .. + D/2, as kKS 16-byte chunks.
+  // Returns the tile's flags.
+  auto load_k = [&](int i, u32x4 (&kr)[kKS]) __attribute__((always_inline)) -> int {
+    int pa, pb;
+    tile_pages(win_k, i, pa, pb);
+    const int fl = tile_flags(i, pa, pb);
+    const int kt = tile_of(i) * kWTile;
+    if constexpr (kAppend) {
+      if (kt >= query_start) {  // (uniform; query_start % 32 == 0) the tile's keys are chunk rows
+        // rows past the chunk's end read zero; tiles past the last are clamped to row T
+        const int row = min(kt - query_start, T) + col;
+        const int base = (row * int(tok_stride) + kvh * D + (D / 2) * half) * 2;
+#pragma unroll
+        for (int s = 0; s < kKS; ++s)
+          kr[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, base + 16 * s, 0, 0));
+        return fl;
+      }
+    }
+    const int page = col < kWBlock ? ((fl & 1) ? pa : 0) : ((fl & 2) ? pb : 0);
+    const f16* src = head_pool + int64_t(page) * page_elems + (col % kWBlock) * tok_stride + (D / 2) * half;
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) kr[s] = ld16(src + 8 * s);
+    return fl;
+  };
+  // V: DMA straight into one of the wave's two LDS tile buffers (buffer_load_dwordx4 ... lds, 64
+  // lanes x 16 bytes per instruction at consecutive LDS addresses).  Slot 64 n + lane of page half
+  // h is LDS row (slot / kRowSlots) of the half, 16-byte chunk (slot % kRowSlots); chunks past the
+  // row's D / 8 are padding.  Each half reads through a buffer resource that ends after the page's
+  // keys below the end of the sequence (none for an invalid page), so every other row, and the
+  // padding (offset past any resource), is written as zeros: masked keys contribute exactly nothing.
+  uint32_t voff[C::kHalfInstr];
+#pragma unroll
+  for (int n = 0; n < C::kHalfInstr; ++n) {
+    const int slot = n * kWave + lane, r = slot / C::kRowSlots, c = slot % C::kRowSlots;
+    voff[n] = r < 16 && c < D / 8 ? uint32_t((r * int(tok_stride) + 8 * c) * 2) : 0x7ffffff0u;
+  }
+  __attribute__((address_space(3))) unsigned char* const vlds =
+      (__attribute__((address_space(3))) unsigned char*)(smem) + grp * C::kVBufs * C::kVBufBytes;
+  auto dma_v = [&](int i, int buf) __attribute__((always_inline)) {
+    int pa, pb;
+    tile_pages(win_v, i, pa, pb);
+    const int fl = tile_flags(i, pa, pb);
+    const int kt = tile_of(i) * kWTile;
+    __attribute__((address_space(3))) unsigned char* const dst = vlds + buf * C::kVBufBytes;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      __amdgpu_buffer_rsrc_t r;
+      uint32_t add = 0;
+      bool chunk_rows = false;
+      if constexpr (kAppend) chunk_rows = kt >= query_start;  // (uniform) the tile's keys are chunk rows
+      if (chunk_rows) {
+        r = rv;  // rows past the chunk's end read zero
+        add = uint32_t(((min(kt - query_start, T) + 16 * h) * int(tok_stride) + kvh * D) * 2);
+      } else {
+        // (page and key count are uniform; readfirstlane keeps the descriptor in scalar registers)
+        const bool ok = ((fl >> h) & 1) != 0;
+        const int page = __builtin_amdgcn_readfirstlane(ok ? (h == 0 ? pa : pb) : 0);
+        const int keys = __builtin_amdgcn_readfirstlane(ok ? min(max(total - (kt + 16 * h), 0), 16) : 0);
+        r = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(head_pool + v_off + int64_t(page) * page_elems), 0,
+                                              keys * int(tok_stride) * 2, 0x00020000);
+      }
+#pragma unroll
+      for (int n = 0; n < C::kHalfInstr; ++n)
+        dma16(r, dst + (h * C::kHalfSlots + n * kWave) * 16, voff[n] + add);
+    }
+  };
+
+  // transposing V reads: lane = 16 g + 4 r + q reads key row 4 (lane / 32) + r of a page half,
+  // dims 16 (g % 2) + 4 q (halves)
+  const int tr_off = (4 * half + (lane % 16) / 4) * C::kVS + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
+
+  float m[2] = {kNegBig, kNegBig}, lsum[2] = {0.f, 0.f};
+  f32x16 acc[kDT][2];
+#pragma unroll
+  for (int dt = 0; dt < kDT; ++dt) acc[dt][0] = acc[dt][1] = f32x16{};
+
+  // Pipeline.  Iteration i turns tile i's scores (computed in the previous iteration) into
+  // probabilities while the matrix cores compute tile i + 1's scores: the S MFMAs of tile i + 1 are
+  // issued first and the softmax VALU work of tile i fills their execution (scheduling groups
+  // interleave them).  Then come the V DMA of tile i + 2 (into the buffer tile i - 1 used), the K
+  // loads of tile i + 2, and tile i's PV MFMAs.  VMEM instructions complete in order, so when the K
+  // loads of a tile are waited for, every V DMA issued before them has landed too; at most kVWait
+  // requests (a V DMA and a K load group) are outstanding when tile i's V is read.  Every request is
+  // unconditional (past the last tile they read page 0 or zeros), so these counts are exact.
+  u32x4 kr[kKS];
+  dma_v(0, 0);
+  dma_v(1, 1);
+  int kfl = load_k(0, kr);
+  auto s_mfma = [&](f32x16 (&st)[2]) __attribute__((always_inline)) {  // S^T of both row tiles
+    st[0] = f32x16{};
+    st[1] = f32x16{};
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) {
+      const f16x8 kf = as_h8(kr[s]);
+      st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[0][s], st[0], 0, 0, 0);
+      st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[1][s], st[1], 0, 0, 0);
+    }
+  };
+  f32x16 st[2];
+  s_mfma(st);  // tile 0
+  int sfl = kfl;
+  kfl = load_k(1, kr);
+
+  for (int i = 0; i < iters; ++i) {
+    const int fl = sfl;
+    const int kt = tile_of(i) * kWTile;
+    const int buf = i % C::kVBufs;
+    float sv[2][16];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) sv[rt][r] = st[rt][r];
+    // online softmax of tile i.  Causal mask, end of sequence, invalid pages:
+    if (!(fl & 4)) {
+      const bool oka = (fl & 1) != 0, okb = (fl & 2) != 0;
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int kk = 8 * (r / 4) + 4 * half + (r % 4);
+          const bool ok = (kk >= kWBlock ? okb : oka) & (kt + kk <= my_pos[rt]) & (kt + kk < total);
+          sv[rt][r] = ok ? sv[rt][r] : -INFINITY;
+        }
+    }
+    // Row maxima (a tree, then the lane ^ 32 partner's) and the lazy rescale: the reference maximum
+    // moves only when a score exceeds it by more than kSlack (log2 units), so P = 2^(s - m) <
+    // 2^kSlack; acc and lsum stay relative to m.
+    constexpr float kSlack = 8.f;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float mq[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a)
+        mq[a] = fmaxf(fmaxf(sv[rt][4 * a], sv[rt][4 * a + 1]), fmaxf(sv[rt][4 * a + 2], sv[rt][4 * a + 3]));
+      float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float cand = mx * scale_log2;
+      const bool grow = cand > m[rt] + kSlack;
+      if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow) != 0, 0)) {  // rare after the first tile
+        const float mn = grow ? cand : m[rt];
+        const float alpha = exp2_fast(m[rt] - mn);
+        lsum[rt] *= alpha;
+#pragma unroll
+        for (int dt = 0; dt < kDT; ++dt) acc[dt][rt] *= alpha;
+        m[rt] = mn;
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // One scheduling region: tile i + 1's S MFMAs (issued first; they read K(i + 1), loaded one
+    // iteration ago) and tile i's exponentials, row sums and fp16 packing, interleaved one MFMA to
+    // a group of VALU instructions.  (Past the last tile the MFMAs multiply a zero or page-0 tile,
+    // never used.)
+    s_mfma(st);
+    sfl = kfl;
+    f16x8 pb16[2][2];
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      float pv[16];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) pv[r] = exp2_fast(fmaf(sv[rt][r], scale_log2, -m[rt]));
+      // row sum: four partial sums, each in key order
+      float ps[4];
+#pragma unroll
+      for (int a = 0; a < 4; ++a) ps[a] = (pv[4 * a] + pv[4 * a + 1]) + (pv[4 * a + 2] + pv[4 * a + 3]);
+      lsum[rt] += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+      pb16[rt][0] = f16x8{f16(pv[0]), f16(pv[1]), f16(pv[2]), f16(pv[3]), f16(pv[4]), f16(pv[5]), f16(pv[6]),
+                          f16(pv[7])};
+      pb16[rt][1] = f16x8{f16(pv[8]), f16(pv[9]), f16(pv[10]), f16(pv[11]), f16(pv[12]), f16(pv[13]),
+                          f16(pv[14]), f16(pv[15])};
+    }
+    // (the probabilities are pinned here, so the exponentials are not sunk to their use in the PV
+    // MFMAs below, out of the MFMAs' shadow)
+    pin_regs(pb16[0][0], pb16[0][1], pb16[1][0], pb16[1][1]);
+#pragma unroll
+    for (int k = 0; k < 2 * kKS; ++k) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // the buffer of tile i - 1 takes tile i + 2 once tile i - 1's reads have completed (DMA writes
+    // reach LDS outside the wave's LDS instruction order); then tile i + 2's keys
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    dma_v(i + 2, (i + 2) % C::kVBufs);
+    kfl = load_k(i + 2, kr);
+    // tile i's V DMA has landed once at most kVWait later VMEM instructions are outstanding
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::kVWait) : "memory");
+    // O^T += V^T . P^T: each V^T fragment feeds both row tiles.  A = V^T for dims 32 dt + col, keys
+    // 16 u + 4 half + 0..3 and 16 u + 8 + 4 half + 0..3 (page half u).
+    const f16* vt = reinterpret_cast<const f16*>(smem + (grp * C::kVBufs + buf) * C::kVBufBytes);
+    // two dim tiles per batch: 8 reads in flight, one wait, 8 MFMAs
+#pragma unroll
+    for (int d0 = 0; d0 < kDT; d0 += 2) {
+      u32x2 rd[8];
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const f16* vp = vt + u * C::kHalfSlots * 8 + tr_off + 32 * (d0 + j);
+          rd[4 * j + 2 * u] = ds_read_tr16(vp);
+          rd[4 * j + 2 * u + 1] = ds_read_tr16(vp + 8 * C::kVS);
+        }
+      wait_lds(rd);
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const f16x4 lo = __builtin_bit_cast(f16x4, rd[4 * j + 2 * u]);
+          const f16x4 hi = __builtin_bit_cast(f16x4, rd[4 * j + 2 * u + 1]);
+          const f16x8 vf = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          acc[d0 + j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[0][u], acc[d0 + j][0], 0, 0, 0);
+          acc[d0 + j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[1][u], acc[d0 + j][1], 0, 0, 0);
+        }
+    }
+  }
+  // Outstanding DMAs (tiles past the last) land before the LDS is reused for the merge.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+
+  float lt[2];
+#pragma unroll
+  for (int rt = 0; rt < 2; ++rt) lt[rt] = lsum[rt] + __shfl_xor(lsum[rt], 32);
+  // Key-group merge: every wave writes its (m, l) and all its blocks to LDS; block p = (dim tile
+  // p / 2, row tile p % 2) is then finished by wave p % 4, from the four groups' copies in group
+  // order.  Every block a wave finishes has row tile rt_own = grp % 2.
+  const int rt_own = grp % 2;
+  float* mlb = reinterpret_cast<float*>(smem);                 // [wave][rt][32][2]
+  f32x4* accb = reinterpret_cast<f32x4*>(mlb + C::kMlFloats);  // [wave][block][4][lane]
+  if (half == 0) {
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      mlb[((grp * 2 + rt) * 32 + col) * 2 + 0] = m[rt];
+      mlb[((grp * 2 + rt) * 32 + col) * 2 + 1] = lt[rt];
+    }
+  }
+#pragma unroll
+  for (int p = 0; p < C::kBlocks; ++p)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const f32x16& a = acc[p / 2][p % 2];
+      accb[((grp * C::kBlocks + p) * 4 + r4) * kWave + lane] = f32x4{a[4 * r4], a[4 * r4 + 1], a[4 * r4 + 2], a[4 * r4 + 3]};
+    }
+  __syncthreads();
+  float mk[kWGroups], lk[kWGroups];
+#pragma unroll
+  for (int k = 0; k < kWGroups; ++k) {
+    mk[k] = mlb[((k * 2 + rt_own) * 32 + col) * 2];
+    lk[k] = mlb[((k * 2 + rt_own) * 32 + col) * 2 + 1];
+  }
+  float mfin = mk[0];
+#pragma unroll
+  for (int k = 1; k < kWGroups; ++k) mfin = fmaxf(mfin, mk[k]);
+  float wk[kWGroups];
+#pragma unroll
+  for (int k = 0; k < kWGroups; ++k) wk[k] = exp2_fast(mk[k] - mfin);
+  float lfin = wk[0] * lk[0];
+#pragma unroll
+  for (int k = 1; k < kWGroups; ++k) lfin = fmaf(wk[k], lk[k], lfin);
+  f32x4 o[C::kOwned][4];  // the blocks this wave finishes: p = grp + 4 ob
+#pragma unroll
+  for (int ob = 0; ob < C::kOwned; ++ob) {
+    const int p = grp + kWGroups * ob;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      f32x4 x = accb[((0 * C::kBlocks + p) * 4 + r4) * kWave + lane];
+      f32x4 y = x * wk[0];
+#pragma unroll
+      for (int k = 1; k < kWGroups; ++k) {
+        x = accb[((k * C::kBlocks + p) * 4 + r4) * kWave + lane];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = fmaf(wk[k], x[e], y[e]);
+      }
+      o[ob][r4] = y;
+    }
+  }
+
+  if (nsplit > 1) {
+    // Cross-workgroup merge: every wave publishes its blocks of this split's partial with 16-byte
+    // device-coherent stores (lane-contiguous), waves 0 and 1 their row tile's (m, l); once all are
+    // acknowledged one thread takes the (query block, kv head) ticket.  The last of the nsplit
+    // arrivals combines every split's partial, its own included (read back), in split order, so
+    // the result does not depend on the arrival order.
+    __shared__ uint32_t s_ticket;
+    const int64_t pair = int64_t(qb) * num_kv_heads + kvh;
+    const int64_t slot = pair * nsplit + split;
+    const int64_t nslots = int64_t(n_qb) * num_kv_heads * nsplit;
+    const __amdgpu_buffer_rsrc_t r_o = make_rsrc(ws.o, uint32_t(nslots * kWRows * D * 4));
+    const __amdgpu_buffer_rsrc_t r_ml = make_rsrc(ws.ml, uint32_t(nslots * kWRows * 2 * 4));
+    auto o_off = [&](int64_t sl, int p, int r4) __attribute__((always_inline)) {
+      return uint32_t((((sl * C::kBlocks + p) * 4 + r4) * kWave + lane) * 16);
+    };
+    const uint32_t ml_row = uint32_t(rt_own * 32 + col) * 8;
+#pragma unroll
+    for (int ob = 0; ob < C::kOwned; ++ob)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) st_dev4(r_o, o_off(slot, grp + kWGroups * ob, r4), o[ob][r4]);
+    if (grp < 2 && half == 0) st_dev2(r_ml, uint32_t(slot * kWRows * 8) + ml_row, f32x2{mfin, lfin});
+    wait_all_mem();   // this wave's stores are acknowledged
+    __syncthreads();  // ... and every other wave's
+    if (tid == 0) s_ticket = __hip_atomic_fetch_add(ws.count + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __syncthreads();
+    if (s_ticket != uint32_t(nsplit - 1)) return;
+    compiler_fence();  // the merge loads below stay behind the ticket
+    float mx = kNegBig;
+    for (int s2 = 0; s2 < nsplit; ++s2) mx = fmaxf(mx, ld_dev2(r_ml, uint32_t((pair * nsplit + s2) * kWRows * 8) + ml_row)[0]);
+    lfin = 0.f;
+#pragma unroll
+    for (int ob = 0; ob < C::kOwned; ++ob)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) o[ob][r4] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // splits in batches of kSplitBatch, every load of a batch in flight at once
+    constexpr int kSplitBatch = 4;
+    for (int s0 = 0; s0 < nsplit; s0 += kSplitBatch) {
+#pragma unroll
+      for (int sb = 0; sb < kSplitBatch; ++sb) {
+        const int s2 = s0 + sb;
+        if (s2 < nsplit) {
+          const int64_t sl = pair * nsplit + s2;
+          const f32x2 ml = ld_dev2(r_ml, uint32_t(sl * kWRows * 8) + ml_row);
+          f32x4 x[C::kOwned][4];
+#pragma unroll
+          for (int ob = 0; ob < C::kOwned; ++ob)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4) x[ob][r4] = ld_dev4(r_o, o_off(sl, grp + kWGroups * ob, r4));
+          const float wsp = exp2_fast(ml[0] - mx);
+          lfin = fmaf(wsp, ml[1], lfin);
+#pragma unroll
+          for (int ob = 0; ob < C::kOwned; ++ob)
+#pragma unroll
+            for (int r4 = 0; r4 < 4; ++r4)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) o[ob][r4][e] = fmaf(wsp, x[ob][r4][e], o[ob][r4][e]);
+        }
+      }
+    }
+    mfin = mx;
+    if (tid == 0) reset_ticket(ws.count + pair);
+  }
+
+  if (!q_ok[rt_own]) return;
+  const float inv = lfin > 0.f ? 1.f / lfin : 0.f;
+  f16* orow = out + (int64_t(my_q[rt_own]) * hq + my_head[rt_own]) * D;
+#pragma unroll
+  for (int ob = 0; ob < C::kOwned; ++ob) {
+    const int dt = (grp + kWGroups * ob) / 2;
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {  // dims 32 dt + 8 r4 + 4 half + 0..3
+      const f32x4 y = o[ob][r4];
+      *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * r4 + 4 * half) =
+          f16x4{f16(y[0] * inv), f16(y[1] * inv), f16(y[2] * inv), f16(y[3] * inv)};
+    }
+  }
+}
+
+typedef void (*WideKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t, int32_t, int32_t,
+                           int32_t, float, PrefillWorkspace, PrefillAppend);
+
+static WideKernel pick_wide(int d, int g, bool append) {
+#define IFN_WIDE_CASE(DD, GG)                                                                        \
+  if (d == DD && g == GG) return append ? prefill_wide_kernel<DD, GG, true> : prefill_wide_kernel<DD, GG, false>;
+  IFN_WIDE_CASE(64, 1) IFN_WIDE_CASE(64, 2) IFN_WIDE_CASE(64, 4) IFN_WIDE_CASE(64, 8)
+  IFN_WIDE_CASE(128, 1) IFN_WIDE_CASE(128, 2) IFN_WIDE_CASE(128, 4) IFN_WIDE_CASE(128, 8)
+#undef IFN_WIDE_CASE
+  return nullptr;
+}
+
+bool wide_prefill_supported(int32_t hq, int32_t hkv, int32_t d) {
+  return hkv >= 1 && hq % hkv == 0 && pick_wide(d, hq / hkv, false) != nullptr;
+}
+
+size_t wide_prefill_ws_bytes(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
+  return plan_wide(T, query_start, hq, hkv, d, cus).bytes;
+}
+
+int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* table,
+                        int32_t query_start, int32_t T, int32_t hq, int32_t hkv, int32_t d, float scale_log2,
+                        void* workspace, size_t workspace_bytes, const PrefillAppend& ap, int cus,
+                        hipStream_t stream) {
+  WideKernel k = pick_wide(d, hq / hkv, ap.pool != nullptr);
+  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
+  const WidePlan p = plan_wide(T, query_start, hq, hkv, d, cus);
+  if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
+  PrefillWorkspace ws{nullptr, nullptr, nullptr};
+  if (p.nsplit > 1) {
+    if (workspace == nullptr || workspace_bytes < p.bytes) return IFN_ERR_WORKSPACE;
+    IFN_CHECK_ALIGN16(workspace);
+    uint8_t* wsb = static_cast<uint8_t*>(workspace);
+    ws.count = reinterpret_cast<uint32_t*>(wsb);
+    ws.ml = reinterpret_cast<float*>(wsb + p.off_ml);
+    ws.o = reinterpret_cast<float*>(wsb + p.off_o);
+  }
+  k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(kWThreads), 0, stream>>>(
+      out, q, pool, num_pages, table, query_start, T, hkv, int(p.n_qb), p.nsplit, scale_log2, ws, ap);
+  return ifn_launch_status();
+}
+
+}  // namespace ifn
