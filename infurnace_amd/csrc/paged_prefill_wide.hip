@@ -17,14 +17,15 @@
 //    so a lane's K-steps read 128 contiguous bytes of its key row.  The B operand (the queries) is
 //    held for the whole kernel.  Each K fragment feeds both row tiles.
 //  * O^T += V^T . P^T: the probabilities stay in registers (a lane's 16 scores of a 32-key tile are
-//    the B operands of two K = 16 steps); V goes to the wave's own LDS tile as it is in the pool,
-//    [key][dim], and the A operand comes from transposing LDS reads (ds_read_b64_tr_b16).  Each V^T
-//    fragment feeds both row tiles.
-//  * Pipeline: tile i + 1's K and tile i + 2's V are in flight while tile i is multiplied; every
-//    load addresses a real row (an invalid page reads page 0), so each iteration waits for a fixed
-//    number of loads.  Keys past the end or in an invalid page are masked and their V rows zeroed.
+//    the B operands of two K = 16 steps); V goes through registers to the wave's own LDS tile as it
+//    is in the pool, [key][dim] (16-byte chunks XOR-swizzled by row), and the A operand comes from
+//    transposing LDS reads (ds_read_b64_tr_b16).  Each V^T fragment feeds both row tiles.
+//  * Pipeline: tile i + 1's scores are computed while tile i's probabilities are formed, and the
+//    next tiles' K and V loads are spread between the MFMAs; every load addresses a real row (an
+//    invalid page reads page 0).  Keys past the end or in an invalid page are masked (only in the
+//    tiles that hold such keys) and their V rows zeroed.
 //  * Online softmax in base 2, per lane and row tile (one lane ^ 32 exchange per tile), with the
-//    lazy rescale of the running maximum (slack 2^8).
+//    lazy rescale of the running maximum (slack 2^8); row sums add the fp16 probabilities.
 //  * Epilogue: the 4 key groups merge log-sum-exp style through LDS, each wave finishing its own
 //    (dim tile, row tile) blocks; then the key-split merge and the fp16 stores.
 #include "ifn_common.hpp"
@@ -45,25 +46,22 @@ struct WideCfg {
   static constexpr int kDT = D / 32;                 // 32-dim output tiles
   static constexpr int kBlocks = 2 * kDT;            // output blocks: (dim tile, row tile)
   static constexpr int kOwned = kBlocks / kWGroups;  // blocks each wave finishes
-  // V tile in LDS: two page halves of 16 key rows, row stride kVS halves (the 4 rows a 16-lane
-  // group reads in a transposing load sit on disjoint banks), each half padded to whole 64-slot
-  // (1 KiB) DMA instructions.
-  static constexpr int kVS = D + 16;
-  static constexpr int kRowSlots = kVS / 8;          // 16-byte slots per LDS row
-  static constexpr int kHalfSlots = (16 * kRowSlots + kWave - 1) / kWave * kWave;
-  static constexpr int kHalfInstr = kHalfSlots / kWave;  // DMA instructions per page half
-  static constexpr int kVBufBytes = 2 * kHalfSlots * 16;
-  static constexpr int kVBufs = 3;                   // V tiles in LDS per wave: i, i + 1, i + 2
+  // V tile in LDS: two page halves of 16 key rows x D dims, [key][dim] as in the pool and
+  // unpadded; the 16-byte chunk c of row r sits at chunk position c ^ 2 (r % 4), so the 4 rows a
+  // 16-lane group reads in one transposing load fall on disjoint banks.
+  static constexpr int kRowChunks = D / 8;                     // 16-byte chunks per key row
+  static constexpr int kHalfInstr = 16 * kRowChunks / kWave;   // DMA instructions per page half
+  static constexpr int kHalfBytes = 16 * D * 2;
+  static constexpr int kVBufBytes = 2 * kHalfBytes;
+  static constexpr int kVInstr = 2 * kHalfInstr;     // 16-byte loads (and LDS writes) per lane per tile
+  static constexpr int kVBufs = 2;                   // V tiles in LDS per wave: i and i + 1
   static constexpr int kTileBytes = kWGroups * kVBufs * kVBufBytes;
   static constexpr int kMlFloats = kWGroups * 2 * 32 * 2;
   static constexpr int kMergeBytes = kMlFloats * 4 + kWGroups * kBlocks * 16 * kWave * 4;
   static constexpr int kLdsBytes = kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes;
-  // VMEM instructions that may still be outstanding when a tile's V is read: the V DMA of the tile
-  // two ahead and the K loads of the next (see the main loop).
-  static constexpr int kVWait = 2 * kHalfInstr + kKSteps;
   static_assert(kQw * G == kWRows, "64 rows per workgroup");
   static_assert(kBlocks % kWGroups == 0, "every wave finishes the same number of blocks");
-  static_assert(kVWait < 64, "vmcnt range");
+  static_assert(16 * kRowChunks % kWave == 0 && kRowChunks >= 8, "whole loads per page half; swizzle in range");
 };
 
 struct WidePlan {
@@ -113,37 +111,33 @@ __device__ __forceinline__ void wide_store_chunk(f16* __restrict__ pool, int64_t
   }
 }
 
-// 16-byte buffer load of each lane straight into LDS at lds + 16 * lane (buffer_load_dwordx4 ... lds);
-// an offset past the resource's end writes zeros.  (Device compilation only, like the asm below: the
-// host pass does not know the builtin and would drop the kernels' launch stubs.)
-__device__ __forceinline__ void dma16(__amdgpu_buffer_rsrc_t r, __attribute__((address_space(3))) void* lds,
-                                      uint32_t off) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, lds, 16, off, 0, 0, 0);
-#endif
-}
+typedef __attribute__((address_space(3))) unsigned char lds_u8;
 
-// Transposing LDS read (ds_read_b64_tr_b16) issued through inline asm.  The V tiles arrive by DMA
-// (buffer_load ... lds), which the compiler orders against LDS reads only per LDS object -- it would
-// wait for the newest DMA into any of the three buffers before every read.  The kernel waits for
-// the right DMA itself (vmcnt) and for these reads with wait_lds below.
-__device__ __forceinline__ u32x2 ds_read_tr16(const void* p) {
-  u32x2 r = u32x2{0u, 0u};
+// Transposing LDS read of 4 fp16 per lane (ds_read_b64_tr_b16).  (Device compilation only, like the
+// other gfx950 builtins below: the host pass does not know them and would drop the kernels' launch
+// stubs.)
+__device__ __forceinline__ u32x2 ds_read_tr16(const lds_u8* p) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const uint32_t a = uint32_t(reinterpret_cast<uintptr_t>((__attribute__((address_space(3))) const void*)(p)));
-  asm volatile("ds_read_b64_tr_b16 %0, %1" : "=v"(r) : "v"(a));
-#endif
-  return r;
-}
-// Waits for every outstanding LDS access of the wave; the values passed through it are the ones the
-// reads above return, so nothing that uses them is scheduled before the wait.
-__device__ __forceinline__ void wait_lds(u32x2 (&r)[8]) {
-#if defined(__HIP_DEVICE_COMPILE__)
-  asm volatile("s_waitcnt lgkmcnt(0)"
-               : "+v"(r[0]), "+v"(r[1]), "+v"(r[2]), "+v"(r[3]), "+v"(r[4]), "+v"(r[5]), "+v"(r[6]), "+v"(r[7]));
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  return __builtin_bit_cast(
+      u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)(const_cast<lds_u8*>(p))));
+#else
+  return u32x2{0u, 0u};
 #endif
 }
-
+// 16-byte buffer load (buffer_load_dwordx4); an offset past the resource's end reads zeros.
+__device__ __forceinline__ u32x4 buf_ld16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0));
+}
+// Maximum of lanes l and l ^ 32 (v_permlane32_swap: a VALU exchange, no LDS traffic).
+__device__ __forceinline__ float max_lane32(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+#else
+  return x;
+#endif
+}
 // No instruction: the values must exist at this point (and the scheduler treats it as a boundary).
 __device__ __forceinline__ void pin_regs(f16x8& a, f16x8& b, f16x8& c, f16x8& d) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -173,7 +167,6 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   const int total = query_start + T;
   const int q0 = qb * kQw;
   const int key_end = min(total, query_start + q0 + kQw);  // keys some row of the block sees
-  const int min_pos = query_start + q0;                    // the block's first query position
   const int n_tiles = int(ceil_div(key_end, kWTile));
   auto tile_of = [&](int i) { return (i * nsplit + split) * kWGroups + grp; };
   const int first = split * kWGroups + grp;
@@ -190,15 +183,6 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     my_pos[rt] = query_start + my_q[rt];
     q_ok[rt] = my_q[rt] < T;
   }
-  // Q^T as the B operand, K-step s = dims D/2 * half + 8 s .. + 7
-  f16x8 qreg[2][kKS];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int s = 0; s < kKS; ++s)
-      qreg[rt][s] = q_ok[rt] ? as_h8(ld16(q + (int64_t(my_q[rt]) * hq + my_head[rt]) * D + (D / 2) * half + 8 * s))
-                             : f16x8{};
-
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kLdsBytes];
 
   const int64_t tok_stride = int64_t(num_kv_heads) * D;
@@ -211,14 +195,15 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
                      int64_t(blockIdx.x) * kWThreads + tid, int64_t(gridDim.x) * kWThreads);
 
   // Page ids: a tile of 32 keys spans two pages.  Lane l of a window holds page 2 * tile + (l & 1) of
-  // the wave's (l / 2)-th tile of that window (32 tiles), read with v_readlane.  The K and the V
-  // loads run one tile apart, each through its own window, so neither reloads a window twice.
+  // the wave's (l / 2)-th tile of that window (32 tiles), read with v_readlane.  A tile's K and V
+  // are requested in the same step, so one window serves both.
   const int seq_pages = int(ceil_div(total, kWBlock));
   struct Window {
     int ids, w;
   };
-  Window win_k{-1, -1}, win_v{-1, -1};
-  auto tile_pages = [&](Window& wn, int i, int& pa, int& pb) __attribute__((always_inline)) {
+  Window win_k{-1, -1};
+  // (uniform branch, taken once per 32 tiles)
+  auto ensure_window = [&](Window& wn, int i) __attribute__((always_inline)) {
     if ((i >> 5) != wn.w) {
       wn.w = i >> 5;
       const int pg = 2 * tile_of(32 * wn.w + lane / 2) + (lane & 1);
@@ -226,163 +211,194 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
       wn.ids = pg < seq_pages ? id : -1;
       asm volatile("" ::"v"(wn.ids));  // the window load completes here, not at every readlane
     }
+  };
+  // pages of tile i, whose window is loaded
+  auto tile_pages = [&](Window& wn, int i, int& pa, int& pb) __attribute__((always_inline)) {
     pa = __builtin_amdgcn_readlane(wn.ids, 2 * (i & 31));
     pb = __builtin_amdgcn_readlane(wn.ids, 2 * (i & 31) + 1);
   };
-  // Tile flags (uniform): bit 0/1 = first/second page valid, bit 2 = every key of the tile is
-  // visible to every row of the block (no mask, no zero fill).
-  auto tile_flags = [&](int i, int pa, int pb) __attribute__((always_inline)) -> int {
-    const int kt = tile_of(i) * kWTile;
+  // Tile flags (uniform): bit 0/1 = first/second page valid.
+  auto tile_flags = [&](int pa, int pb) __attribute__((always_inline)) -> int {
     const int oka = pa >= 0 && int64_t(pa) < num_pages, okb = pb >= 0 && int64_t(pb) < num_pages;
-    const int full = oka && okb && kt + kWTile <= total && kt + kWTile - 1 <= min_pos;
-    return oka | (okb << 1) | (full << 2);
+    return oka | (okb << 1);
   };
 
-  // Fused append: buffer resources over the chunk's rows (T rows; past them a load reads zero).
-  const int rsrc_bytes = kAppend ? T * int(tok_stride) * 2 : 0;
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_k), 0, rsrc_bytes, 0x00020000);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_v), 0, rsrc_bytes, 0x00020000);
-
-  // K: this lane's key row (col) of the tile, dims D/2 * half .. + D/2, as kKS 16-byte chunks.
-  // Returns the tile's flags.
-  auto load_k = [&](int i, u32x4 (&kr)[kKS]) __attribute__((always_inline)) -> int {
-    int pa, pb;
-    tile_pages(win_k, i, pa, pb);
-    const int fl = tile_flags(i, pa, pb);
-    const int kt = tile_of(i) * kWTile;
-    if constexpr (kAppend) {
-      if (kt >= query_start) {  // (uniform; query_start % 32 == 0) the tile's keys are chunk rows
-        // rows past the chunk's end read zero; tiles past the last are clamped to row T
-        const int row = min(kt - query_start, T) + col;
-        const int base = (row * int(tok_stride) + kvh * D + (D / 2) * half) * 2;
+  // The first page-id window is read before the queries, so the first K loads wait for it alone.
+  {
+    win_k.w = 0;
+    const int pg = 2 * tile_of(lane / 2) + (lane & 1);
+    const int id = table[min(pg, seq_pages - 1)];
+    win_k.ids = pg < seq_pages ? id : -1;
+  }
+  // Q^T as the B operand, K-step s = dims D/2 * half + 8 s .. + 7
+  f16x8 qreg[2][kKS];
 #pragma unroll
-        for (int s = 0; s < kKS; ++s)
-          kr[s] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rk, base + 16 * s, 0, 0));
-        return fl;
-      }
-    }
+  for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+    for (int s = 0; s < kKS; ++s)
+      qreg[rt][s] = q_ok[rt] ? as_h8(ld16(q + (int64_t(my_q[rt]) * hq + my_head[rt]) * D + (D / 2) * half + 8 * s))
+                             : f16x8{};
+  asm volatile("" ::"v"(win_k.ids));
+
+  // K: this lane's key row (col) of the tile, dims D/2 * half .. + D/2, as kKS 16-byte global
+  // loads (k_load).  A key that no row may see still reads a real row (page 0 for an invalid page;
+  // the chunk's last row past its end), whose scores the mask replaces.
+  auto k_tile = [&](int i, int pa, int pb, int fl) __attribute__((always_inline)) -> const f16* {
     const int page = col < kWBlock ? ((fl & 1) ? pa : 0) : ((fl & 2) ? pb : 0);
     const f16* src = head_pool + int64_t(page) * page_elems + (col % kWBlock) * tok_stride + (D / 2) * half;
-#pragma unroll
-    for (int s = 0; s < kKS; ++s) kr[s] = ld16(src + 8 * s);
-    return fl;
+    if constexpr (kAppend) {
+      // (uniform; query_start % 32 == 0) a tile at or past query_start holds the chunk's own rows
+      const int kt = tile_of(i) * kWTile;
+      const f16* own = ap.new_k + int64_t(min(kt - query_start + col, T - 1)) * tok_stride + kvh * D + (D / 2) * half;
+      src = kt >= query_start ? own : src;
+    }
+    return src;
   };
-  // V: DMA straight into one of the wave's two LDS tile buffers (buffer_load_dwordx4 ... lds, 64
-  // lanes x 16 bytes per instruction at consecutive LDS addresses).  Slot 64 n + lane of page half
-  // h is LDS row (slot / kRowSlots) of the half, 16-byte chunk (slot % kRowSlots); chunks past the
-  // row's D / 8 are padding.  Each half reads through a buffer resource that ends after the page's
-  // keys below the end of the sequence (none for an invalid page), so every other row, and the
-  // padding (offset past any resource), is written as zeros: masked keys contribute exactly nothing.
+
+  // V: 16-byte buffer loads into registers one step ahead (v_load), then 16-byte writes into one of
+  // the wave's two LDS tile buffers (v_store), lane l of load n of page half h to slot 64 n + l:
+  // LDS row r = slot / (D / 8) of the half at chunk position slot % (D / 8), which holds the row's
+  // chunk (slot % (D / 8)) ^ 2 (r % 4).  Each half reads through a buffer resource that ends after
+  // the page's keys below the end of the sequence (none for an invalid page; the chunk's rows for a
+  // tile of them), so every other row is zeros: masked keys contribute exactly nothing.
+  const int rsrc_bytes = kAppend ? T * int(tok_stride) * 2 : 0;
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_v), 0, rsrc_bytes, 0x00020000);
   uint32_t voff[C::kHalfInstr];
 #pragma unroll
   for (int n = 0; n < C::kHalfInstr; ++n) {
-    const int slot = n * kWave + lane, r = slot / C::kRowSlots, c = slot % C::kRowSlots;
-    voff[n] = r < 16 && c < D / 8 ? uint32_t((r * int(tok_stride) + 8 * c) * 2) : 0x7ffffff0u;
+    const int slot = n * kWave + lane, r = slot / C::kRowChunks;
+    const int c = (slot % C::kRowChunks) ^ (2 * (r % 4));
+    voff[n] = uint32_t((r * int(tok_stride) + 8 * c) * 2);
   }
-  __attribute__((address_space(3))) unsigned char* const vlds =
-      (__attribute__((address_space(3))) unsigned char*)(smem) + grp * C::kVBufs * C::kVBufBytes;
-  auto dma_v = [&](int i, int buf) __attribute__((always_inline)) {
-    int pa, pb;
-    tile_pages(win_v, i, pa, pb);
-    const int fl = tile_flags(i, pa, pb);
+  lds_u8* const vlds = (lds_u8*)(smem) + grp * C::kVBufs * C::kVBufBytes;
+  struct VTile {
+    __amdgpu_buffer_rsrc_t r[2];
+    uint32_t add[2];
+  };
+  auto v_tile = [&](int i, int pa, int pb, int fl) __attribute__((always_inline)) -> VTile {
     const int kt = tile_of(i) * kWTile;
-    __attribute__((address_space(3))) unsigned char* const dst = vlds + buf * C::kVBufBytes;
+    VTile t;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
-      __amdgpu_buffer_rsrc_t r;
-      uint32_t add = 0;
-      bool chunk_rows = false;
-      if constexpr (kAppend) chunk_rows = kt >= query_start;  // (uniform) the tile's keys are chunk rows
-      if (chunk_rows) {
-        r = rv;  // rows past the chunk's end read zero
-        add = uint32_t(((min(kt - query_start, T) + 16 * h) * int(tok_stride) + kvh * D) * 2);
-      } else {
-        // (page and key count are uniform; readfirstlane keeps the descriptor in scalar registers)
-        const bool ok = ((fl >> h) & 1) != 0;
-        const int page = __builtin_amdgcn_readfirstlane(ok ? (h == 0 ? pa : pb) : 0);
-        const int keys = __builtin_amdgcn_readfirstlane(ok ? min(max(total - (kt + 16 * h), 0), 16) : 0);
-        r = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(head_pool + v_off + int64_t(page) * page_elems), 0,
-                                              keys * int(tok_stride) * 2, 0x00020000);
+      // (page and key count are uniform; readfirstlane keeps the descriptor in scalar registers)
+      const bool ok = ((fl >> h) & 1) != 0;
+      const int page = __builtin_amdgcn_readfirstlane(ok ? (h == 0 ? pa : pb) : 0);
+      const int keys = __builtin_amdgcn_readfirstlane(ok ? min(max(total - (kt + 16 * h), 0), 16) : 0);
+      t.r[h] = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(head_pool + v_off + int64_t(page) * page_elems), 0,
+                                                 keys * int(tok_stride) * 2, 0x00020000);
+      t.add[h] = 0;
+      if constexpr (kAppend) {
+        if (kt >= query_start) {  // (uniform) the chunk's own rows; past its end they read zero
+          t.r[h] = rv;
+          t.add[h] = uint32_t(((min(kt - query_start, T) + 16 * h) * int(tok_stride) + kvh * D) * 2);
+        }
       }
-#pragma unroll
-      for (int n = 0; n < C::kHalfInstr; ++n)
-        dma16(r, dst + (h * C::kHalfSlots + n * kWave) * 16, voff[n] + add);
     }
+    return t;
+  };
+  // load j (of kVInstr) of a tile's V, and its LDS write into buffer dst
+  auto v_load = [&](const VTile& t, int j) __attribute__((always_inline)) {
+    const int h = j / C::kHalfInstr, n = j % C::kHalfInstr;
+    return buf_ld16(t.r[h], voff[n] + t.add[h]);
+  };
+  auto v_store = [&](lds_u8* dst, int j, u32x4 v) __attribute__((always_inline)) {
+    const int h = j / C::kHalfInstr, n = j % C::kHalfInstr;
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst + h * C::kHalfBytes + (n * kWave + lane) * 16) = v;
   };
 
-  // transposing V reads: lane = 16 g + 4 r + q reads key row 4 (lane / 32) + r of a page half,
-  // dims 16 (g % 2) + 4 q (halves)
-  const int tr_off = (4 * half + (lane % 16) / 4) * C::kVS + 16 * ((lane / 16) % 2) + 4 * (lane % 4);
+  // Transposing V reads: lane = 16 g + 4 rr + q reads key row R = 4 (lane / 32) + rr of a page half,
+  // dims 32 dt + 16 (g % 2) + 4 q .. + 3, i.e. logical chunk c = 4 dt + 2 (g % 2) + q / 2 at chunk
+  // position c ^ 2 rr = 4 (dt ^ (rr / 2)) + (2 (g % 2) + q / 2) ^ 2 (rr % 2).  The dt part is a
+  // constant offset of 64 dt bytes from one of two lane bases, for even and for odd dt.
+  int tr_even, tr_odd;
+  {
+    const int rr = (lane % 16) / 4, q4 = lane % 4, g2 = (lane / 16) % 2;
+    const int b2 = rr / 2;
+    const int low = (2 * g2 + q4 / 2) ^ (2 * (rr % 2));
+    const int base = (4 * half + rr) * 2 * D + 16 * low + 8 * (q4 % 2);
+    tr_even = base + 64 * b2;
+    tr_odd = base - 64 * b2;
+  }
 
   float m[2] = {kNegBig, kNegBig}, lsum[2] = {0.f, 0.f};
   f32x16 acc[kDT][2];
 #pragma unroll
   for (int dt = 0; dt < kDT; ++dt) acc[dt][0] = acc[dt][1] = f32x16{};
 
-  // Pipeline.  Iteration i turns tile i's scores (computed in the previous iteration) into
-  // probabilities while the matrix cores compute tile i + 1's scores: the S MFMAs of tile i + 1 are
-  // issued first and the softmax VALU work of tile i fills their execution (scheduling groups
-  // interleave them).  Then come the V DMA of tile i + 2 (into the buffer tile i - 1 used), the K
-  // loads of tile i + 2, and tile i's PV MFMAs.  VMEM instructions complete in order, so when the K
-  // loads of a tile are waited for, every V DMA issued before them has landed too; at most kVWait
-  // requests (a V DMA and a K load group) are outstanding when tile i's V is read.  Every request is
-  // unconditional (past the last tile they read page 0 or zeros), so these counts are exact.
+  // Addressing of a tile: this lane's K row, the V buffer resources, the page flags, and whether
+  // every key is visible to every row of the block (no mask needed).
+  struct TileInfo {
+    const f16* k;
+    VTile v;
+    int kt, fl;
+    bool full;
+  };
+  auto tile_info = [&](int t) __attribute__((always_inline)) -> TileInfo {
+    int pa, pb;
+    tile_pages(win_k, t, pa, pb);
+    TileInfo ti;
+    ti.fl = tile_flags(pa, pb);
+    ti.kt = tile_of(t) * kWTile;
+    ti.k = k_tile(t, pa, pb, ti.fl);
+    ti.v = v_tile(t, pa, pb, ti.fl);
+    ti.full = ti.fl == 3 && ti.kt + kWTile <= total && ti.kt + kWTile - 1 <= query_start + q0;
+    return ti;
+  };
+
+  // Pipeline.  Step i (one tile) is two scheduling regions:
+  //  A: tile i + 1's S MFMAs (its keys are in registers), each K fragment reloaded with tile
+  //     i + 2's keys right after its two MFMAs, and tile i's probabilities, fp16 packing and
+  //     partial row sums in the MFMAs' shadow;
+  //  B: tile i's PV MFMAs (V(i) from LDS through transposing reads), tile i + 1's V (loaded in the
+  //     previous step) written to the LDS buffer tile i - 1 used, and tile i + 2's V loads between
+  //     them.
+  // Then tile i + 1's mask (when some key of it is hidden from some row) and row maxima.  The lazy
+  // rescale for tile i + 1 opens the next step.  Every request is unconditional (past the last
+  // tile they read page 0 or zeros).
   u32x4 kr[kKS];
-  dma_v(0, 0);
-  dma_v(1, 1);
-  int kfl = load_k(0, kr);
-  auto s_mfma = [&](f32x16 (&st)[2]) __attribute__((always_inline)) {  // S^T of both row tiles
-    st[0] = f32x16{};
-    st[1] = f32x16{};
+  u32x4 vst[C::kVInstr];  // the next tile's V, in flight to LDS
+  auto s_mfma_step = [&](f32x16 (&st)[2], int s) __attribute__((always_inline)) {  // S^T, K-step s
+    const f16x8 kf = as_h8(kr[s]);
+    st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[0][s], s == 0 ? f32x16{} : st[0], 0, 0, 0);
+    st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[1][s], s == 0 ? f32x16{} : st[1], 0, 0, 0);
+  };
+  // Causal mask, end of sequence and invalid pages (scores -> -inf): key kk of the tile is visible
+  // to this lane's row iff kk <= lim and its page is valid; the lane's score r is key
+  // 8 (r / 4) + 4 half + r % 4.
+  auto mask = [&](f32x16 (&st)[2], const TileInfo& ti) __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < kKS; ++s) {
-      const f16x8 kf = as_h8(kr[s]);
-      st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[0][s], st[0], 0, 0, 0);
-      st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[1][s], st[1], 0, 0, 0);
+    for (int rt = 0; rt < 2; ++rt) {
+      const int lim = min(my_pos[rt], total - 1) - ti.kt;
+      const int la = ((ti.fl & 1) ? lim : -1) - 4 * half;
+      const int lb = ((ti.fl & 2) ? lim : kWBlock - 1) - 4 * half;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int c = 8 * (r / 4) + (r % 4);
+        st[rt][r] = c <= (r < 8 ? la : lb) ? st[rt][r] : -INFINITY;
+      }
     }
   };
-  f32x16 st[2];
-  s_mfma(st);  // tile 0
-  int sfl = kfl;
-  kfl = load_k(1, kr);
-
-  for (int i = 0; i < iters; ++i) {
-    const int fl = sfl;
-    const int kt = tile_of(i) * kWTile;
-    const int buf = i % C::kVBufs;
-    float sv[2][16];
-#pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) sv[rt][r] = st[rt][r];
-    // online softmax of tile i.  Causal mask, end of sequence, invalid pages:
-    if (!(fl & 4)) {
-      const bool oka = (fl & 1) != 0, okb = (fl & 2) != 0;
-#pragma unroll
-      for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int kk = 8 * (r / 4) + 4 * half + (r % 4);
-          const bool ok = (kk >= kWBlock ? okb : oka) & (kt + kk <= my_pos[rt]) & (kt + kk < total);
-          sv[rt][r] = ok ? sv[rt][r] : -INFINITY;
-        }
-    }
-    // Row maxima (a tree, then the lane ^ 32 partner's) and the lazy rescale: the reference maximum
-    // moves only when a score exceeds it by more than kSlack (log2 units), so P = 2^(s - m) <
-    // 2^kSlack; acc and lsum stay relative to m.
-    constexpr float kSlack = 8.f;
+  // Each row's maximum over the tile and the lane ^ 32 partner (log2 units)
+  float cand[2];
+  auto row_max = [&](const f32x16 (&st)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float mq[4];
 #pragma unroll
       for (int a = 0; a < 4; ++a)
-        mq[a] = fmaxf(fmaxf(sv[rt][4 * a], sv[rt][4 * a + 1]), fmaxf(sv[rt][4 * a + 2], sv[rt][4 * a + 3]));
-      float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float cand = mx * scale_log2;
-      const bool grow = cand > m[rt] + kSlack;
-      if (__builtin_expect(__builtin_amdgcn_ballot_w64(grow) != 0, 0)) {  // rare after the first tile
-        const float mn = grow ? cand : m[rt];
+        mq[a] = fmaxf(fmaxf(st[rt][4 * a], st[rt][4 * a + 1]), fmaxf(st[rt][4 * a + 2], st[rt][4 * a + 3]));
+      cand[rt] = max_lane32(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]))) * scale_log2;
+    }
+  };
+  // Lazy rescale: the reference maximum moves only when a score exceeds it by more than kSlack
+  // (log2 units), so P = 2^(s - m) < 2^kSlack; acc and lsum stay relative to m.
+  auto rescale = [&]() __attribute__((always_inline)) {
+    constexpr float kSlack = 8.f;
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt) {
+      const bool grow = cand[rt] > m[rt] + kSlack;
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // rare after the first tile
+        const float mn = grow ? cand[rt] : m[rt];
         const float alpha = exp2_fast(m[rt] - mn);
         lsum[rt] *= alpha;
 #pragma unroll
@@ -390,61 +406,82 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
         m[rt] = mn;
       }
     }
-    __builtin_amdgcn_sched_barrier(0);
-    // One scheduling region: tile i + 1's S MFMAs (issued first; they read K(i + 1), loaded one
-    // iteration ago) and tile i's exponentials, row sums and fp16 packing, interleaved one MFMA to
-    // a group of VALU instructions.  (Past the last tile the MFMAs multiply a zero or page-0 tile,
-    // never used.)
-    s_mfma(st);
-    sfl = kfl;
-    f16x8 pb16[2][2];
+  };
+  // P of a tile in fp16 (the B operands of its PV MFMAs) and this lane's partial row sums of the
+  // fp16 values (the ones the PV MFMAs multiply)
+  auto numerators = [&](const f32x16 (&sc)[2], f16x8 (&pb16)[2][2], float (&ps)[2]) __attribute__((always_inline)) {
 #pragma unroll
     for (int rt = 0; rt < 2; ++rt) {
       float pv[16];
 #pragma unroll
-      for (int r = 0; r < 16; ++r) pv[r] = exp2_fast(fmaf(sv[rt][r], scale_log2, -m[rt]));
-      // row sum: four partial sums, each in key order
-      float ps[4];
-#pragma unroll
-      for (int a = 0; a < 4; ++a) ps[a] = (pv[4 * a] + pv[4 * a + 1]) + (pv[4 * a + 2] + pv[4 * a + 3]);
-      lsum[rt] += (ps[0] + ps[1]) + (ps[2] + ps[3]);
+      for (int r = 0; r < 16; ++r) pv[r] = exp2_fast(fmaf(sc[rt][r], scale_log2, -m[rt]));
       pb16[rt][0] = f16x8{f16(pv[0]), f16(pv[1]), f16(pv[2]), f16(pv[3]), f16(pv[4]), f16(pv[5]), f16(pv[6]),
                           f16(pv[7])};
       pb16[rt][1] = f16x8{f16(pv[8]), f16(pv[9]), f16(pv[10]), f16(pv[11]), f16(pv[12]), f16(pv[13]),
                           f16(pv[14]), f16(pv[15])};
+      const f16x2 one = f16x2{f16(1.f), f16(1.f)};
+      float s = 0.f;
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          s = __builtin_amdgcn_fdot2(f16x2{pb16[rt][u][2 * e], pb16[rt][u][2 * e + 1]}, one, s, false);
+      ps[rt] = s;
     }
+  };
+  // VALU instructions per MFMA in region A: ~100 for a tile's probabilities over 2 kKS MFMAs
+  constexpr int kAValu = (100 + 2 * kKS - 1) / (2 * kKS);
+  TileInfo ti1;  // tile i + 1
+  auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], int i) __attribute__((always_inline)) {
+    rescale();  // for tile i, whose maxima were taken in the previous step
+    ensure_window(win_k, i + 2);
+    const TileInfo ti2 = tile_info(i + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    // region A
+    const f16* const k2 = ti2.k;
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) {
+      s_mfma_step(sn, s);
+      kr[s] = ld16(k2 + 8 * s);
+    }
+    f16x8 pb16[2][2];
+    float ps[2];
+    numerators(sc, pb16, ps);
     // (the probabilities are pinned here, so the exponentials are not sunk to their use in the PV
     // MFMAs below, out of the MFMAs' shadow)
     pin_regs(pb16[0][0], pb16[0][1], pb16[1][0], pb16[1][1]);
 #pragma unroll
-    for (int k = 0; k < 2 * kKS; ++k) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // one MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 6, 0);  // six VALU
+    for (int s = 0; s < kKS; ++s) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, kAValu, 0);  // VALU
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);       // K load
+      __builtin_amdgcn_sched_group_barrier(0x002, kAValu, 0);  // VALU
     }
     __builtin_amdgcn_sched_barrier(0);
-    // the buffer of tile i - 1 takes tile i + 2 once tile i - 1's reads have completed (DMA writes
-    // reach LDS outside the wave's LDS instruction order); then tile i + 2's keys
-    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    dma_v(i + 2, (i + 2) % C::kVBufs);
-    kfl = load_k(i + 2, kr);
-    // tile i's V DMA has landed once at most kVWait later VMEM instructions are outstanding
-    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(C::kVWait) : "memory");
-    // O^T += V^T . P^T: each V^T fragment feeds both row tiles.  A = V^T for dims 32 dt + col, keys
-    // 16 u + 4 half + 0..3 and 16 u + 8 + 4 half + 0..3 (page half u).
-    const f16* vt = reinterpret_cast<const f16*>(smem + (grp * C::kVBufs + buf) * C::kVBufBytes);
-    // two dim tiles per batch: 8 reads in flight, one wait, 8 MFMAs
-#pragma unroll
-    for (int d0 = 0; d0 < kDT; d0 += 2) {
+    lsum[0] += ps[0];
+    lsum[1] += ps[1];
+    // region B
+    const lds_u8* const vcur = vlds + (i % C::kVBufs) * C::kVBufBytes;
+    const lds_u8* const ae = vcur + tr_even;
+    const lds_u8* const ao = vcur + tr_odd;
+    lds_u8* const vnext = vlds + ((i + 1) % C::kVBufs) * C::kVBufBytes;
+    const VTile v2 = ti2.v;
+    // O^T += V^T . P^T, two dim tiles per batch (8 reads, 8 MFMAs).  A = V^T for dims 32 dt + col,
+    // keys 16 u + 4 half + 0..3 and 16 u + 8 + 4 half + 0..3 (page half u).  Tile i + 1's V goes to
+    // LDS (first batch) and tile i + 2's is loaded (last batch) between the MFMAs.
+    auto batch = [&](auto bc) __attribute__((always_inline)) {
+      constexpr int b = decltype(bc)::value;
+      constexpr int d0 = 2 * b, HB = C::kHalfBytes, HI = 16 * D;
       u32x2 rd[8];
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const f16* vp = vt + u * C::kHalfSlots * 8 + tr_off + 32 * (d0 + j);
-          rd[4 * j + 2 * u] = ds_read_tr16(vp);
-          rd[4 * j + 2 * u + 1] = ds_read_tr16(vp + 8 * C::kVS);
-        }
-      wait_lds(rd);
+      rd[0] = ds_read_tr16(ae + 64 * d0);
+      rd[1] = ds_read_tr16(ae + 64 * d0 + HI);
+      rd[2] = ds_read_tr16(ae + HB + 64 * d0);
+      rd[3] = ds_read_tr16(ae + HB + 64 * d0 + HI);
+      rd[4] = ds_read_tr16(ao + 64 * (d0 + 1));
+      rd[5] = ds_read_tr16(ao + 64 * (d0 + 1) + HI);
+      rd[6] = ds_read_tr16(ao + HB + 64 * (d0 + 1));
+      rd[7] = ds_read_tr16(ao + HB + 64 * (d0 + 1) + HI);
 #pragma unroll
       for (int j = 0; j < 2; ++j)
 #pragma unroll
@@ -454,11 +491,58 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
           const f16x8 vf = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           acc[d0 + j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[0][u], acc[d0 + j][0], 0, 0, 0);
           acc[d0 + j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[1][u], acc[d0 + j][1], 0, 0, 0);
+          const int pr = 2 * j + u;  // MFMA pair 0..3 of the batch
+          if constexpr (kDT == 4) {
+            if constexpr (b == 0) {
+              v_store(vnext, 2 * pr, vst[2 * pr]);
+              v_store(vnext, 2 * pr + 1, vst[2 * pr + 1]);
+            } else {
+              vst[2 * pr] = v_load(v2, 2 * pr);
+              vst[2 * pr + 1] = v_load(v2, 2 * pr + 1);
+            }
+          } else {
+            v_store(vnext, pr, vst[pr]);
+            vst[pr] = v_load(v2, pr);
+          }
         }
-    }
+    };
+    static_assert(C::kVInstr == 2 * kDT, "one V load per MFMA pair over the batches");
+    batch(std::integral_constant<int, 0>{});
+    if constexpr (kDT == 4) batch(std::integral_constant<int, 1>{});
+    __builtin_amdgcn_sched_barrier(0);
+    if (!ti1.full) mask(sn, ti1);
+    row_max(sn);
+    ti1 = ti2;
+  };
+
+  // prologue: K(0) and V(0) loads, S(0), K(1) loads, V(0) to LDS, V(1) loads; tile 0's mask
+  f32x16 sa[2], sb[2];
+  {
+    const TileInfo ti0 = tile_info(0);
+    ti1 = tile_info(1);
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti0.k + 8 * s);
+#pragma unroll
+    for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(ti0.v, j);
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) s_mfma_step(sa, s);
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti1.k + 8 * s);
+#pragma unroll
+    for (int j = 0; j < C::kVInstr; ++j) v_store(vlds, j, vst[j]);
+#pragma unroll
+    for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(ti1.v, j);
+    if (!ti0.full) mask(sa, ti0);
+    row_max(sa);
   }
-  // Outstanding DMAs (tiles past the last) land before the LDS is reused for the merge.
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  int i = 0;
+  for (; i + 1 < iters; i += 2) {
+    step(sa, sb, i);
+    step(sb, sa, i + 1);
+  }
+  if (i < iters) step(sa, sb, i);
+
+  // every wave's V reads are done before the LDS is reused for the merge
   __syncthreads();
 
   float lt[2];
