@@ -230,6 +230,9 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     const int id = table[min(pg, seq_pages - 1)];
     win_k.ids = pg < seq_pages ? id : -1;
   }
+  // The window arrives before the queries are requested; they and the first tiles' K and V are then
+  // in flight together.
+  asm volatile("" ::"v"(win_k.ids) : "memory");
   // Q^T as the B operand, K-step s = dims D/2 * half + 8 s .. + 7
   f16x8 qreg[2][kKS];
 #pragma unroll
@@ -238,7 +241,6 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     for (int s = 0; s < kKS; ++s)
       qreg[rt][s] = q_ok[rt] ? as_h8(ld16(q + (int64_t(my_q[rt]) * hq + my_head[rt]) * D + (D / 2) * half + 8 * s))
                              : f16x8{};
-  asm volatile("" ::"v"(win_k.ids));
 
   // K: this lane's key row (col) of the tile, dims D/2 * half .. + D/2, as kKS 16-byte global
   // loads (k_load).  A key that no row may see still reads a real row (page 0 for an invalid page;
@@ -630,12 +632,20 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     if (s_ticket != uint32_t(nsplit - 1)) return;
     compiler_fence();  // the merge loads below stay behind the ticket
     float mx = kNegBig;
-    for (int s2 = 0; s2 < nsplit; ++s2) mx = fmaxf(mx, ld_dev2(r_ml, uint32_t((pair * nsplit + s2) * kWRows * 8) + ml_row)[0]);
-    lfin = 0.f;
+    // (this split's own partial is taken from registers, not read back)
+    const float m_own = mfin, l_own = lfin;
+    f32x4 mine[C::kOwned][4];
 #pragma unroll
     for (int ob = 0; ob < C::kOwned; ++ob)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) o[ob][r4] = f32x4{0.f, 0.f, 0.f, 0.f};
+      for (int r4 = 0; r4 < 4; ++r4) {
+        mine[ob][r4] = o[ob][r4];
+        o[ob][r4] = f32x4{0.f, 0.f, 0.f, 0.f};
+      }
+    mx = m_own;
+    for (int s2 = 0; s2 < nsplit; ++s2)
+      if (s2 != split) mx = fmaxf(mx, ld_dev2(r_ml, uint32_t((pair * nsplit + s2) * kWRows * 8) + ml_row)[0]);
+    lfin = 0.f;
     // splits in batches of kSplitBatch, every load of a batch in flight at once
     constexpr int kSplitBatch = 4;
     for (int s0 = 0; s0 < nsplit; s0 += kSplitBatch) {
@@ -644,12 +654,19 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
         const int s2 = s0 + sb;
         if (s2 < nsplit) {
           const int64_t sl = pair * nsplit + s2;
-          const f32x2 ml = ld_dev2(r_ml, uint32_t(sl * kWRows * 8) + ml_row);
+          f32x2 ml = f32x2{m_own, l_own};
           f32x4 x[C::kOwned][4];
 #pragma unroll
           for (int ob = 0; ob < C::kOwned; ++ob)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) x[ob][r4] = ld_dev4(r_o, o_off(sl, grp + kWGroups * ob, r4));
+            for (int r4 = 0; r4 < 4; ++r4) x[ob][r4] = mine[ob][r4];
+          if (s2 != split) {  // (uniform)
+            ml = ld_dev2(r_ml, uint32_t(sl * kWRows * 8) + ml_row);
+#pragma unroll
+            for (int ob = 0; ob < C::kOwned; ++ob)
+#pragma unroll
+              for (int r4 = 0; r4 < 4; ++r4) x[ob][r4] = ld_dev4(r_o, o_off(sl, grp + kWGroups * ob, r4));
+          }
           const float wsp = exp2_fast(ml[0] - mx);
           lfin = fmaf(wsp, ml[1], lfin);
 #pragma unroll
