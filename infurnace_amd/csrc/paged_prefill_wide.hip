@@ -56,12 +56,16 @@ struct WideCfg {
   static constexpr int kVInstr = 2 * kHalfInstr;     // 16-byte loads (and LDS writes) per lane per tile
   static constexpr int kVBufs = 2;                   // V tiles in LDS per wave: i and i + 1
   static constexpr int kTileBytes = kWGroups * kVBufs * kVBufBytes;
+  // The queries, staged once per workgroup: 64 rows x D dims, chunk c of row r at c ^ (r % 8).
+  static constexpr int kQBytes = kWRows * D * 2;
+  static constexpr int kQInstr = kQBytes / 16 / kWThreads;  // 16-byte loads per lane
   static constexpr int kMlFloats = kWGroups * 2 * 32 * 2;
   static constexpr int kMergeBytes = kMlFloats * 4 + kWGroups * kBlocks * 16 * kWave * 4;
-  static constexpr int kLdsBytes = kTileBytes > kMergeBytes ? kTileBytes : kMergeBytes;
+  static constexpr int kLdsBytes = kTileBytes + kQBytes > kMergeBytes ? kTileBytes + kQBytes : kMergeBytes;
   static_assert(kQw * G == kWRows, "64 rows per workgroup");
   static_assert(kBlocks % kWGroups == 0, "every wave finishes the same number of blocks");
   static_assert(16 * kRowChunks % kWave == 0 && kRowChunks >= 8, "whole loads per page half; swizzle in range");
+  static_assert(kQBytes % (16 * kWThreads) == 0 && 16 * kRowChunks * kWGroups == kWRows * kRowChunks, "Q staging");
 };
 
 struct WidePlan {
@@ -138,6 +142,14 @@ __device__ __forceinline__ float max_lane32(float x) {
   return x;
 #endif
 }
+// No instruction: the value is held in accumulation registers from here on (the queries, read
+// only as MFMA operands, which take them from there without copies).
+__device__ __forceinline__ void pin_agpr(f16x8& a) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("" : "+a"(a));
+#endif
+}
+
 // No instruction: the values must exist at this point (and the scheduler treats it as a boundary).
 __device__ __forceinline__ void pin_regs(f16x8& a, f16x8& b, f16x8& c, f16x8& d) {
 #if defined(__HIP_DEVICE_COMPILE__)
@@ -230,17 +242,20 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     const int id = table[min(pg, seq_pages - 1)];
     win_k.ids = pg < seq_pages ? id : -1;
   }
-  // The window arrives before the queries are requested; they and the first tiles' K and V are then
-  // in flight together.
+  // The workgroup's queries, each row read once: wave grp loads rows 16 grp .. + 15 (a row past the
+  // chunk as zeros), for the LDS staging below.
+  lds_u8* const qlds = (lds_u8*)(smem) + C::kTileBytes;
+  u32x4 qst[C::kQInstr];
+#pragma unroll
+  for (int n = 0; n < C::kQInstr; ++n) {
+    const int slot = n * kWave + lane, rho = 16 * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
+    const int qi = q0 + rho % kQw;
+    const u32x4 v = ld16(q + (int64_t(min(qi, T - 1)) * hq + kvh * G + rho / kQw) * D + 8 * c);
+    qst[n] = qi < T ? v : u32x4{0u, 0u, 0u, 0u};
+  }
+  // The window arrives before the first tiles' K and V are requested.
   asm volatile("" ::"v"(win_k.ids) : "memory");
-  // Q^T as the B operand, K-step s = dims D/2 * half + 8 s .. + 7
-  f16x8 qreg[2][kKS];
-#pragma unroll
-  for (int rt = 0; rt < 2; ++rt)
-#pragma unroll
-    for (int s = 0; s < kKS; ++s)
-      qreg[rt][s] = q_ok[rt] ? as_h8(ld16(q + (int64_t(my_q[rt]) * hq + my_head[rt]) * D + (D / 2) * half + 8 * s))
-                             : f16x8{};
+  f16x8 qreg[2][kKS];  // Q^T (filled from LDS in the prologue)
 
   // K: this lane's key row (col) of the tile, dims D/2 * half .. + D/2, as kKS 16-byte global
   // loads (k_load).  A key that no row may see still reads a real row (page 0 for an invalid page;
@@ -526,6 +541,26 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti0.k + 8 * s);
 #pragma unroll
     for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(ti0.v, j);
+    // Q through LDS: Q^T as the B operand, K-step s = dims D/2 * half + 8 s .. + 7 of row 32 rt + col
+#pragma unroll
+    for (int n = 0; n < C::kQInstr; ++n) {
+      const int slot = n * kWave + lane, rho = 16 * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
+      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((c ^ (rho % 8)) * 16)) = qst[n];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+      for (int s = 0; s < kKS; ++s) {
+        const int rho = 32 * rt + col, c = (D / 16) * half + s;
+        qreg[rt][s] = as_h8(*reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((c ^ (rho % 8)) * 16)));
+        pin_agpr(qreg[rt][s]);
+      }
+    // The barrier above leaves the 4 waves in step; started in step they would reach their load
+    // and their MFMA phases together for the whole loop and queue on the CU's shared memory path.
+    // Wave grp starts 6 x 64 x grp cycles late instead (a quarter of a step or so apart; measured:
+    // 71.9 -> 67.4 us per config-3 layer).
+    for (int w = 0; w < grp; ++w) __builtin_amdgcn_s_sleep(6);
 #pragma unroll
     for (int s = 0; s < kKS; ++s) s_mfma_step(sa, s);
 #pragma unroll
