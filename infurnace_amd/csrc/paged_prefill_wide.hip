@@ -13,8 +13,8 @@
 //    tiles and the last to finish merges their partials through the workspace.
 //  * Scores, transposed: S^T = K . Q^T with v_mfma_f32_32x32x16_f16.  The A operand (32 keys x 16
 //    dims) is one key row per lane, loaded straight from the pool into registers: MFMA K-step s
-//    takes dims D/2 * half + 8 s .. + 7, a permutation of the head dims applied to both operands,
-//    so a lane's K-steps read 128 contiguous bytes of its key row.  The B operand (the queries) is
+//    takes dims 16 s + 8 half .. + 7, a permutation of the head dims applied to both operands, so
+//    the two lanes of a key row read 32 contiguous bytes per load.  The B operand (the queries) is
 //    held for the whole kernel.  Each K fragment feeds both row tiles.
 //  * O^T += V^T . P^T: the probabilities stay in registers (a lane's 16 scores of a 32-key tile are
 //    the B operands of two K = 16 steps); V goes through registers to the wave's own LDS tile as it
@@ -257,16 +257,16 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   asm volatile("" ::"v"(win_k.ids) : "memory");
   f16x8 qreg[2][kKS];  // Q^T (filled from LDS in the prologue)
 
-  // K: this lane's key row (col) of the tile, dims D/2 * half .. + D/2, as kKS 16-byte global
+  // K: this lane's key row (col) of the tile, dims 16 s + 8 half .. + 7 for K-step s, as kKS 16-byte global
   // loads (k_load).  A key that no row may see still reads a real row (page 0 for an invalid page;
   // the chunk's last row past its end), whose scores the mask replaces.
   auto k_tile = [&](int i, int pa, int pb, int fl) __attribute__((always_inline)) -> const f16* {
     const int page = col < kWBlock ? ((fl & 1) ? pa : 0) : ((fl & 2) ? pb : 0);
-    const f16* src = head_pool + int64_t(page) * page_elems + (col % kWBlock) * tok_stride + (D / 2) * half;
+    const f16* src = head_pool + int64_t(page) * page_elems + (col % kWBlock) * tok_stride + 8 * half;
     if constexpr (kAppend) {
       // (uniform; query_start % 32 == 0) a tile at or past query_start holds the chunk's own rows
       const int kt = tile_of(i) * kWTile;
-      const f16* own = ap.new_k + int64_t(min(kt - query_start + col, T - 1)) * tok_stride + kvh * D + (D / 2) * half;
+      const f16* own = ap.new_k + int64_t(min(kt - query_start + col, T - 1)) * tok_stride + kvh * D + 8 * half;
       src = kt >= query_start ? own : src;
     }
     return src;
@@ -459,7 +459,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
 #pragma unroll
     for (int s = 0; s < kKS; ++s) {
       s_mfma_step(sn, s);
-      kr[s] = ld16(k2 + 8 * s);
+      kr[s] = ld16(k2 + 16 * s);
     }
     f16x8 pb16[2][2];
     float ps[2];
@@ -538,10 +538,10 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     const TileInfo ti0 = tile_info(0);
     ti1 = tile_info(1);
 #pragma unroll
-    for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti0.k + 8 * s);
+    for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti0.k + 16 * s);
 #pragma unroll
     for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(ti0.v, j);
-    // Q through LDS: Q^T as the B operand, K-step s = dims D/2 * half + 8 s .. + 7 of row 32 rt + col
+    // Q through LDS: Q^T as the B operand, K-step s = dims 16 s + 8 half .. + 7 of row 32 rt + col
 #pragma unroll
     for (int n = 0; n < C::kQInstr; ++n) {
       const int slot = n * kWave + lane, rho = 16 * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
@@ -552,7 +552,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     for (int rt = 0; rt < 2; ++rt)
 #pragma unroll
       for (int s = 0; s < kKS; ++s) {
-        const int rho = 32 * rt + col, c = (D / 16) * half + s;
+        const int rho = 32 * rt + col, c = 2 * s + half;
         qreg[rt][s] = as_h8(*reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((c ^ (rho % 8)) * 16)));
         pin_agpr(qreg[rt][s]);
       }
@@ -564,7 +564,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
 #pragma unroll
     for (int s = 0; s < kKS; ++s) s_mfma_step(sa, s);
 #pragma unroll
-    for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti1.k + 8 * s);
+    for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti1.k + 16 * s);
 #pragma unroll
     for (int j = 0; j < C::kVInstr; ++j) v_store(vlds, j, vst[j]);
 #pragma unroll
