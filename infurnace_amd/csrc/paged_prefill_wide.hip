@@ -98,14 +98,14 @@ static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hk
 __device__ __forceinline__ void wide_store_chunk(f16* __restrict__ pool, int64_t num_pages,
                                                  const int32_t* __restrict__ table, int32_t query_start, int32_t T,
                                                  int32_t hkv, int32_t d, const f16* __restrict__ new_k,
-                                                 const f16* __restrict__ new_v, int64_t first, int64_t step) {
+                                                 const f16* __restrict__ new_v, int first, int step) {
   const int chunks = hkv * d / 8;
   const int64_t tok_stride = int64_t(hkv) * d;
-  const int64_t items = int64_t(T) * 2 * chunks;
-  for (int64_t it = first; it < items; it += step) {
-    const int t = int(it / (2 * chunks));
-    const int rem = int(it % (2 * chunks));
-    const int kv = rem / chunks, c = rem % chunks;
+  const int items = T * 2 * chunks;  // (< 2^31: checked at launch)
+  for (int it = first; it < items; it += step) {
+    const int t = it / (2 * chunks);
+    const int rem = it - t * 2 * chunks;
+    const int kv = rem >= chunks, c = rem - kv * chunks;
     const int pos = query_start + t;
     const int page = table[pos / kWBlock];
     if (page < 0 || int64_t(page) >= num_pages) continue;
@@ -204,7 +204,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
 
   if constexpr (kAppend)
     wide_store_chunk(ap.pool, num_pages, table, query_start, T, num_kv_heads, D, ap.new_k, ap.new_v,
-                     int64_t(blockIdx.x) * kWThreads + tid, int64_t(gridDim.x) * kWThreads);
+                     int(blockIdx.x) * kWThreads + tid, int(gridDim.x) * kWThreads);
 
   // Page ids: a tile of 32 keys spans two pages.  Lane l of a window holds page 2 * tile + (l & 1) of
   // the wave's (l / 2)-th tile of that window (32 tiles), read with v_readlane.  A tile's K and V
@@ -760,6 +760,8 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   const WidePlan p = plan_wide(T, query_start, hq, hkv, d, cus);
   if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
+  // (the fused append indexes the chunk's K and V rows with 32-bit byte offsets)
+  if (ap.pool != nullptr && int64_t(T) * hkv * d * 2 >= int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
   PrefillWorkspace ws{nullptr, nullptr, nullptr};
   if (p.nsplit > 1) {
     if (workspace == nullptr || workspace_bytes < p.bytes) return IFN_ERR_WORKSPACE;
