@@ -446,6 +446,34 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
       ps[rt] = s;
     }
   };
+  // PV batch b of a tile: O^T += V^T . P^T for dim tiles 2 b and 2 b + 1 (8 transposing reads, 8
+  // MFMAs).  A = V^T for dims 32 dt + col, keys 16 u + 4 half + 0..3 and 16 u + 8 + 4 half + 0..3
+  // (page half u).  after(pr) runs after MFMA pair pr (0..3) of the batch.
+  auto pv_batch = [&](auto bc, const lds_u8* ae, const lds_u8* ao, const f16x8 (&pb16)[2][2], auto&& after)
+      __attribute__((always_inline)) {
+    constexpr int b = decltype(bc)::value;
+    constexpr int d0 = 2 * b, HB = C::kHalfBytes, HI = 16 * D;
+    u32x2 rd[8];
+    rd[0] = ds_read_tr16(ae + 64 * d0);
+    rd[1] = ds_read_tr16(ae + 64 * d0 + HI);
+    rd[2] = ds_read_tr16(ae + HB + 64 * d0);
+    rd[3] = ds_read_tr16(ae + HB + 64 * d0 + HI);
+    rd[4] = ds_read_tr16(ao + 64 * (d0 + 1));
+    rd[5] = ds_read_tr16(ao + 64 * (d0 + 1) + HI);
+    rd[6] = ds_read_tr16(ao + HB + 64 * (d0 + 1));
+    rd[7] = ds_read_tr16(ao + HB + 64 * (d0 + 1) + HI);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        const f16x4 lo = __builtin_bit_cast(f16x4, rd[4 * j + 2 * u]);
+        const f16x4 hi = __builtin_bit_cast(f16x4, rd[4 * j + 2 * u + 1]);
+        const f16x8 vf = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc[d0 + j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[0][u], acc[d0 + j][0], 0, 0, 0);
+        acc[d0 + j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[1][u], acc[d0 + j][1], 0, 0, 0);
+        after(2 * j + u);
+      }
+  };
   // VALU instructions per MFMA in region A: ~100 for a tile's probabilities over 2 kKS MFMAs
   constexpr int kAValu = (100 + 2 * kKS - 1) / (2 * kKS);
   TileInfo ti1;  // tile i + 1
@@ -484,44 +512,24 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     const lds_u8* const ao = vcur + tr_odd;
     lds_u8* const vnext = vlds + ((i + 1) % C::kVBufs) * C::kVBufBytes;
     const VTile v2 = ti2.v;
-    // O^T += V^T . P^T, two dim tiles per batch (8 reads, 8 MFMAs).  A = V^T for dims 32 dt + col,
-    // keys 16 u + 4 half + 0..3 and 16 u + 8 + 4 half + 0..3 (page half u).  Tile i + 1's V goes to
-    // LDS (first batch) and tile i + 2's is loaded (last batch) between the MFMAs.
+    // Tile i's PV MFMAs; tile i + 1's V goes to LDS (first batch) and tile i + 2's is loaded (last
+    // batch) between them.
     auto batch = [&](auto bc) __attribute__((always_inline)) {
       constexpr int b = decltype(bc)::value;
-      constexpr int d0 = 2 * b, HB = C::kHalfBytes, HI = 16 * D;
-      u32x2 rd[8];
-      rd[0] = ds_read_tr16(ae + 64 * d0);
-      rd[1] = ds_read_tr16(ae + 64 * d0 + HI);
-      rd[2] = ds_read_tr16(ae + HB + 64 * d0);
-      rd[3] = ds_read_tr16(ae + HB + 64 * d0 + HI);
-      rd[4] = ds_read_tr16(ao + 64 * (d0 + 1));
-      rd[5] = ds_read_tr16(ao + 64 * (d0 + 1) + HI);
-      rd[6] = ds_read_tr16(ao + HB + 64 * (d0 + 1));
-      rd[7] = ds_read_tr16(ao + HB + 64 * (d0 + 1) + HI);
-#pragma unroll
-      for (int j = 0; j < 2; ++j)
-#pragma unroll
-        for (int u = 0; u < 2; ++u) {
-          const f16x4 lo = __builtin_bit_cast(f16x4, rd[4 * j + 2 * u]);
-          const f16x4 hi = __builtin_bit_cast(f16x4, rd[4 * j + 2 * u + 1]);
-          const f16x8 vf = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          acc[d0 + j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[0][u], acc[d0 + j][0], 0, 0, 0);
-          acc[d0 + j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[1][u], acc[d0 + j][1], 0, 0, 0);
-          const int pr = 2 * j + u;  // MFMA pair 0..3 of the batch
-          if constexpr (kDT == 4) {
-            if constexpr (b == 0) {
-              v_store(vnext, 2 * pr, vst[2 * pr]);
-              v_store(vnext, 2 * pr + 1, vst[2 * pr + 1]);
-            } else {
-              vst[2 * pr] = v_load(v2, 2 * pr);
-              vst[2 * pr + 1] = v_load(v2, 2 * pr + 1);
-            }
+      pv_batch(bc, ae, ao, pb16, [&](const int pr) __attribute__((always_inline)) {
+        if constexpr (kDT == 4) {
+          if constexpr (b == 0) {
+            v_store(vnext, 2 * pr, vst[2 * pr]);
+            v_store(vnext, 2 * pr + 1, vst[2 * pr + 1]);
           } else {
-            v_store(vnext, pr, vst[pr]);
-            vst[pr] = v_load(v2, pr);
+            vst[2 * pr] = v_load(v2, 2 * pr);
+            vst[2 * pr + 1] = v_load(v2, 2 * pr + 1);
           }
+        } else {
+          v_store(vnext, pr, vst[pr]);
+          vst[pr] = v_load(v2, pr);
         }
+      });
     };
     static_assert(C::kVInstr == 2 * kDT, "one V load per MFMA pair over the batches");
     batch(std::integral_constant<int, 0>{});
@@ -530,6 +538,19 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     if (!ti1.full) mask(sn, ti1);
     row_max(sn);
     ti1 = ti2;
+  };
+  // A wave's last step: tile i's probabilities and PV MFMAs only (no next tile to score or load).
+  auto last_step = [&](const f32x16 (&sc)[2], int i) __attribute__((always_inline)) {
+    rescale();
+    f16x8 pb16[2][2];
+    float ps[2];
+    numerators(sc, pb16, ps);
+    lsum[0] += ps[0];
+    lsum[1] += ps[1];
+    const lds_u8* const vcur = vlds + (i % C::kVBufs) * C::kVBufBytes;
+    auto none = [](int) {};
+    pv_batch(std::integral_constant<int, 0>{}, vcur + tr_even, vcur + tr_odd, pb16, none);
+    if constexpr (kDT == 4) pv_batch(std::integral_constant<int, 1>{}, vcur + tr_even, vcur + tr_odd, pb16, none);
   };
 
   // prologue: K(0) and V(0) loads, S(0), K(1) loads, V(0) to LDS, V(1) loads; tile 0's mask
@@ -572,12 +593,22 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     if (!ti0.full) mask(sa, ti0);
     row_max(sa);
   }
+  // Pairs of steps, then the last one or two tiles: the last tile's scores are in sa or sb
+  // depending on the parity of iters (one call site for the last step keeps the register
+  // allocation of the loop).
   int i = 0;
-  for (; i + 1 < iters; i += 2) {
+  for (; i + 2 < iters; i += 2) {
     step(sa, sb, i);
     step(sb, sa, i + 1);
   }
-  if (i < iters) step(sa, sb, i);
+  if (iters > 0) {
+    const bool two = i + 2 == iters;
+    if (two) step(sa, sb, i);
+    f32x16 sl[2];
+    sl[0] = two ? sb[0] : sa[0];
+    sl[1] = two ? sb[1] : sa[1];
+    last_step(sl, iters - 1);
+  }
 
   // every wave's V reads are done before the LDS is reused for the merge
   __syncthreads();
