@@ -37,14 +37,15 @@ constexpr int kWTile = 32;     // keys per tile
 constexpr int kWGroups = 4;    // waves (key groups) per workgroup
 constexpr int kWThreads = kWGroups * kWave;
 constexpr int kWMaxSplit = 16;
-constexpr int kWRows = 64;     // query rows per workgroup
 
-template <int D, int G>
+// RT row tiles of 32 query rows per wave (and per workgroup)
+template <int D, int G, int RT>
 struct WideCfg {
-  static constexpr int kQw = kWRows / G;             // queries per workgroup
+  static constexpr int kRows = 32 * RT;              // query rows per workgroup
+  static constexpr int kQw = kRows / G;              // queries per workgroup
   static constexpr int kKSteps = D / 16;             // MFMA K-steps over the head dims
   static constexpr int kDT = D / 32;                 // 32-dim output tiles
-  static constexpr int kBlocks = 2 * kDT;            // output blocks: (dim tile, row tile)
+  static constexpr int kBlocks = RT * kDT;           // output blocks: (dim tile, row tile)
   static constexpr int kOwned = kBlocks / kWGroups;  // blocks each wave finishes
   // V tile in LDS: two page halves of 16 key rows x D dims, [key][dim] as in the pool and
   // unpadded; the 16-byte chunk c of row r sits at chunk position c ^ 2 (r % 4), so the 4 rows a
@@ -55,31 +56,47 @@ struct WideCfg {
   static constexpr int kVBufBytes = 2 * kHalfBytes;
   static constexpr int kVInstr = 2 * kHalfInstr;     // 16-byte loads (and LDS writes) per lane per tile
   static constexpr int kVBufs = 2;                   // V tiles in LDS per wave: i and i + 1
-  static constexpr int kTileBytes = kWGroups * kVBufs * kVBufBytes;
-  // The queries, staged once per workgroup: 64 rows x D dims, chunk c of row r at c ^ (r % 8).
-  static constexpr int kQBytes = kWRows * D * 2;
+  // K tile in LDS: [chunk c][32 key rows] of 16-byte chunks, row r of chunk c at slot
+  // r ^ 2 (c % 8), so that a lane's MFMA fragment for K-step s sits at a constant offset of 1 KiB s
+  // from one of four lane bases, and both the 16-lane write and read passes cover all banks once.
+  static constexpr int kKInstr = 32 * kRowChunks / kWave;  // 16-byte loads (and writes) per lane
+  static constexpr int kKBufBytes = 32 * kRowChunks * 16;
+  static constexpr int kWaveBytes = kVBufs * kVBufBytes + kKBufBytes;
+  static constexpr int kTileBytes = kWGroups * kWaveBytes;
+  // The queries, staged once per workgroup: kRows rows x D dims, chunk c of row r at c ^ (r % 8).
+  static constexpr int kQBytes = kRows * D * 2;
   static constexpr int kQInstr = kQBytes / 16 / kWThreads;  // 16-byte loads per lane
-  static constexpr int kMlFloats = kWGroups * 2 * 32 * 2;
+  static constexpr int kQRowsPerWave = kRows / kWGroups;     // rows each wave stages
+  static constexpr int kMlFloats = kWGroups * RT * 32 * 2;
   static constexpr int kMergeBytes = kMlFloats * 4 + kWGroups * kBlocks * 16 * kWave * 4;
   static constexpr int kLdsBytes = kTileBytes + kQBytes > kMergeBytes ? kTileBytes + kQBytes : kMergeBytes;
-  static_assert(kQw * G == kWRows, "64 rows per workgroup");
+  static_assert(RT == 1 || RT == 2, "one or two row tiles");
+  static_assert(kQw * G == kRows, "32 RT rows per workgroup");
   static_assert(kBlocks % kWGroups == 0, "every wave finishes the same number of blocks");
   static_assert(16 * kRowChunks % kWave == 0 && kRowChunks >= 8, "whole loads per page half; swizzle in range");
-  static_assert(kQBytes % (16 * kWThreads) == 0 && 16 * kRowChunks * kWGroups == kWRows * kRowChunks, "Q staging");
+  static_assert(kRowChunks % 8 == 0 && kKInstr % 2 == 0, "K loads: 8 rows x 8 chunks each, within one page half");
+  static_assert(kQBytes % (16 * kWThreads) == 0 && kQRowsPerWave * kRowChunks == kQInstr * kWave, "Q staging");
 };
 
 struct WidePlan {
   int64_t n_qb;
-  int nsplit;
+  int rt, nsplit;
   size_t off_ml, off_o, bytes;
 };
 
+// Row tiles per wave: two (64 rows per workgroup, every K and V fragment feeding two MFMA chains)
+// unless the (query block, kv head) pairs of 64 rows would fill at most half the CUs; then, for
+// head dim 128, one (32 rows per workgroup), which doubles the pairs instead of splitting their
+// keys over workgroups that merge through memory.
 // Key split: enough workgroups to cover the CUs when (query blocks x kv heads) alone does not,
 // provided every split still gets at least two tiles per key group.
 static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
   WidePlan p;
   const int g = hq / hkv;
-  p.n_qb = (int64_t(T) + kWRows / g - 1) / (kWRows / g);
+  auto blocks = [&](int rows) { return (int64_t(T) + rows / g - 1) / (rows / g); };
+  p.rt = d == 128 && blocks(64) * hkv * 2 <= cus ? 1 : 2;
+  const int rows = 32 * p.rt;
+  p.n_qb = blocks(rows);
   const int64_t units = p.n_qb * hkv;
   const int64_t max_tiles = (int64_t(query_start) + T + kWTile - 1) / kWTile;
   int ns = 1;
@@ -88,8 +105,8 @@ static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hk
   p.nsplit = ns;
   const size_t slots = size_t(units) * ns;
   p.off_ml = kTicketBytes;
-  p.off_o = p.off_ml + align256(slots * kWRows * 2 * sizeof(float));
-  p.bytes = ns > 1 ? p.off_o + align256(slots * kWRows * size_t(d) * sizeof(float)) : 256;
+  p.off_o = p.off_ml + align256(slots * rows * 2 * sizeof(float));
+  p.bytes = ns > 1 ? p.off_o + align256(slots * rows * size_t(d) * sizeof(float)) : 256;
   return p;
 }
 
@@ -151,18 +168,22 @@ __device__ __forceinline__ void pin_agpr(f16x8& a) {
 }
 
 // No instruction: the values must exist at this point (and the scheduler treats it as a boundary).
-__device__ __forceinline__ void pin_regs(f16x8& a, f16x8& b, f16x8& c, f16x8& d) {
+template <int RT>
+__device__ __forceinline__ void pin_probs(f16x8 (&p)[RT][2]) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  asm volatile("" : "+v"(a), "+v"(b), "+v"(c), "+v"(d));
+  if constexpr (RT == 2)
+    asm volatile("" : "+v"(p[0][0]), "+v"(p[0][1]), "+v"(p[1][0]), "+v"(p[1][1]));
+  else
+    asm volatile("" : "+v"(p[0][0]), "+v"(p[0][1]));
 #endif
 }
 
-template <int D, int G, bool kAppend>
+template <int D, int G, int RT, bool kAppend>
 __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
     const int32_t* __restrict__ table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb,
     int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap) {
-  using C = WideCfg<D, G>;
+  using C = WideCfg<D, G, RT>;
   constexpr int kKS = C::kKSteps;
   constexpr int kDT = C::kDT;
   constexpr int kQw = C::kQw;
@@ -185,10 +206,10 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   const int iters = n_tiles > first ? int(ceil_div(n_tiles - first, kWGroups * nsplit)) : 0;
 
   // This lane's row in each row tile: row = 32 rt + col = g * kQw + query offset.
-  int my_q[2], my_pos[2], my_head[2];
-  bool q_ok[2];
+  int my_q[RT], my_pos[RT], my_head[RT];
+  bool q_ok[RT];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) {
+  for (int rt = 0; rt < RT; ++rt) {
     const int rho = 32 * rt + col;
     my_q[rt] = q0 + rho % kQw;
     my_head[rt] = kvh * G + rho / kQw;
@@ -248,38 +269,27 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   u32x4 qst[C::kQInstr];
 #pragma unroll
   for (int n = 0; n < C::kQInstr; ++n) {
-    const int slot = n * kWave + lane, rho = 16 * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
+    const int slot = n * kWave + lane, rho = C::kQRowsPerWave * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
     const int qi = q0 + rho % kQw;
     const u32x4 v = ld16(q + (int64_t(min(qi, T - 1)) * hq + kvh * G + rho / kQw) * D + 8 * c);
     qst[n] = qi < T ? v : u32x4{0u, 0u, 0u, 0u};
   }
   // The window arrives before the first tiles' K and V are requested.
   asm volatile("" ::"v"(win_k.ids) : "memory");
-  f16x8 qreg[2][kKS];  // Q^T (filled from LDS in the prologue)
+  f16x8 qreg[RT][kKS];  // Q^T (filled from LDS in the prologue)
 
-  // K: this lane's key row (col) of the tile, dims 16 s + 8 half .. + 7 for K-step s, as kKS 16-byte global
-  // loads (k_load).  A key that no row may see still reads a real row (page 0 for an invalid page;
-  // the chunk's last row past its end), whose scores the mask replaces.
-  auto k_tile = [&](int i, int pa, int pb, int fl) __attribute__((always_inline)) -> const f16* {
-    const int page = col < kWBlock ? ((fl & 1) ? pa : 0) : ((fl & 2) ? pb : 0);
-    const f16* src = head_pool + int64_t(page) * page_elems + (col % kWBlock) * tok_stride + 8 * half;
-    if constexpr (kAppend) {
-      // (uniform; query_start % 32 == 0) a tile at or past query_start holds the chunk's own rows
-      const int kt = tile_of(i) * kWTile;
-      const f16* own = ap.new_k + int64_t(min(kt - query_start + col, T - 1)) * tok_stride + kvh * D + 8 * half;
-      src = kt >= query_start ? own : src;
-    }
-    return src;
-  };
-
-  // V: 16-byte buffer loads into registers one step ahead (v_load), then 16-byte writes into one of
-  // the wave's two LDS tile buffers (v_store), lane l of load n of page half h to slot 64 n + l:
-  // LDS row r = slot / (D / 8) of the half at chunk position slot % (D / 8), which holds the row's
-  // chunk (slot % (D / 8)) ^ 2 (r % 4).  Each half reads through a buffer resource that ends after
-  // the page's keys below the end of the sequence (none for an invalid page; the chunk's rows for a
-  // tile of them), so every other row is zeros: masked keys contribute exactly nothing.
+  // K and V tiles are read from the pool with 16-byte buffer loads into registers a step ahead of
+  // their 16-byte writes into the wave's LDS buffers.  Each page half reads through a buffer
+  // resource that ends after the page's keys below the end of the sequence (none for an invalid
+  // page; the chunk's rows for a tile of them), so every other row reads zeros: masked keys
+  // contribute exactly nothing (their scores are replaced by the mask).
+  //  * V, lane l of load n of page half h -> slot 64 n + l: LDS row r = slot / (D / 8) of the half
+  //    at chunk position slot % (D / 8), which holds the row's chunk (slot % (D / 8)) ^ 2 (r % 4).
+  //  * K, load n (8 key rows x 8 chunks: every 8 consecutive lanes read one 128-byte line),
+  //    lane l = 8 a + e: tile row r = 8 (n / (D / 64)) + a, chunk c = 8 (n % (D / 64)) + e.
   const int rsrc_bytes = kAppend ? T * int(tok_stride) * 2 : 0;
   const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_v), 0, rsrc_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(ap.new_k), 0, rsrc_bytes, 0x00020000);
   uint32_t voff[C::kHalfInstr];
 #pragma unroll
   for (int n = 0; n < C::kHalfInstr; ++n) {
@@ -287,12 +297,31 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     const int c = (slot % C::kRowChunks) ^ (2 * (r % 4));
     voff[n] = uint32_t((r * int(tok_stride) + 8 * c) * 2);
   }
-  lds_u8* const vlds = (lds_u8*)(smem) + grp * C::kVBufs * C::kVBufBytes;
+  constexpr int kCB = C::kRowChunks / 8;  // chunk blocks per row
+  uint32_t koff[C::kKInstr / 2];          // (the same for both page halves)
+  uint32_t kwr[2];                        // LDS write offsets (row blocks n / kCB even, odd)
+  {
+    const int a = lane / 8, e = lane % 8;
+#pragma unroll
+    for (int n = 0; n < C::kKInstr / 2; ++n) {
+      const int r = 8 * ((n / kCB) % 2) + a, c = 8 * (n % kCB) + e;
+      koff[n] = uint32_t((r * int(tok_stride) + 8 * c) * 2);
+    }
+#pragma unroll
+    for (int o = 0; o < 2; ++o) kwr[o] = uint32_t((e * 32 + ((8 * o + a) ^ (2 * e))) * 16);
+  }
+  lds_u8* const vlds = (lds_u8*)(smem) + grp * C::kWaveBytes;
+  lds_u8* const klds = vlds + C::kVBufs * C::kVBufBytes;
+  // this lane's K fragment of K-step s (key row col, chunk 2 s + half) is at kfrag[s % 4] + 1 KiB s
+  const lds_u8* kfrag[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) kfrag[j] = klds + half * 512 + (col ^ ((4 * j + 2 * half) % 16)) * 16;
   struct VTile {
     __amdgpu_buffer_rsrc_t r[2];
     uint32_t add[2];
   };
-  auto v_tile = [&](int i, int pa, int pb, int fl) __attribute__((always_inline)) -> VTile {
+  auto kv_tile = [&](int i, int pa, int pb, int fl, int64_t base, __amdgpu_buffer_rsrc_t own)
+      __attribute__((always_inline)) -> VTile {
     const int kt = tile_of(i) * kWTile;
     VTile t;
 #pragma unroll
@@ -301,12 +330,12 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
       const bool ok = ((fl >> h) & 1) != 0;
       const int page = __builtin_amdgcn_readfirstlane(ok ? (h == 0 ? pa : pb) : 0);
       const int keys = __builtin_amdgcn_readfirstlane(ok ? min(max(total - (kt + 16 * h), 0), 16) : 0);
-      t.r[h] = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(head_pool + v_off + int64_t(page) * page_elems), 0,
+      t.r[h] = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(head_pool + base + int64_t(page) * page_elems), 0,
                                                  keys * int(tok_stride) * 2, 0x00020000);
       t.add[h] = 0;
       if constexpr (kAppend) {
         if (kt >= query_start) {  // (uniform) the chunk's own rows; past its end they read zero
-          t.r[h] = rv;
+          t.r[h] = own;
           t.add[h] = uint32_t(((min(kt - query_start, T) + 16 * h) * int(tok_stride) + kvh * D) * 2);
         }
       }
@@ -321,6 +350,19 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   auto v_store = [&](lds_u8* dst, int j, u32x4 v) __attribute__((always_inline)) {
     const int h = j / C::kHalfInstr, n = j % C::kHalfInstr;
     *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(dst + h * C::kHalfBytes + (n * kWave + lane) * 16) = v;
+  };
+  // load n (of kKInstr) of a tile's K, its LDS write, and the read of K-step s's fragment
+  auto k_load = [&](const VTile& t, int n) __attribute__((always_inline)) {
+    const int h = n / (C::kKInstr / 2);
+    return buf_ld16(t.r[h], koff[n % (C::kKInstr / 2)] + t.add[h]);
+  };
+  auto k_store = [&](int n, u32x4 v) __attribute__((always_inline)) {
+    const int rb = n / kCB, cb = n % kCB;  // row block (8 rows), chunk block (8 chunks)
+    // slot c 32 + (r ^ 2 (c % 8)) = 256 cb + 16 (rb / 2) + [e 32 + ((8 (rb % 2) + a) ^ 2 e)]
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(klds + kwr[rb % 2] + cb * 4096 + (rb / 2) * 256) = v;
+  };
+  auto k_read = [&](int s) __attribute__((always_inline)) {
+    return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(kfrag[s % 4] + 1024 * s);
   };
 
   // Transposing V reads: lane = 16 g + 4 rr + q reads key row R = 4 (lane / 32) + rr of a page half,
@@ -337,54 +379,63 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     tr_odd = base - 64 * b2;
   }
 
-  float m[2] = {kNegBig, kNegBig}, lsum[2] = {0.f, 0.f};
-  f32x16 acc[kDT][2];
+  float m[RT], lsum[RT];
+  f32x16 acc[kDT][RT];
 #pragma unroll
-  for (int dt = 0; dt < kDT; ++dt) acc[dt][0] = acc[dt][1] = f32x16{};
+  for (int rt = 0; rt < RT; ++rt) {
+    m[rt] = kNegBig;
+    lsum[rt] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < kDT; ++dt) acc[dt][rt] = f32x16{};
+  }
 
-  // Addressing of a tile: this lane's K row, the V buffer resources, the page flags, and whether
-  // every key is visible to every row of the block (no mask needed).
-  struct TileInfo {
-    const f16* k;
-    VTile v;
-    int kt, fl;
+  // A tile's first key, pages, page flags, and whether every key is visible to every row of the
+  // block (no mask needed); all uniform.
+  struct TilePos {
+    int kt, pa, pb, fl;
     bool full;
   };
-  auto tile_info = [&](int t) __attribute__((always_inline)) -> TileInfo {
-    int pa, pb;
-    tile_pages(win_k, t, pa, pb);
-    TileInfo ti;
-    ti.fl = tile_flags(pa, pb);
-    ti.kt = tile_of(t) * kWTile;
-    ti.k = k_tile(t, pa, pb, ti.fl);
-    ti.v = v_tile(t, pa, pb, ti.fl);
-    ti.full = ti.fl == 3 && ti.kt + kWTile <= total && ti.kt + kWTile - 1 <= query_start + q0;
-    return ti;
+  auto tile_pos = [&](int t) __attribute__((always_inline)) -> TilePos {
+    TilePos tp;
+    tile_pages(win_k, t, tp.pa, tp.pb);
+    tp.fl = tile_flags(tp.pa, tp.pb);
+    tp.kt = tile_of(t) * kWTile;
+    tp.full = (tp.fl == 3) & (tp.kt + kWTile <= total) & (tp.kt + kWTile - 1 <= query_start + q0);
+    return tp;
+  };
+  // buffer resources of a tile's K and V
+  auto k_tile = [&](int t, const TilePos& tp) __attribute__((always_inline)) {
+    return kv_tile(t, tp.pa, tp.pb, tp.fl, 0, rk);
+  };
+  auto v_tile = [&](int t, const TilePos& tp) __attribute__((always_inline)) {
+    return kv_tile(t, tp.pa, tp.pb, tp.fl, v_off, rv);
   };
 
   // Pipeline.  Step i (one tile) is two scheduling regions:
-  //  A: tile i + 1's S MFMAs (its keys are in registers), each K fragment reloaded with tile
-  //     i + 2's keys right after its two MFMAs, and tile i's probabilities, fp16 packing and
-  //     partial row sums in the MFMAs' shadow;
+  //  A: tile i + 1's S MFMAs (K fragments read from the wave's K buffer), tile i + 2's K (loaded
+  //     in the previous step) written to that buffer once every fragment is read, tile i + 3's K
+  //     loads, and tile i's probabilities and fp16 packing in the MFMAs' shadow;
   //  B: tile i's PV MFMAs (V(i) from LDS through transposing reads), tile i + 1's V (loaded in the
-  //     previous step) written to the LDS buffer tile i - 1 used, and tile i + 2's V loads between
-  //     them.
-  // Then tile i + 1's mask (when some key of it is hidden from some row) and row maxima.  The lazy
-  // rescale for tile i + 1 opens the next step.  Every request is unconditional (past the last
-  // tile they read page 0 or zeros).
+  //     previous step) written to the LDS buffer tile i - 1 used, tile i + 2's V loads, tile i + 1's
+  //     row maxima and tile i's row sums between them.
+  // Tile i + 1's mask (when some key of it is hidden from some row) sits between the regions; the
+  // lazy rescale for tile i + 1 opens the next step.  Every request is unconditional (past the last
+  // tile they read zeros).
   u32x4 kr[kKS];
+  u32x4 kst[C::kKInstr];  // K two tiles ahead, in flight to LDS
   u32x4 vst[C::kVInstr];  // the next tile's V, in flight to LDS
-  auto s_mfma_step = [&](f32x16 (&st)[2], int s) __attribute__((always_inline)) {  // S^T, K-step s
+  auto s_mfma_step = [&](f32x16 (&st)[RT], int s) __attribute__((always_inline)) {  // S^T, K-step s
     const f16x8 kf = as_h8(kr[s]);
-    st[0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[0][s], s == 0 ? f32x16{} : st[0], 0, 0, 0);
-    st[1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[1][s], s == 0 ? f32x16{} : st[1], 0, 0, 0);
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt)
+      st[rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf, qreg[rt][s], s == 0 ? f32x16{} : st[rt], 0, 0, 0);
   };
   // Causal mask, end of sequence and invalid pages (scores -> -inf): key kk of the tile is visible
   // to this lane's row iff kk <= lim and its page is valid; the lane's score r is key
   // 8 (r / 4) + 4 half + r % 4.
-  auto mask = [&](f32x16 (&st)[2], const TileInfo& ti) __attribute__((always_inline)) {
+  auto mask = [&](f32x16 (&st)[RT], const TilePos& ti) __attribute__((always_inline)) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const int lim = min(my_pos[rt], total - 1) - ti.kt;
       const int la = ((ti.fl & 1) ? lim : -1) - 4 * half;
       const int lb = ((ti.fl & 2) ? lim : kWBlock - 1) - 4 * half;
@@ -396,10 +447,10 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     }
   };
   // Each row's maximum over the tile and the lane ^ 32 partner (log2 units)
-  float cand[2];
-  auto row_max = [&](const f32x16 (&st)[2]) __attribute__((always_inline)) {
+  float cand[RT];
+  auto row_max = [&](const f32x16 (&st)[RT]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       float mq[4];
 #pragma unroll
       for (int a = 0; a < 4; ++a)
@@ -412,7 +463,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   auto rescale = [&]() __attribute__((always_inline)) {
     constexpr float kSlack = 8.f;
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       const bool grow = cand[rt] > m[rt] + kSlack;
       if (__builtin_amdgcn_ballot_w64(grow) != 0) {  // rare after the first tile
         const float mn = grow ? cand[rt] : m[rt];
@@ -424,11 +475,10 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
       }
     }
   };
-  // P of a tile in fp16 (the B operands of its PV MFMAs) and this lane's partial row sums of the
-  // fp16 values (the ones the PV MFMAs multiply)
-  auto numerators = [&](const f32x16 (&sc)[2], f16x8 (&pb16)[2][2], float (&ps)[2]) __attribute__((always_inline)) {
+  // P of a tile in fp16 (the B operands of its PV MFMAs)
+  auto numerators = [&](const f32x16 (&sc)[RT], f16x8 (&pb16)[RT][2]) __attribute__((always_inline)) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
+    for (int rt = 0; rt < RT; ++rt) {
       float pv[16];
 #pragma unroll
       for (int r = 0; r < 16; ++r) pv[r] = exp2_fast(fmaf(sc[rt][r], scale_log2, -m[rt]));
@@ -436,20 +486,27 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
                           f16(pv[7])};
       pb16[rt][1] = f16x8{f16(pv[8]), f16(pv[9]), f16(pv[10]), f16(pv[11]), f16(pv[12]), f16(pv[13]),
                           f16(pv[14]), f16(pv[15])};
-      const f16x2 one = f16x2{f16(1.f), f16(1.f)};
+    }
+  };
+  // This lane's partial row sums of the fp16 probabilities (the values the PV MFMAs multiply),
+  // added to lsum.
+  auto add_row_sums = [&](const f16x8 (&pb16)[RT][2]) __attribute__((always_inline)) {
+    const f16x2 one = f16x2{f16(1.f), f16(1.f)};
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) {
       float s = 0.f;
 #pragma unroll
       for (int u = 0; u < 2; ++u)
 #pragma unroll
         for (int e = 0; e < 4; ++e)
           s = __builtin_amdgcn_fdot2(f16x2{pb16[rt][u][2 * e], pb16[rt][u][2 * e + 1]}, one, s, false);
-      ps[rt] = s;
+      lsum[rt] += s;
     }
   };
   // PV batch b of a tile: O^T += V^T . P^T for dim tiles 2 b and 2 b + 1 (8 transposing reads, 8
   // MFMAs).  A = V^T for dims 32 dt + col, keys 16 u + 4 half + 0..3 and 16 u + 8 + 4 half + 0..3
   // (page half u).  after(pr) runs after MFMA pair pr (0..3) of the batch.
-  auto pv_batch = [&](auto bc, const lds_u8* ae, const lds_u8* ao, const f16x8 (&pb16)[2][2], auto&& after)
+  auto pv_batch = [&](auto bc, const lds_u8* ae, const lds_u8* ao, const f16x8 (&pb16)[RT][2], auto&& after)
       __attribute__((always_inline)) {
     constexpr int b = decltype(bc)::value;
     constexpr int d0 = 2 * b, HB = C::kHalfBytes, HI = 16 * D;
@@ -469,49 +526,56 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
         const f16x4 lo = __builtin_bit_cast(f16x4, rd[4 * j + 2 * u]);
         const f16x4 hi = __builtin_bit_cast(f16x4, rd[4 * j + 2 * u + 1]);
         const f16x8 vf = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        acc[d0 + j][0] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[0][u], acc[d0 + j][0], 0, 0, 0);
-        acc[d0 + j][1] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[1][u], acc[d0 + j][1], 0, 0, 0);
+#pragma unroll
+        for (int rt = 0; rt < RT; ++rt)
+          acc[d0 + j][rt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pb16[rt][u], acc[d0 + j][rt], 0, 0, 0);
         after(2 * j + u);
       }
   };
-  // VALU instructions per MFMA in region A: ~100 for a tile's probabilities over 2 kKS MFMAs
-  constexpr int kAValu = (100 + 2 * kKS - 1) / (2 * kKS);
-  TileInfo ti1;  // tile i + 1
-  auto step = [&](f32x16 (&sc)[2], f32x16 (&sn)[2], int i) __attribute__((always_inline)) {
+  // VALU instructions per MFMA in region A: ~50 per row tile for a tile's probabilities, over
+  // RT kKS MFMAs (two VALU groups per K-step)
+  constexpr int kAValu = (50 * RT + 2 * kKS - 1) / (2 * kKS);
+  TilePos p1, p2;  // tiles i + 1 and i + 2
+  auto step = [&](f32x16 (&sc)[RT], f32x16 (&sn)[RT], int i) __attribute__((always_inline)) {
     rescale();  // for tile i, whose maxima were taken in the previous step
-    ensure_window(win_k, i + 2);
-    const TileInfo ti2 = tile_info(i + 2);
+    ensure_window(win_k, i + 3);
+    const TilePos p3 = tile_pos(i + 3);
+    const VTile k3 = k_tile(i + 3, p3);
+    const VTile v2 = v_tile(i + 2, p2);
     __builtin_amdgcn_sched_barrier(0);
     // region A
-    const f16* const k2 = ti2.k;
 #pragma unroll
-    for (int s = 0; s < kKS; ++s) {
-      s_mfma_step(sn, s);
-      kr[s] = ld16(k2 + 16 * s);
-    }
-    f16x8 pb16[2][2];
-    float ps[2];
-    numerators(sc, pb16, ps);
+    for (int s = 0; s < kKS; ++s) kr[s] = k_read(s);
+#pragma unroll
+    for (int s = 0; s < kKS; ++s) s_mfma_step(sn, s);
+#pragma unroll
+    for (int n = 0; n < C::kKInstr; ++n) k_store(n, kst[n]);
+#pragma unroll
+    for (int n = 0; n < C::kKInstr; ++n) kst[n] = k_load(k3, n);
+    f16x8 pb16[RT][2];
+    numerators(sc, pb16);
     // (the probabilities are pinned here, so the exponentials are not sunk to their use in the PV
     // MFMAs below, out of the MFMAs' shadow)
-    pin_regs(pb16[0][0], pb16[0][1], pb16[1][0], pb16[1][1]);
+    pin_probs<RT>(pb16);
+    static_assert(C::kKInstr == kKS, "one K write and load per K-step");
+    __builtin_amdgcn_sched_group_barrier(0x100, kKS, 0);  // K fragment reads
 #pragma unroll
     for (int s = 0; s < kKS; ++s) {
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, kAValu, 0);  // VALU
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
+      if constexpr (RT == 2) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);       // K write
       __builtin_amdgcn_sched_group_barrier(0x020, 1, 0);       // K load
       __builtin_amdgcn_sched_group_barrier(0x002, kAValu, 0);  // VALU
     }
     __builtin_amdgcn_sched_barrier(0);
-    lsum[0] += ps[0];
-    lsum[1] += ps[1];
+    // tile i + 1's mask, when some key of it is hidden from some row
+    if (!p1.full) mask(sn, p1);
     // region B
     const lds_u8* const vcur = vlds + (i % C::kVBufs) * C::kVBufBytes;
     const lds_u8* const ae = vcur + tr_even;
     const lds_u8* const ao = vcur + tr_odd;
     lds_u8* const vnext = vlds + ((i + 1) % C::kVBufs) * C::kVBufBytes;
-    const VTile v2 = ti2.v;
     // Tile i's PV MFMAs; tile i + 1's V goes to LDS (first batch) and tile i + 2's is loaded (last
     // batch) between them.
     auto batch = [&](auto bc) __attribute__((always_inline)) {
@@ -534,63 +598,73 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     static_assert(C::kVInstr == 2 * kDT, "one V load per MFMA pair over the batches");
     batch(std::integral_constant<int, 0>{});
     if constexpr (kDT == 4) batch(std::integral_constant<int, 1>{});
-    __builtin_amdgcn_sched_barrier(0);
-    if (!ti1.full) mask(sn, ti1);
+    // tile i + 1's row maxima and tile i's row sums, in the PV MFMAs' shadow
     row_max(sn);
-    ti1 = ti2;
+    add_row_sums(pb16);
+    __builtin_amdgcn_sched_barrier(0);
+    p1 = p2;
+    p2 = p3;
   };
   // A wave's last step: tile i's probabilities and PV MFMAs only (no next tile to score or load).
-  auto last_step = [&](const f32x16 (&sc)[2], int i) __attribute__((always_inline)) {
+  auto last_step = [&](const f32x16 (&sc)[RT], int i) __attribute__((always_inline)) {
     rescale();
-    f16x8 pb16[2][2];
-    float ps[2];
-    numerators(sc, pb16, ps);
-    lsum[0] += ps[0];
-    lsum[1] += ps[1];
+    f16x8 pb16[RT][2];
+    numerators(sc, pb16);
+    add_row_sums(pb16);
     const lds_u8* const vcur = vlds + (i % C::kVBufs) * C::kVBufBytes;
     auto none = [](int) {};
     pv_batch(std::integral_constant<int, 0>{}, vcur + tr_even, vcur + tr_odd, pb16, none);
     if constexpr (kDT == 4) pv_batch(std::integral_constant<int, 1>{}, vcur + tr_even, vcur + tr_odd, pb16, none);
   };
 
-  // prologue: K(0) and V(0) loads, S(0), K(1) loads, V(0) to LDS, V(1) loads; tile 0's mask
-  f32x16 sa[2], sb[2];
+  // prologue: K(0) and V(0) loads; K(0) to LDS, K(1) loads; S(0); K(1) to LDS, K(2) loads; V(0)
+  // to LDS, V(1) loads; tile 0's mask
+  f32x16 sa[RT], sb[RT];
   {
-    const TileInfo ti0 = tile_info(0);
-    ti1 = tile_info(1);
+    const TilePos p0 = tile_pos(0);
+    p1 = tile_pos(1);
+    p2 = tile_pos(2);
 #pragma unroll
-    for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti0.k + 16 * s);
+    for (int n = 0; n < C::kKInstr; ++n) kst[n] = k_load(k_tile(0, p0), n);
 #pragma unroll
-    for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(ti0.v, j);
+    for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(v_tile(0, p0), j);
     // Q through LDS: Q^T as the B operand, K-step s = dims 16 s + 8 half .. + 7 of row 32 rt + col
 #pragma unroll
     for (int n = 0; n < C::kQInstr; ++n) {
-      const int slot = n * kWave + lane, rho = 16 * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
+      const int slot = n * kWave + lane, rho = C::kQRowsPerWave * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
       *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((c ^ (rho % 8)) * 16)) = qst[n];
     }
     __syncthreads();
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt)
+    for (int rt = 0; rt < RT; ++rt)
 #pragma unroll
       for (int s = 0; s < kKS; ++s) {
         const int rho = 32 * rt + col, c = 2 * s + half;
         qreg[rt][s] = as_h8(*reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((c ^ (rho % 8)) * 16)));
         pin_agpr(qreg[rt][s]);
       }
+#pragma unroll
+    for (int n = 0; n < C::kKInstr; ++n) k_store(n, kst[n]);
+#pragma unroll
+    for (int n = 0; n < C::kKInstr; ++n) kst[n] = k_load(k_tile(1, p1), n);
     // The barrier above leaves the 4 waves in step; started in step they would reach their load
     // and their MFMA phases together for the whole loop and queue on the CU's shared memory path.
     // Wave grp starts 6 x 64 x grp cycles late instead (a quarter of a step or so apart; measured:
     // 71.9 -> 67.4 us per config-3 layer).
     for (int w = 0; w < grp; ++w) __builtin_amdgcn_s_sleep(6);
 #pragma unroll
+    for (int s = 0; s < kKS; ++s) kr[s] = k_read(s);
+#pragma unroll
     for (int s = 0; s < kKS; ++s) s_mfma_step(sa, s);
 #pragma unroll
-    for (int s = 0; s < kKS; ++s) kr[s] = ld16(ti1.k + 16 * s);
+    for (int n = 0; n < C::kKInstr; ++n) k_store(n, kst[n]);
+#pragma unroll
+    for (int n = 0; n < C::kKInstr; ++n) kst[n] = k_load(k_tile(2, p2), n);
 #pragma unroll
     for (int j = 0; j < C::kVInstr; ++j) v_store(vlds, j, vst[j]);
 #pragma unroll
-    for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(ti1.v, j);
-    if (!ti0.full) mask(sa, ti0);
+    for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(v_tile(1, p1), j);
+    if (!p0.full) mask(sa, p0);
     row_max(sa);
   }
   // Pairs of steps, then the last one or two tiles: the last tile's scores are in sa or sb
@@ -604,44 +678,44 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   if (iters > 0) {
     const bool two = i + 2 == iters;
     if (two) step(sa, sb, i);
-    f32x16 sl[2];
-    sl[0] = two ? sb[0] : sa[0];
-    sl[1] = two ? sb[1] : sa[1];
+    f32x16 sl[RT];
+#pragma unroll
+    for (int rt = 0; rt < RT; ++rt) sl[rt] = two ? sb[rt] : sa[rt];
     last_step(sl, iters - 1);
   }
 
   // every wave's V reads are done before the LDS is reused for the merge
   __syncthreads();
 
-  float lt[2];
+  float lt[RT];
 #pragma unroll
-  for (int rt = 0; rt < 2; ++rt) lt[rt] = lsum[rt] + __shfl_xor(lsum[rt], 32);
+  for (int rt = 0; rt < RT; ++rt) lt[rt] = lsum[rt] + __shfl_xor(lsum[rt], 32);
   // Key-group merge: every wave writes its (m, l) and all its blocks to LDS; block p = (dim tile
-  // p / 2, row tile p % 2) is then finished by wave p % 4, from the four groups' copies in group
-  // order.  Every block a wave finishes has row tile rt_own = grp % 2.
-  const int rt_own = grp % 2;
+  // p / RT, row tile p % RT) is then finished by wave p % 4, from the four groups' copies in group
+  // order.  Every block a wave finishes has row tile rt_own = grp % RT.
+  const int rt_own = grp % RT;
   float* mlb = reinterpret_cast<float*>(smem);                 // [wave][rt][32][2]
   f32x4* accb = reinterpret_cast<f32x4*>(mlb + C::kMlFloats);  // [wave][block][4][lane]
   if (half == 0) {
 #pragma unroll
-    for (int rt = 0; rt < 2; ++rt) {
-      mlb[((grp * 2 + rt) * 32 + col) * 2 + 0] = m[rt];
-      mlb[((grp * 2 + rt) * 32 + col) * 2 + 1] = lt[rt];
+    for (int rt = 0; rt < RT; ++rt) {
+      mlb[((grp * RT + rt) * 32 + col) * 2 + 0] = m[rt];
+      mlb[((grp * RT + rt) * 32 + col) * 2 + 1] = lt[rt];
     }
   }
 #pragma unroll
   for (int p = 0; p < C::kBlocks; ++p)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
-      const f32x16& a = acc[p / 2][p % 2];
+      const f32x16& a = acc[p / RT][p % RT];
       accb[((grp * C::kBlocks + p) * 4 + r4) * kWave + lane] = f32x4{a[4 * r4], a[4 * r4 + 1], a[4 * r4 + 2], a[4 * r4 + 3]};
     }
   __syncthreads();
   float mk[kWGroups], lk[kWGroups];
 #pragma unroll
   for (int k = 0; k < kWGroups; ++k) {
-    mk[k] = mlb[((k * 2 + rt_own) * 32 + col) * 2];
-    lk[k] = mlb[((k * 2 + rt_own) * 32 + col) * 2 + 1];
+    mk[k] = mlb[((k * RT + rt_own) * 32 + col) * 2];
+    lk[k] = mlb[((k * RT + rt_own) * 32 + col) * 2 + 1];
   }
   float mfin = mk[0];
 #pragma unroll
@@ -680,8 +754,8 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     const int64_t pair = int64_t(qb) * num_kv_heads + kvh;
     const int64_t slot = pair * nsplit + split;
     const int64_t nslots = int64_t(n_qb) * num_kv_heads * nsplit;
-    const __amdgpu_buffer_rsrc_t r_o = make_rsrc(ws.o, uint32_t(nslots * kWRows * D * 4));
-    const __amdgpu_buffer_rsrc_t r_ml = make_rsrc(ws.ml, uint32_t(nslots * kWRows * 2 * 4));
+    const __amdgpu_buffer_rsrc_t r_o = make_rsrc(ws.o, uint32_t(nslots * C::kRows * D * 4));
+    const __amdgpu_buffer_rsrc_t r_ml = make_rsrc(ws.ml, uint32_t(nslots * C::kRows * 2 * 4));
     auto o_off = [&](int64_t sl, int p, int r4) __attribute__((always_inline)) {
       return uint32_t((((sl * C::kBlocks + p) * 4 + r4) * kWave + lane) * 16);
     };
@@ -690,7 +764,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     for (int ob = 0; ob < C::kOwned; ++ob)
 #pragma unroll
       for (int r4 = 0; r4 < 4; ++r4) st_dev4(r_o, o_off(slot, grp + kWGroups * ob, r4), o[ob][r4]);
-    if (grp < 2 && half == 0) st_dev2(r_ml, uint32_t(slot * kWRows * 8) + ml_row, f32x2{mfin, lfin});
+    if (grp < RT && half == 0) st_dev2(r_ml, uint32_t(slot * C::kRows * 8) + ml_row, f32x2{mfin, lfin});
     wait_all_mem();   // this wave's stores are acknowledged
     __syncthreads();  // ... and every other wave's
     if (tid == 0) s_ticket = __hip_atomic_fetch_add(ws.count + pair, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -710,7 +784,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
       }
     mx = m_own;
     for (int s2 = 0; s2 < nsplit; ++s2)
-      if (s2 != split) mx = fmaxf(mx, ld_dev2(r_ml, uint32_t((pair * nsplit + s2) * kWRows * 8) + ml_row)[0]);
+      if (s2 != split) mx = fmaxf(mx, ld_dev2(r_ml, uint32_t((pair * nsplit + s2) * C::kRows * 8) + ml_row)[0]);
     lfin = 0.f;
     // splits in batches of kSplitBatch, every load of a batch in flight at once
     constexpr int kSplitBatch = 4;
@@ -727,7 +801,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
 #pragma unroll
             for (int r4 = 0; r4 < 4; ++r4) x[ob][r4] = mine[ob][r4];
           if (s2 != split) {  // (uniform)
-            ml = ld_dev2(r_ml, uint32_t(sl * kWRows * 8) + ml_row);
+            ml = ld_dev2(r_ml, uint32_t(sl * C::kRows * 8) + ml_row);
 #pragma unroll
             for (int ob = 0; ob < C::kOwned; ++ob)
 #pragma unroll
@@ -753,7 +827,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   f16* orow = out + (int64_t(my_q[rt_own]) * hq + my_head[rt_own]) * D;
 #pragma unroll
   for (int ob = 0; ob < C::kOwned; ++ob) {
-    const int dt = (grp + kWGroups * ob) / 2;
+    const int dt = (grp + kWGroups * ob) / RT;
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {  // dims 32 dt + 8 r4 + 4 half + 0..3
       const f32x4 y = o[ob][r4];
@@ -766,17 +840,20 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
 typedef void (*WideKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t, int32_t, int32_t,
                            int32_t, float, PrefillWorkspace, PrefillAppend);
 
-static WideKernel pick_wide(int d, int g, bool append) {
-#define IFN_WIDE_CASE(DD, GG)                                                                        \
-  if (d == DD && g == GG) return append ? prefill_wide_kernel<DD, GG, true> : prefill_wide_kernel<DD, GG, false>;
-  IFN_WIDE_CASE(64, 1) IFN_WIDE_CASE(64, 2) IFN_WIDE_CASE(64, 4) IFN_WIDE_CASE(64, 8)
-  IFN_WIDE_CASE(128, 1) IFN_WIDE_CASE(128, 2) IFN_WIDE_CASE(128, 4) IFN_WIDE_CASE(128, 8)
+// (row tiles: 2 for every shape, 1 for head dim 128, where a wave's 4 dim tiles are 4 blocks)
+static WideKernel pick_wide(int d, int g, int rt, bool append) {
+#define IFN_WIDE_CASE(DD, GG, RR)                                                                    \
+  if (d == DD && g == GG && rt == RR)                                                                \
+    return append ? prefill_wide_kernel<DD, GG, RR, true> : prefill_wide_kernel<DD, GG, RR, false>;
+  IFN_WIDE_CASE(64, 1, 2) IFN_WIDE_CASE(64, 2, 2) IFN_WIDE_CASE(64, 4, 2) IFN_WIDE_CASE(64, 8, 2)
+  IFN_WIDE_CASE(128, 1, 2) IFN_WIDE_CASE(128, 2, 2) IFN_WIDE_CASE(128, 4, 2) IFN_WIDE_CASE(128, 8, 2)
+  IFN_WIDE_CASE(128, 1, 1) IFN_WIDE_CASE(128, 2, 1) IFN_WIDE_CASE(128, 4, 1) IFN_WIDE_CASE(128, 8, 1)
 #undef IFN_WIDE_CASE
   return nullptr;
 }
 
 bool wide_prefill_supported(int32_t hq, int32_t hkv, int32_t d) {
-  return hkv >= 1 && hq % hkv == 0 && pick_wide(d, hq / hkv, false) != nullptr;
+  return hkv >= 1 && hq % hkv == 0 && pick_wide(d, hq / hkv, 2, false) != nullptr;
 }
 
 size_t wide_prefill_ws_bytes(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
@@ -787,9 +864,9 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
                         int32_t query_start, int32_t T, int32_t hq, int32_t hkv, int32_t d, float scale_log2,
                         void* workspace, size_t workspace_bytes, const PrefillAppend& ap, int cus,
                         hipStream_t stream) {
-  WideKernel k = pick_wide(d, hq / hkv, ap.pool != nullptr);
-  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   const WidePlan p = plan_wide(T, query_start, hq, hkv, d, cus);
+  WideKernel k = pick_wide(d, hq / hkv, p.rt, ap.pool != nullptr);
+  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
   // (the fused append indexes the chunk's K and V rows with 32-bit byte offsets)
   if (ap.pool != nullptr && int64_t(T) * hkv * d * 2 >= int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
