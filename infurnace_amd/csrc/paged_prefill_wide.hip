@@ -56,9 +56,10 @@ struct WideCfg {
   static constexpr int kVBufBytes = 2 * kHalfBytes;
   static constexpr int kVInstr = 2 * kHalfInstr;     // 16-byte loads (and LDS writes) per lane per tile
   static constexpr int kVBufs = 2;                   // V tiles in LDS per wave: i and i + 1
-  // K tile in LDS: [chunk c][32 key rows] of 16-byte chunks, row r of chunk c at slot
-  // r ^ 2 (c % 8), so that a lane's MFMA fragment for K-step s sits at a constant offset of 1 KiB s
-  // from one of four lane bases, and both the 16-lane write and read passes cover all banks once.
+  // K tile in LDS: [chunk c][32 key rows] of 16-byte chunks, row r of chunk c at slot r ^ (c % 8),
+  // so that a lane's MFMA fragment for K-step s sits at a constant offset of 1 KiB s from one of
+  // four lane bases, and every 8 lanes of a 16-byte write or read (one 128-byte LDS cycle) cover
+  // the 32 banks once.
   static constexpr int kKInstr = 32 * kRowChunks / kWave;  // 16-byte loads (and writes) per lane
   static constexpr int kKBufBytes = 32 * kRowChunks * 16;
   static constexpr int kWaveBytes = kVBufs * kVBufBytes + kKBufBytes;
@@ -299,7 +300,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   }
   constexpr int kCB = C::kRowChunks / 8;  // chunk blocks per row
   uint32_t koff[C::kKInstr / 2];          // (the same for both page halves)
-  uint32_t kwr[2];                        // LDS write offsets (row blocks n / kCB even, odd)
+  uint32_t kwr;                           // LDS write offset (of load 0)
   {
     const int a = lane / 8, e = lane % 8;
 #pragma unroll
@@ -307,15 +308,14 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
       const int r = 8 * ((n / kCB) % 2) + a, c = 8 * (n % kCB) + e;
       koff[n] = uint32_t((r * int(tok_stride) + 8 * c) * 2);
     }
-#pragma unroll
-    for (int o = 0; o < 2; ++o) kwr[o] = uint32_t((e * 32 + ((8 * o + a) ^ (2 * e))) * 16);
+    kwr = uint32_t((e * 32 + (a ^ e)) * 16);
   }
   lds_u8* const vlds = (lds_u8*)(smem) + grp * C::kWaveBytes;
   lds_u8* const klds = vlds + C::kVBufs * C::kVBufBytes;
   // this lane's K fragment of K-step s (key row col, chunk 2 s + half) is at kfrag[s % 4] + 1 KiB s
   const lds_u8* kfrag[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) kfrag[j] = klds + half * 512 + (col ^ ((4 * j + 2 * half) % 16)) * 16;
+  for (int j = 0; j < 4; ++j) kfrag[j] = klds + half * 512 + (col ^ ((2 * j + half) % 8)) * 16;
   struct VTile {
     __amdgpu_buffer_rsrc_t r[2];
     uint32_t add[2];
@@ -358,8 +358,8 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   };
   auto k_store = [&](int n, u32x4 v) __attribute__((always_inline)) {
     const int rb = n / kCB, cb = n % kCB;  // row block (8 rows), chunk block (8 chunks)
-    // slot c 32 + (r ^ 2 (c % 8)) = 256 cb + 16 (rb / 2) + [e 32 + ((8 (rb % 2) + a) ^ 2 e)]
-    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(klds + kwr[rb % 2] + cb * 4096 + (rb / 2) * 256) = v;
+    // slot c 32 + (r ^ (c % 8)) = 256 cb + 8 rb + [32 e + (a ^ e)]
+    *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(klds + kwr + cb * 4096 + rb * 128) = v;
   };
   auto k_read = [&](int s) __attribute__((always_inline)) {
     return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(kfrag[s % 4] + 1024 * s);
