@@ -34,19 +34,20 @@ namespace ifn {
 
 constexpr int kWBlock = 16;    // tokens per page compiled in
 constexpr int kWTile = 32;     // keys per tile
-constexpr int kWGroups = 4;    // waves (key groups) per workgroup
-constexpr int kWThreads = kWGroups * kWave;
 constexpr int kWMaxSplit = 16;
 
-// RT row tiles of 32 query rows per wave (and per workgroup)
-template <int D, int G, int RT>
+// RT row tiles of 32 query rows per wave (and per workgroup); W waves (key groups) per workgroup
+template <int D, int G, int RT, int W>
 struct WideCfg {
+  static constexpr int kThreads = W * kWave;
   static constexpr int kRows = 32 * RT;              // query rows per workgroup
   static constexpr int kQw = kRows / G;              // queries per workgroup
   static constexpr int kKSteps = D / 16;             // MFMA K-steps over the head dims
   static constexpr int kDT = D / 32;                 // 32-dim output tiles
   static constexpr int kBlocks = RT * kDT;           // output blocks: (dim tile, row tile)
-  static constexpr int kOwned = kBlocks / kWGroups;  // blocks each wave finishes
+  // Each wave finishes kOwnU quarter blocks (4 accumulator rows of a block per lane): whole blocks
+  // p = wave + W ob when there are at least W blocks, else a run of quarters of block wave % kBlocks.
+  static constexpr int kOwnU = 4 * kBlocks / W;
   // V tile in LDS: two page halves of 16 key rows x D dims, [key][dim] as in the pool and
   // unpadded; the 16-byte chunk c of row r sits at chunk position c ^ 2 (r % 4), so the 4 rows a
   // 16-lane group reads in one transposing load fall on disjoint banks.
@@ -55,7 +56,9 @@ struct WideCfg {
   static constexpr int kHalfBytes = 16 * D * 2;
   static constexpr int kVBufBytes = 2 * kHalfBytes;
   static constexpr int kVInstr = 2 * kHalfInstr;     // 16-byte loads (and LDS writes) per lane per tile
-  static constexpr int kVBufs = 2;                   // V tiles in LDS per wave: i and i + 1
+  // V tiles in LDS per wave: i and i + 1 with 4 waves; with 8 (two per SIMD, so half the LDS
+  // each) one, rewritten with tile i + 1 once every read of tile i is issued
+  static constexpr int kVBufs = W == 8 ? 1 : 2;
   // K tile in LDS: [chunk c][32 key rows] of 16-byte chunks, row r of chunk c at slot r ^ (c % 8),
   // so that a lane's MFMA fragment for K-step s sits at a constant offset of 1 KiB s from one of
   // four lane bases, and every 8 lanes of a 16-byte write or read (one 128-byte LDS cycle) cover
@@ -63,32 +66,33 @@ struct WideCfg {
   static constexpr int kKInstr = 32 * kRowChunks / kWave;  // 16-byte loads (and writes) per lane
   static constexpr int kKBufBytes = 32 * kRowChunks * 16;
   static constexpr int kWaveBytes = kVBufs * kVBufBytes + kKBufBytes;
-  static constexpr int kTileBytes = kWGroups * kWaveBytes;
+  static constexpr int kTileBytes = W * kWaveBytes;
   // The queries, staged once per workgroup: kRows rows x D dims, chunk c of row r at c ^ (r % 8).
   static constexpr int kQBytes = kRows * D * 2;
-  static constexpr int kQInstr = kQBytes / 16 / kWThreads;  // 16-byte loads per lane
-  static constexpr int kQRowsPerWave = kRows / kWGroups;     // rows each wave stages
-  static constexpr int kMlFloats = kWGroups * RT * 32 * 2;
-  static constexpr int kMergeBytes = kMlFloats * 4 + kWGroups * kBlocks * 16 * kWave * 4;
+  static constexpr int kQInstr = kQBytes / 16 / kThreads;  // 16-byte loads per lane
+  static constexpr int kQRowsPerWave = kRows / W;          // rows each wave stages
+  static constexpr int kMlFloats = W * RT * 32 * 2;
+  static constexpr int kMergeBytes = kMlFloats * 4 + W * kBlocks * 16 * kWave * 4;
   static constexpr int kLdsBytes = kTileBytes + kQBytes > kMergeBytes ? kTileBytes + kQBytes : kMergeBytes;
   static_assert(RT == 1 || RT == 2, "one or two row tiles");
   static_assert(kQw * G == kRows, "32 RT rows per workgroup");
-  static_assert(kBlocks % kWGroups == 0, "every wave finishes the same number of blocks");
+  static_assert(W == 4 || W == 8, "4 or 8 waves");
+  static_assert((4 * kBlocks) % W == 0 && (kBlocks % W == 0 || W % kBlocks == 0), "every wave finishes the same share");
   static_assert(16 * kRowChunks % kWave == 0 && kRowChunks >= 8, "whole loads per page half; swizzle in range");
   static_assert(kRowChunks % 8 == 0 && kKInstr % 2 == 0, "K loads: 8 rows x 8 chunks each, within one page half");
-  static_assert(kQBytes % (16 * kWThreads) == 0 && kQRowsPerWave * kRowChunks == kQInstr * kWave, "Q staging");
+  static_assert(kQBytes % (16 * kThreads) == 0 && kQRowsPerWave * kRowChunks == kQInstr * kWave, "Q staging");
 };
 
 struct WidePlan {
   int64_t n_qb;
-  int rt, nsplit;
+  int rt, w, nsplit;
   size_t off_ml, off_o, bytes;
 };
 
 // Row tiles per wave: two (64 rows per workgroup, every K and V fragment feeding two MFMA chains)
 // unless the (query block, kv head) pairs of 64 rows would fill at most half the CUs; then, for
 // head dim 128, one (32 rows per workgroup), which doubles the pairs instead of splitting their
-// keys over workgroups that merge through memory.
+// keys over workgroups that merge through memory, with 8 waves (two per SIMD) in place of 4.
 // Key split: enough workgroups to cover the CUs when (query blocks x kv heads) alone does not,
 // provided every split still gets at least two tiles per key group.
 static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
@@ -96,12 +100,13 @@ static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hk
   const int g = hq / hkv;
   auto blocks = [&](int rows) { return (int64_t(T) + rows / g - 1) / (rows / g); };
   p.rt = d == 128 && blocks(64) * hkv * 2 <= cus ? 1 : 2;
+  p.w = p.rt == 1 ? 8 : 4;
   const int rows = 32 * p.rt;
   p.n_qb = blocks(rows);
   const int64_t units = p.n_qb * hkv;
   const int64_t max_tiles = (int64_t(query_start) + T + kWTile - 1) / kWTile;
   int ns = 1;
-  while (ns < kWMaxSplit && units * ns * 2 <= cus && max_tiles >= int64_t(2 * ns) * 2 * kWGroups) ns *= 2;
+  while (ns < kWMaxSplit && units * ns * 2 <= cus && max_tiles >= int64_t(2 * ns) * 2 * p.w) ns *= 2;
   if (units > kMaxTickets) ns = 1;
   p.nsplit = ns;
   const size_t slots = size_t(units) * ns;
@@ -179,12 +184,12 @@ __device__ __forceinline__ void pin_probs(f16x8 (&p)[RT][2]) {
 #endif
 }
 
-template <int D, int G, int RT, bool kAppend>
-__global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
+template <int D, int G, int RT, int W, bool kAppend>
+__global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
     const int32_t* __restrict__ table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb,
     int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap) {
-  using C = WideCfg<D, G, RT>;
+  using C = WideCfg<D, G, RT, W>;
   constexpr int kKS = C::kKSteps;
   constexpr int kDT = C::kDT;
   constexpr int kQw = C::kQw;
@@ -202,9 +207,9 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   const int q0 = qb * kQw;
   const int key_end = min(total, query_start + q0 + kQw);  // keys some row of the block sees
   const int n_tiles = int(ceil_div(key_end, kWTile));
-  auto tile_of = [&](int i) { return (i * nsplit + split) * kWGroups + grp; };
-  const int first = split * kWGroups + grp;
-  const int iters = n_tiles > first ? int(ceil_div(n_tiles - first, kWGroups * nsplit)) : 0;
+  auto tile_of = [&](int i) { return (i * nsplit + split) * W + grp; };
+  const int first = split * W + grp;
+  const int iters = n_tiles > first ? int(ceil_div(n_tiles - first, W * nsplit)) : 0;
 
   // This lane's row in each row tile: row = 32 rt + col = g * kQw + query offset.
   int my_q[RT], my_pos[RT], my_head[RT];
@@ -226,7 +231,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
 
   if constexpr (kAppend)
     wide_store_chunk(ap.pool, num_pages, table, query_start, T, num_kv_heads, D, ap.new_k, ap.new_v,
-                     int(blockIdx.x) * kWThreads + tid, int(gridDim.x) * kWThreads);
+                     int(blockIdx.x) * C::kThreads + tid, int(gridDim.x) * C::kThreads);
 
   // Page ids: a tile of 32 keys spans two pages.  Lane l of a window holds page 2 * tile + (l & 1) of
   // the wave's (l / 2)-th tile of that window (32 tiles), read with v_readlane.  A tile's K and V
@@ -558,9 +563,12 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     // MFMAs below, out of the MFMAs' shadow)
     pin_probs<RT>(pb16);
     static_assert(C::kKInstr == kKS, "one K write and load per K-step");
-    __builtin_amdgcn_sched_group_barrier(0x100, kKS, 0);  // K fragment reads
+    // K fragment reads: all first with 4 waves; two ahead of their MFMAs with 8 (registers)
+    constexpr int kAhead = W == 4 ? kKS : 2;
+    __builtin_amdgcn_sched_group_barrier(0x100, kAhead, 0);
 #pragma unroll
     for (int s = 0; s < kKS; ++s) {
+      if (s + kAhead < kKS) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
       __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);       // MFMA
       __builtin_amdgcn_sched_group_barrier(0x002, kAValu, 0);  // VALU
       if constexpr (RT == 2) __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
@@ -576,12 +584,20 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     const lds_u8* const ae = vcur + tr_even;
     const lds_u8* const ao = vcur + tr_odd;
     lds_u8* const vnext = vlds + ((i + 1) % C::kVBufs) * C::kVBufBytes;
-    // Tile i's PV MFMAs; tile i + 1's V goes to LDS (first batch) and tile i + 2's is loaded (last
-    // batch) between them.
+    // Tile i's PV MFMAs; tile i + 1's V goes to LDS (first batch; with one V buffer, the last,
+    // after every read of tile i) and tile i + 2's is loaded (last batch) between them.
     auto batch = [&](auto bc) __attribute__((always_inline)) {
       constexpr int b = decltype(bc)::value;
       pv_batch(bc, ae, ao, pb16, [&](const int pr) __attribute__((always_inline)) {
-        if constexpr (kDT == 4) {
+        if constexpr (C::kVBufs == 1) {
+          if constexpr (b == kDT / 2 - 1) {
+            constexpr int per = C::kVInstr / 4;  // V loads per MFMA pair
+#pragma unroll
+            for (int t = 0; t < per; ++t) v_store(vnext, per * pr + t, vst[per * pr + t]);
+#pragma unroll
+            for (int t = 0; t < per; ++t) vst[per * pr + t] = v_load(v2, per * pr + t);
+          }
+        } else if constexpr (kDT == 4) {
           if constexpr (b == 0) {
             v_store(vnext, 2 * pr, vst[2 * pr]);
             v_store(vnext, 2 * pr + 1, vst[2 * pr + 1]);
@@ -641,7 +657,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
       for (int s = 0; s < kKS; ++s) {
         const int rho = 32 * rt + col, c = 2 * s + half;
         qreg[rt][s] = as_h8(*reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((c ^ (rho % 8)) * 16)));
-        pin_agpr(qreg[rt][s]);
+        if constexpr (W == 4) pin_agpr(qreg[rt][s]);
       }
 #pragma unroll
     for (int n = 0; n < C::kKInstr; ++n) k_store(n, kst[n]);
@@ -651,7 +667,7 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     // and their MFMA phases together for the whole loop and queue on the CU's shared memory path.
     // Wave grp starts 6 x 64 x grp cycles late instead (a quarter of a step or so apart; measured:
     // 71.9 -> 67.4 us per config-3 layer).
-    for (int w = 0; w < grp; ++w) __builtin_amdgcn_s_sleep(6);
+    for (int w = 0; w < grp % 4; ++w) __builtin_amdgcn_s_sleep(6);
 #pragma unroll
     for (int s = 0; s < kKS; ++s) kr[s] = k_read(s);
 #pragma unroll
@@ -691,9 +707,18 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) lt[rt] = lsum[rt] + __shfl_xor(lsum[rt], 32);
   // Key-group merge: every wave writes its (m, l) and all its blocks to LDS; block p = (dim tile
-  // p / RT, row tile p % RT) is then finished by wave p % 4, from the four groups' copies in group
-  // order.  Every block a wave finishes has row tile rt_own = grp % RT.
-  const int rt_own = grp % RT;
+  // p / RT, row tile p % RT) is then finished, quarter by quarter, by the waves that own it, from
+  // the W groups' copies in group order.  Every quarter a wave finishes has row tile rt_own.
+  auto own = [&](int u, int& p, int& r4) __attribute__((always_inline)) {  // owned quarter u
+    if constexpr (C::kBlocks >= W) {
+      p = grp + W * (u / 4);
+      r4 = u % 4;
+    } else {
+      p = grp % C::kBlocks;
+      r4 = (grp / C::kBlocks) * C::kOwnU + u;
+    }
+  };
+  const int rt_own = (C::kBlocks >= W ? grp : grp % C::kBlocks) % RT;
   float* mlb = reinterpret_cast<float*>(smem);                 // [wave][rt][32][2]
   f32x4* accb = reinterpret_cast<f32x4*>(mlb + C::kMlFloats);  // [wave][block][4][lane]
   if (half == 0) {
@@ -711,42 +736,40 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
       accb[((grp * C::kBlocks + p) * 4 + r4) * kWave + lane] = f32x4{a[4 * r4], a[4 * r4 + 1], a[4 * r4 + 2], a[4 * r4 + 3]};
     }
   __syncthreads();
-  float mk[kWGroups], lk[kWGroups];
+  float mk[W], lk[W];
 #pragma unroll
-  for (int k = 0; k < kWGroups; ++k) {
+  for (int k = 0; k < W; ++k) {
     mk[k] = mlb[((k * RT + rt_own) * 32 + col) * 2];
     lk[k] = mlb[((k * RT + rt_own) * 32 + col) * 2 + 1];
   }
   float mfin = mk[0];
 #pragma unroll
-  for (int k = 1; k < kWGroups; ++k) mfin = fmaxf(mfin, mk[k]);
-  float wk[kWGroups];
+  for (int k = 1; k < W; ++k) mfin = fmaxf(mfin, mk[k]);
+  float wk[W];
 #pragma unroll
-  for (int k = 0; k < kWGroups; ++k) wk[k] = exp2_fast(mk[k] - mfin);
+  for (int k = 0; k < W; ++k) wk[k] = exp2_fast(mk[k] - mfin);
   float lfin = wk[0] * lk[0];
 #pragma unroll
-  for (int k = 1; k < kWGroups; ++k) lfin = fmaf(wk[k], lk[k], lfin);
-  f32x4 o[C::kOwned][4];  // the blocks this wave finishes: p = grp + 4 ob
+  for (int k = 1; k < W; ++k) lfin = fmaf(wk[k], lk[k], lfin);
+  f32x4 o[C::kOwnU];  // the quarters this wave finishes
 #pragma unroll
-  for (int ob = 0; ob < C::kOwned; ++ob) {
-    const int p = grp + kWGroups * ob;
+  for (int u = 0; u < C::kOwnU; ++u) {
+    int p, r4;
+    own(u, p, r4);
+    f32x4 x = accb[((0 * C::kBlocks + p) * 4 + r4) * kWave + lane];
+    f32x4 y = x * wk[0];
 #pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      f32x4 x = accb[((0 * C::kBlocks + p) * 4 + r4) * kWave + lane];
-      f32x4 y = x * wk[0];
+    for (int k = 1; k < W; ++k) {
+      x = accb[((k * C::kBlocks + p) * 4 + r4) * kWave + lane];
 #pragma unroll
-      for (int k = 1; k < kWGroups; ++k) {
-        x = accb[((k * C::kBlocks + p) * 4 + r4) * kWave + lane];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) y[e] = fmaf(wk[k], x[e], y[e]);
-      }
-      o[ob][r4] = y;
+      for (int e = 0; e < 4; ++e) y[e] = fmaf(wk[k], x[e], y[e]);
     }
+    o[u] = y;
   }
 
   if (nsplit > 1) {
-    // Cross-workgroup merge: every wave publishes its blocks of this split's partial with 16-byte
-    // device-coherent stores (lane-contiguous), waves 0 and 1 their row tile's (m, l); once all are
+    // Cross-workgroup merge: every wave publishes its quarters of this split's partial with 16-byte
+    // device-coherent stores (lane-contiguous), waves 0 .. RT - 1 their row tile's (m, l); once all are
     // acknowledged one thread takes the (query block, kv head) ticket.  The last of the nsplit
     // arrivals combines every split's partial, its own included (read back), in split order, so
     // the result does not depend on the arrival order.
@@ -761,9 +784,11 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     };
     const uint32_t ml_row = uint32_t(rt_own * 32 + col) * 8;
 #pragma unroll
-    for (int ob = 0; ob < C::kOwned; ++ob)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) st_dev4(r_o, o_off(slot, grp + kWGroups * ob, r4), o[ob][r4]);
+    for (int u = 0; u < C::kOwnU; ++u) {
+      int p, r4;
+      own(u, p, r4);
+      st_dev4(r_o, o_off(slot, p, r4), o[u]);
+    }
     if (grp < RT && half == 0) st_dev2(r_ml, uint32_t(slot * C::kRows * 8) + ml_row, f32x2{mfin, lfin});
     wait_all_mem();   // this wave's stores are acknowledged
     __syncthreads();  // ... and every other wave's
@@ -774,14 +799,12 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
     float mx = kNegBig;
     // (this split's own partial is taken from registers, not read back)
     const float m_own = mfin, l_own = lfin;
-    f32x4 mine[C::kOwned][4];
+    f32x4 mine[C::kOwnU];
 #pragma unroll
-    for (int ob = 0; ob < C::kOwned; ++ob)
-#pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
-        mine[ob][r4] = o[ob][r4];
-        o[ob][r4] = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
+    for (int u = 0; u < C::kOwnU; ++u) {
+      mine[u] = o[u];
+      o[u] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
     mx = m_own;
     for (int s2 = 0; s2 < nsplit; ++s2)
       if (s2 != split) mx = fmaxf(mx, ld_dev2(r_ml, uint32_t((pair * nsplit + s2) * C::kRows * 8) + ml_row)[0]);
@@ -795,26 +818,24 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
         if (s2 < nsplit) {
           const int64_t sl = pair * nsplit + s2;
           f32x2 ml = f32x2{m_own, l_own};
-          f32x4 x[C::kOwned][4];
+          f32x4 x[C::kOwnU];
 #pragma unroll
-          for (int ob = 0; ob < C::kOwned; ++ob)
-#pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4) x[ob][r4] = mine[ob][r4];
+          for (int u = 0; u < C::kOwnU; ++u) x[u] = mine[u];
           if (s2 != split) {  // (uniform)
             ml = ld_dev2(r_ml, uint32_t(sl * C::kRows * 8) + ml_row);
 #pragma unroll
-            for (int ob = 0; ob < C::kOwned; ++ob)
-#pragma unroll
-              for (int r4 = 0; r4 < 4; ++r4) x[ob][r4] = ld_dev4(r_o, o_off(sl, grp + kWGroups * ob, r4));
+            for (int u = 0; u < C::kOwnU; ++u) {
+              int p, r4;
+              own(u, p, r4);
+              x[u] = ld_dev4(r_o, o_off(sl, p, r4));
+            }
           }
           const float wsp = exp2_fast(ml[0] - mx);
           lfin = fmaf(wsp, ml[1], lfin);
 #pragma unroll
-          for (int ob = 0; ob < C::kOwned; ++ob)
+          for (int u = 0; u < C::kOwnU; ++u)
 #pragma unroll
-            for (int r4 = 0; r4 < 4; ++r4)
-#pragma unroll
-              for (int e = 0; e < 4; ++e) o[ob][r4][e] = fmaf(wsp, x[ob][r4][e], o[ob][r4][e]);
+            for (int e = 0; e < 4; ++e) o[u][e] = fmaf(wsp, x[u][e], o[u][e]);
         }
       }
     }
@@ -826,34 +847,33 @@ __global__ __launch_bounds__(kWThreads) void prefill_wide_kernel(
   const float inv = lfin > 0.f ? 1.f / lfin : 0.f;
   f16* orow = out + (int64_t(my_q[rt_own]) * hq + my_head[rt_own]) * D;
 #pragma unroll
-  for (int ob = 0; ob < C::kOwned; ++ob) {
-    const int dt = (grp + kWGroups * ob) / RT;
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {  // dims 32 dt + 8 r4 + 4 half + 0..3
-      const f32x4 y = o[ob][r4];
-      *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * r4 + 4 * half) =
-          f16x4{f16(y[0] * inv), f16(y[1] * inv), f16(y[2] * inv), f16(y[3] * inv)};
-    }
+  for (int u = 0; u < C::kOwnU; ++u) {  // dims 32 dt + 8 r4 + 4 half + 0..3 of block p
+    int p, r4;
+    own(u, p, r4);
+    const int dt = p / RT;
+    const f32x4 y = o[u];
+    *reinterpret_cast<f16x4*>(orow + 32 * dt + 8 * r4 + 4 * half) =
+        f16x4{f16(y[0] * inv), f16(y[1] * inv), f16(y[2] * inv), f16(y[3] * inv)};
   }
 }
 
 typedef void (*WideKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t, int32_t, int32_t,
                            int32_t, float, PrefillWorkspace, PrefillAppend);
 
-// (row tiles: 2 for every shape, 1 for head dim 128, where a wave's 4 dim tiles are 4 blocks)
-static WideKernel pick_wide(int d, int g, int rt, bool append) {
-#define IFN_WIDE_CASE(DD, GG, RR)                                                                    \
-  if (d == DD && g == GG && rt == RR)                                                                \
-    return append ? prefill_wide_kernel<DD, GG, RR, true> : prefill_wide_kernel<DD, GG, RR, false>;
-  IFN_WIDE_CASE(64, 1, 2) IFN_WIDE_CASE(64, 2, 2) IFN_WIDE_CASE(64, 4, 2) IFN_WIDE_CASE(64, 8, 2)
-  IFN_WIDE_CASE(128, 1, 2) IFN_WIDE_CASE(128, 2, 2) IFN_WIDE_CASE(128, 4, 2) IFN_WIDE_CASE(128, 8, 2)
-  IFN_WIDE_CASE(128, 1, 1) IFN_WIDE_CASE(128, 2, 1) IFN_WIDE_CASE(128, 4, 1) IFN_WIDE_CASE(128, 8, 1)
+// (row tiles and waves: 2 and 4 for every shape; 1 and 8 for head dim 128)
+static WideKernel pick_wide(int d, int g, int rt, int w, bool append) {
+#define IFN_WIDE_CASE(DD, GG, RR, WW)                                                                \
+  if (d == DD && g == GG && rt == RR && w == WW)                                                     \
+    return append ? prefill_wide_kernel<DD, GG, RR, WW, true> : prefill_wide_kernel<DD, GG, RR, WW, false>;
+  IFN_WIDE_CASE(64, 1, 2, 4) IFN_WIDE_CASE(64, 2, 2, 4) IFN_WIDE_CASE(64, 4, 2, 4) IFN_WIDE_CASE(64, 8, 2, 4)
+  IFN_WIDE_CASE(128, 1, 2, 4) IFN_WIDE_CASE(128, 2, 2, 4) IFN_WIDE_CASE(128, 4, 2, 4) IFN_WIDE_CASE(128, 8, 2, 4)
+  IFN_WIDE_CASE(128, 1, 1, 8) IFN_WIDE_CASE(128, 2, 1, 8) IFN_WIDE_CASE(128, 4, 1, 8) IFN_WIDE_CASE(128, 8, 1, 8)
 #undef IFN_WIDE_CASE
   return nullptr;
 }
 
 bool wide_prefill_supported(int32_t hq, int32_t hkv, int32_t d) {
-  return hkv >= 1 && hq % hkv == 0 && pick_wide(d, hq / hkv, 2, false) != nullptr;
+  return hkv >= 1 && hq % hkv == 0 && pick_wide(d, hq / hkv, 2, 4, false) != nullptr;
 }
 
 size_t wide_prefill_ws_bytes(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
@@ -865,7 +885,7 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
                         void* workspace, size_t workspace_bytes, const PrefillAppend& ap, int cus,
                         hipStream_t stream) {
   const WidePlan p = plan_wide(T, query_start, hq, hkv, d, cus);
-  WideKernel k = pick_wide(d, hq / hkv, p.rt, ap.pool != nullptr);
+  WideKernel k = pick_wide(d, hq / hkv, p.rt, p.w, ap.pool != nullptr);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
   // (the fused append indexes the chunk's K and V rows with 32-bit byte offsets)
@@ -879,7 +899,7 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
     ws.ml = reinterpret_cast<float*>(wsb + p.off_ml);
     ws.o = reinterpret_cast<float*>(wsb + p.off_o);
   }
-  k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(kWThreads), 0, stream>>>(
+  k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(unsigned(p.w * kWave)), 0, stream>>>(
       out, q, pool, num_pages, table, query_start, T, hkv, int(p.n_qb), p.nsplit, scale_log2, ws, ap);
   return ifn_launch_status();
 }
