@@ -1,33 +1,33 @@
-// Causal chunked-prefill paged attention with 64 query rows per wavefront (gfx950 MFMA fp16).
+// Causal chunked-prefill paged attention with 32 or 64 query rows per wavefront (gfx950 MFMA fp16).
 //
 // Same operation and entry points as paged_prefill.hip (docs/architecture.md:246; contiguous
 // semantics src/infurnace/executor/tinygrad/model.py:116-132: query row i sits at
-// start_position + i and sees keys with key_pos <= query_pos), organised so that every K and V
-// fragment feeds two MFMA chains and K never passes through LDS:
+// start_position + i and sees keys with key_pos <= query_pos):
 //
-//  * Rows.  A workgroup serves one (query block, kv head): 64 rows = 64 / G queries x the G query
-//    heads of the kv head.  Its 4 waves (one per SIMD, up to 512 registers each) are 4 key groups:
-//    wave k takes the 32-key tiles t = k, k + 4, ... (interleaved, so the causal diagonal costs
-//    every group the same) and keeps all 64 rows in registers as two 32-row MFMA tiles.  When
-//    (query blocks x kv heads) cannot cover the CUs, up to kWMaxSplit workgroups share a block's
-//    tiles and the last to finish merges their partials through the workspace.
+//  * Rows.  A workgroup serves one (query block, kv head): 32 RT rows = 32 RT / G queries x the G
+//    query heads of the kv head, held by every wave as RT 32-row MFMA tiles.  Its W waves are W key
+//    groups: wave k takes the 32-key tiles t = k, k + W, ... (interleaved, so the causal diagonal
+//    costs every group the same).  RT = 2 with W = 4 (one wave per SIMD, up to 512 registers),
+//    or, when 64-row blocks would leave CUs idle, RT = 1 with W = 8 (two waves per SIMD in 256
+//    registers each).  When (query blocks x kv heads) still cannot cover the CUs, up to kWMaxSplit
+//    workgroups share a block's tiles and the last to finish merges their partials through the
+//    workspace.
 //  * Scores, transposed: S^T = K . Q^T with v_mfma_f32_32x32x16_f16.  The A operand (32 keys x 16
-//    dims) is one key row per lane, loaded straight from the pool into registers: MFMA K-step s
-//    takes dims 16 s + 8 half .. + 7, a permutation of the head dims applied to both operands, so
-//    the two lanes of a key row read 32 contiguous bytes per load.  The B operand (the queries) is
-//    held for the whole kernel.  Each K fragment feeds both row tiles.
+//    dims) is one key row per lane: K tiles are loaded from the pool row-contiguously (8 lanes per
+//    128-byte line) and staged in the wave's LDS K buffer, from which each lane reads its fragments.
+//    MFMA K-step s takes dims 16 s + 8 half .. + 7 (a permutation of the head dims applied to both
+//    operands).  The B operand (the queries) is held for the whole kernel.
 //  * O^T += V^T . P^T: the probabilities stay in registers (a lane's 16 scores of a 32-key tile are
 //    the B operands of two K = 16 steps); V goes through registers to the wave's own LDS tile as it
 //    is in the pool, [key][dim] (16-byte chunks XOR-swizzled by row), and the A operand comes from
-//    transposing LDS reads (ds_read_b64_tr_b16).  Each V^T fragment feeds both row tiles.
+//    transposing LDS reads (ds_read_b64_tr_b16).
 //  * Pipeline: tile i + 1's scores are computed while tile i's probabilities are formed, and the
-//    next tiles' K and V loads are spread between the MFMAs; every load addresses a real row (an
-//    invalid page reads page 0).  Keys past the end or in an invalid page are masked (only in the
-//    tiles that hold such keys) and their V rows zeroed.
+//    next tiles' K and V loads are spread between the MFMAs.  Keys past the end or in an invalid
+//    page read zeros and are masked (only in the tiles that hold such keys).
 //  * Online softmax in base 2, per lane and row tile (one lane ^ 32 exchange per tile), with the
 //    lazy rescale of the running maximum (slack 2^8); row sums add the fp16 probabilities.
-//  * Epilogue: the 4 key groups merge log-sum-exp style through LDS, each wave finishing its own
-//    (dim tile, row tile) blocks; then the key-split merge and the fp16 stores.
+//  * Epilogue: the W key groups merge log-sum-exp style through LDS, each wave finishing its share
+//    of the output; then the key-split merge and the fp16 stores.
 #include "ifn_common.hpp"
 
 namespace ifn {
