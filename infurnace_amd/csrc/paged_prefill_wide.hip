@@ -90,21 +90,23 @@ struct WidePlan {
 };
 
 // Row tiles per wave: two (64 rows per workgroup, every K and V fragment feeding two MFMA chains)
-// unless the (query block, kv head) pairs of 64 rows would fill at most half the CUs; then, for
-// head dim 128, one (32 rows per workgroup), which doubles the pairs instead of splitting their
-// keys over workgroups that merge through memory, with 8 waves (two per SIMD) in place of 4.
+// unless the (query block, kv head) pairs of 64 rows would fill at most half the CUs and the key
+// range is at most 512 tiles; then, for head dim 128, one (32 rows per workgroup), which doubles
+// the pairs instead of splitting their keys over workgroups that merge through memory, with 8 waves
+// (two per SIMD) in place of 4.  (Past 16K keys the split's fixed cost is paid back: measured at
+// 512 queries, equal at 16K keys and 4% in favour of the split at 32K.)
 // Key split: enough workgroups to cover the CUs when (query blocks x kv heads) alone does not,
 // provided every split still gets at least two tiles per key group.
 static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
   WidePlan p;
   const int g = hq / hkv;
   auto blocks = [&](int rows) { return (int64_t(T) + rows / g - 1) / (rows / g); };
-  p.rt = d == 128 && blocks(64) * hkv * 2 <= cus ? 1 : 2;
+  const int64_t max_tiles = (int64_t(query_start) + T + kWTile - 1) / kWTile;
+  p.rt = d == 128 && blocks(64) * hkv * 2 <= cus && max_tiles <= 512 ? 1 : 2;
   p.w = p.rt == 1 ? 8 : 4;
   const int rows = 32 * p.rt;
   p.n_qb = blocks(rows);
   const int64_t units = p.n_qb * hkv;
-  const int64_t max_tiles = (int64_t(query_start) + T + kWTile - 1) / kWTile;
   int ns = 1;
   while (ns < kWMaxSplit && units * ns * 2 <= cus && max_tiles >= int64_t(2 * ns) * 2 * p.w) ns *= 2;
   if (units > kMaxTickets) ns = 1;
