@@ -255,6 +255,18 @@ struct PrefillAppend {
   f16* pool;  // the layer's pool (the memory the kernel reads)
 };
 
+// Shared-prefix mode of the prefill kernels: every query row sees keys [0, key_len) (no causal
+// mask) and each key split writes its result unnormalised, as the state (m, l, O), for a later
+// merge: ml[((seg * stride + split) * G + g) * 2 + {0,1}], o[((seg * stride + split) * G + g) * D + dim]
+// with seg = row * Hkv + kv head (stride >= nsplit).  No cross-workgroup merge happens here.
+// key_len == 0 is ordinary causal prefill.
+struct PrefixOut {
+  float* ml;
+  float* o;
+  int32_t key_len;
+  int32_t stride;
+};
+
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
 
 // Number of CUs of the current device (queried once per device; 0 when there is none).
@@ -290,6 +302,11 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
                         int32_t query_start, int32_t T, int32_t hq, int32_t hkv, int32_t d, float scale_log2,
                         void* workspace, size_t workspace_bytes, const PrefillAppend& ap, int cus,
                         hipStream_t stream);
+// The shared-prefix pass on that kernel (same contract as prefix_pass / prefix_pass_splits).
+int wide_prefix_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus);
+int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
+                     int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
+                     int32_t stride, int cus, hipStream_t stream);
 
 // Whole-row decode (paged_decode_rows.hip), used by the decode entry points when the token row
 // (num_kv_heads x head_dim fp16) is 2 KiB and its (head_dim, group) is compiled; and its step plan.

@@ -50,17 +50,6 @@ constexpr int kPBlock = 16;  // tokens per page compiled in
 constexpr int kMaxSplit = 16;  // workgroups per (query block, kv head) at most
 
 
-// Shared-prefix mode: every query row sees keys [0, key_len) (no causal mask) and each key split
-// writes its result unnormalised, as the state (m, l, O), for a later merge:
-// ml[((seg * stride + split) * G + g) * 2 + {0,1}], o[((seg * stride + split) * G + g) * D + dim]
-// with seg = row * Hkv + kv head (stride >= nsplit).  No cross-workgroup merge happens here.
-// key_len == 0 is ordinary causal prefill.
-struct PrefixOut {
-  float* ml;
-  float* o;
-  int32_t key_len;
-  int32_t stride;
-};
 
 
 // The chunk's K and V rows -> the pool at table[pos / 16] * 16 + pos % 16, pos = query_start + t:
@@ -631,13 +620,18 @@ static PrefillKernel pick_prefill(int d, int g, int* threads, bool append = fals
   return nullptr;
 }
 
+// (the shapes the wide kernel compiles take it: wide_prefix_splits / wide_prefix_pass)
 int prefix_pass_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus) {
+  if (wide_prefill_supported(hq, hkv, d)) return wide_prefix_splits(batch, hq, hkv, d, key_len, cus);
   return plan_prefill(batch, 0, hq, hkv, d, cus, key_len).nsplit;
 }
 
 int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
                 int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
                 int32_t stride, int cus, hipStream_t stream) {
+  if (wide_prefill_supported(hq, hkv, d))
+    return wide_prefix_pass(q, pool, num_pages, prefix_pages, key_len, batch, hq, hkv, d, scale_log2, px_ml, px_o,
+                            stride, cus, stream);
   int threads = 0;
   PrefillKernel k = pick_prefill(d, hq / hkv, &threads);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;

@@ -97,11 +97,13 @@ struct WidePlan {
 // 512 queries, equal at 16K keys and 4% in favour of the split at 32K.)
 // Key split: enough workgroups to cover the CUs when (query blocks x kv heads) alone does not,
 // provided every split still gets at least two tiles per key group.
-static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
+// key_len > 0: the shared-prefix pass (every row sees keys [0, key_len), query_start unused).
+static WidePlan plan_wide(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus,
+                          int32_t key_len = 0) {
   WidePlan p;
   const int g = hq / hkv;
   auto blocks = [&](int rows) { return (int64_t(T) + rows / g - 1) / (rows / g); };
-  const int64_t max_tiles = (int64_t(query_start) + T + kWTile - 1) / kWTile;
+  const int64_t max_tiles = ((key_len > 0 ? int64_t(key_len) : int64_t(query_start) + T) + kWTile - 1) / kWTile;
   p.rt = d == 128 && blocks(64) * hkv * 2 <= cus && max_tiles <= 512 ? 1 : 2;
   p.w = p.rt == 1 ? 8 : 4;
   const int rows = 32 * p.rt;
@@ -190,7 +192,7 @@ template <int D, int G, int RT, int W, bool kAppend>
 __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
     const int32_t* __restrict__ table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb,
-    int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap) {
+    int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap, PrefixOut px) {
   using C = WideCfg<D, G, RT, W>;
   constexpr int kKS = C::kKSteps;
   constexpr int kDT = C::kDT;
@@ -205,9 +207,12 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
   const int lane = tid % kWave;
   const int col = lane % 32, half = lane / 32;
   const int hq = num_kv_heads * G;
-  const int total = query_start + T;
+  // (shared-prefix mode: every row sees keys [0, key_len), no causal limit)
+  const bool prefix_mode = px.key_len > 0;
+  const int total = prefix_mode ? px.key_len : query_start + T;  // keys that exist
   const int q0 = qb * kQw;
-  const int key_end = min(total, query_start + q0 + kQw);  // keys some row of the block sees
+  const int key_end = prefix_mode ? total : min(total, query_start + q0 + kQw);  // keys some row sees
+  const int min_pos = prefix_mode ? total - 1 : query_start + q0;  // the last key every row sees
   const int n_tiles = int(ceil_div(key_end, kWTile));
   auto tile_of = [&](int i) { return (i * nsplit + split) * W + grp; };
   const int first = split * W + grp;
@@ -221,7 +226,7 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     const int rho = 32 * rt + col;
     my_q[rt] = q0 + rho % kQw;
     my_head[rt] = kvh * G + rho / kQw;
-    my_pos[rt] = query_start + my_q[rt];
+    my_pos[rt] = prefix_mode ? total - 1 : query_start + my_q[rt];
     q_ok[rt] = my_q[rt] < T;
   }
   __shared__ __attribute__((aligned(16))) unsigned char smem[C::kLdsBytes];
@@ -407,7 +412,7 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     tile_pages(win_k, t, tp.pa, tp.pb);
     tp.fl = tile_flags(tp.pa, tp.pb);
     tp.kt = tile_of(t) * kWTile;
-    tp.full = (tp.fl == 3) & (tp.kt + kWTile <= total) & (tp.kt + kWTile - 1 <= query_start + q0);
+    tp.full = (tp.fl == 3) & (tp.kt + kWTile <= total) & (tp.kt + kWTile - 1 <= min_pos);
     return tp;
   };
   // buffer resources of a tile's K and V
@@ -772,6 +777,20 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     o[u] = y;
   }
 
+  if (prefix_mode) {  // this split's unnormalised state of (row my_q, kv head kvh, head g)
+    if (!q_ok[rt_own]) return;
+    const int g = my_head[rt_own] - kvh * G;
+    const int64_t pslot = ((int64_t(my_q[rt_own]) * num_kv_heads + kvh) * px.stride + split) * G + g;
+    if (grp < RT && half == 0) *reinterpret_cast<f32x2*>(px.ml + pslot * 2) = f32x2{mfin, lfin};
+#pragma unroll
+    for (int u = 0; u < C::kOwnU; ++u) {  // dims 32 dt + 8 r4 + 4 half + 0..3 of block p
+      int p, r4;
+      own(u, p, r4);
+      *reinterpret_cast<f32x4*>(px.o + pslot * D + 32 * (p / RT) + 8 * r4 + 4 * half) = o[u];
+    }
+    return;
+  }
+
   if (nsplit > 1) {
     // Cross-workgroup merge: every wave publishes its quarters of this split's partial with 16-byte
     // device-coherent stores (lane-contiguous), waves 0 .. RT - 1 their row tile's (m, l); once all are
@@ -863,7 +882,7 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
 }
 
 typedef void (*WideKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t, int32_t, int32_t,
-                           int32_t, float, PrefillWorkspace, PrefillAppend);
+                           int32_t, float, PrefillWorkspace, PrefillAppend, PrefixOut);
 
 // (row tiles and waves: 2 and 4 for every shape; 1 and 8 for head dim 128)
 static WideKernel pick_wide(int d, int g, int rt, int w, bool append) {
@@ -905,7 +924,27 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
     ws.o = reinterpret_cast<float*>(wsb + p.off_o);
   }
   k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(unsigned(p.w * kWave)), 0, stream>>>(
-      out, q, pool, num_pages, table, query_start, T, hkv, int(p.n_qb), p.nsplit, scale_log2, ws, ap);
+      out, q, pool, num_pages, table, query_start, T, hkv, int(p.n_qb), p.nsplit, scale_log2, ws, ap,
+      PrefixOut{nullptr, nullptr, 0, 0});
+  return ifn_launch_status();
+}
+
+int wide_prefix_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus) {
+  return plan_wide(batch, 0, hq, hkv, d, cus, key_len).nsplit;
+}
+
+int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
+                     int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
+                     int32_t stride, int cus, hipStream_t stream) {
+  if (key_len < 1) return IFN_ERR_INVALID_ARGUMENT;
+  const WidePlan p = plan_wide(batch, 0, hq, hkv, d, cus, key_len);
+  WideKernel k = pick_wide(d, hq / hkv, p.rt, p.w, false);
+  if (k == nullptr) return IFN_ERR_UNSUPPORTED;
+  if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31 || stride < p.nsplit) return IFN_ERR_UNSUPPORTED;
+  k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(unsigned(p.w * kWave)), 0, stream>>>(
+      nullptr, q, pool, num_pages, prefix_pages, 0, batch, hkv, int(p.n_qb), p.nsplit, scale_log2,
+      PrefillWorkspace{nullptr, nullptr, nullptr}, PrefillAppend{nullptr, nullptr, nullptr},
+      PrefixOut{px_ml, px_o, key_len, stride});
   return ifn_launch_status();
 }
 
