@@ -188,6 +188,21 @@ struct DecodeWorkspace {
   float* o;         // [slot][heads][head_dim]
 };
 
+// Shared-prefix (cascade) mode: the first `pages` pages of every row at least pages * block_size
+// keys long (a cascade row) hold a prefix attended separately, for all rows at once; its states
+// are states 0 .. nstates - 2 of each segment (seg = row * Hkv + kv head):
+// ml[((seg * nstates + s) * G + g) * 2 + {0,1}], o[((seg * nstates + s) * G + g) * D + dim].  For a
+// cascade row a decode kernel streams only the pages after the prefix.  The per-segment kernel
+// leaves the segment's unnormalised state (m, l, O) in state nstates - 1 for
+// cascade_combine_kernel; the whole-row kernel merges the prefix states itself and writes fp16.
+// Shorter rows are attended in full and written directly.  pages == 0: ordinary decode.
+struct DecodePrefix {
+  float* ml;
+  float* o;
+  int32_t pages;
+  int32_t nstates;
+};
+
 // Fused append: store new_k / new_v of every active row at slot_mapping[row] (the store_kv
 // of the same step) inside the decode launch.  The attention reads the appended token from
 // new_k / new_v, not from the pool, so no ordering between the store and the reads is needed.
@@ -317,11 +332,12 @@ int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pag
                      const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
                      int blocks, hipStream_t stream);
 // prep (non-null): the fused pre-append variant; ap then carries the slots and the pool, and q is unused.
+// px (non-null): shared-prefix mode (DecodePrefix), without append or plan.
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
                        const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
-                       const DecodePrep* prep = nullptr);
+                       const DecodePrep* prep = nullptr, const DecodePrefix* px = nullptr);
 bool rows_prep_supported(int32_t hq, int32_t hkv, int32_t d);
 
 }  // namespace ifn

@@ -49,19 +49,6 @@ constexpr int kMaxWaves = 1024 * kWavesPerBlock;  // waves of a launch are cappe
 constexpr int kXcds = 8;            // MI355X: 8 XCDs, workgroups dispatched round-robin over them
 
 
-// Shared-prefix (cascade) mode: the first `pages` pages of every row at least pages * block_size
-// keys long (a cascade row) hold a prefix attended separately, for all rows at once.  For a
-// cascade row the kernel streams only the pages after the prefix and leaves each segment
-// (seg = row * Hkv + kv head) as an unnormalised state (m, l, O) in state nstates - 1 of the
-// segment: ml[((seg * nstates + nstates - 1) * G + g) * 2 + {0,1}], o[(... * G + g) * D + dim].
-// States 0 .. nstates - 2 hold the prefix's; cascade_combine_kernel merges them all.  Shorter rows
-// are attended in full and written directly.  pages == 0: ordinary decode.
-struct DecodePrefix {
-  float* ml;
-  float* o;
-  int32_t pages;
-  int32_t nstates;
-};
 
 
 // Workspace: [tickets: kTicketBytes][ml][o].  A launch of n waves publishes into at most
@@ -950,7 +937,9 @@ extern "C" int ifn_paged_decode_prep_append(void* out, const float* q, const flo
 
 namespace ifn {
 
-// Workspace of the shared-prefix entry: [tickets][decode partials][states].  The states are
+// Workspace of the shared-prefix entry: [tickets][decode partials][states].  The partials region
+// fits either decode kernel's (the per-segment kernel's, or the whole-row kernel's with one
+// workgroup per `waves / kWavesPerBlock`).  The states are
 // nstates = (prefix key splits + 1) per (segment, head): the prefix pass writes the first
 // nstates - 1, the decode kernel the last.  The tickets are the same kTicketBytes at offset 0 as in
 // every other entry point (the prefix pass and the combine take none), so one workspace zeroed
@@ -964,7 +953,8 @@ static SharedLayout shared_layout(int32_t batch, int32_t hkv, int32_t g, int32_t
                                   int32_t key_len, int cus) {
   SharedLayout L;
   size_t off_ml, off_o;
-  const size_t dec = decode_ws_layout(batch, hkv, g, d, waves, &off_ml, &off_o);
+  const size_t dec = std::max(decode_ws_layout(batch, hkv, g, d, waves, &off_ml, &off_o),
+                              rows_decode_ws_bytes(batch, hkv * g, d, int(waves / kWavesPerBlock)));
   L.nstates = prefix_pass_splits(batch, hkv * g, hkv, d, key_len, cus) + 1;  // <= kMaxStates
   const size_t states = size_t(batch) * hkv * L.nstates * g;
   L.dec_ml = off_ml;
@@ -1016,9 +1006,11 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
   const int g = num_q_heads / num_kv_heads;
-  DecodeKernel k = pick_decode(head_dim, g, DecodeMode::kCascade);
+  // the private pages on the whole-row kernel where it compiles the shape, else per segment
+  const bool rows = rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len);
+  DecodeKernel k = rows ? nullptr : pick_decode(head_dim, g, DecodeMode::kCascade);
   CombineKernel kc = pick_combine(head_dim);
-  if (k == nullptr || kc == nullptr) return IFN_ERR_UNSUPPORTED;
+  if ((!rows && k == nullptr) || kc == nullptr) return IFN_ERR_UNSUPPORTED;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);
@@ -1042,17 +1034,28 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
                        prefix_pages, key_len, batch, num_q_heads, num_kv_heads, head_dim, scale * kLog2e, px.ml,
                        px.o, L.nstates, cus, s);
   if (rc != IFN_OK) return rc;
-  // 2. the private pages (state nstates - 1 of cascade rows; other rows are written directly)
-  DecodeWorkspace ws;
-  ws.count = reinterpret_cast<uint32_t*>(wsb);
-  ws.ml = reinterpret_cast<float*>(wsb + L.dec_ml);
-  ws.o = reinterpret_cast<float*>(wsb + L.dec_o);
-  k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, s>>>(
-      static_cast<f16*>(out), static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
-      block_tables, max_pages_per_seq, seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws,
-      px, DecodeAppend{nullptr, nullptr, nullptr, nullptr});
-  rc = ifn_launch_status();
+  // 2. the private pages.  Whole-row kernel: each cascade row's own keys merged with its prefix
+  // states, to fp16.  Per-segment kernel: its state goes to state nstates - 1 (other rows are
+  // written directly), merged by the combine below.
+  if (rows) {
+    rc = rows_decode_launch(static_cast<f16*>(out), static_cast<const f16*>(query),
+                            static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
+                            seq_lens, active_mask, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
+                            scale * kLog2e, workspace, blocks, DecodeAppend{nullptr, nullptr, nullptr, nullptr}, false,
+                            nullptr, s, nullptr, &px);
+  } else {
+    DecodeWorkspace ws;
+    ws.count = reinterpret_cast<uint32_t*>(wsb);
+    ws.ml = reinterpret_cast<float*>(wsb + L.dec_ml);
+    ws.o = reinterpret_cast<float*>(wsb + L.dec_o);
+    k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, s>>>(
+        static_cast<f16*>(out), static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
+        block_tables, max_pages_per_seq, seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws,
+        px, DecodeAppend{nullptr, nullptr, nullptr, nullptr});
+    rc = ifn_launch_status();
+  }
   if (rc != IFN_OK) return rc;
+  if (rows) return IFN_OK;  // the whole-row kernel merged the prefix states itself
   // 3. merge the states of every cascade segment into the output
   const int64_t segs = int64_t(batch) * num_kv_heads;
   const int32_t cap = int32_t(std::min<int64_t>(int64_t(max_pages_per_seq) * kBlock, max_seq_len));

@@ -111,14 +111,20 @@ __device__ __forceinline__ int row_slot(const int32_t* slots, const uint8_t* act
 
 // Offsets of the rows in the split's virtual token list, into s_cum[0 .. batch] (all threads of the
 // workgroup call it; returns the total).  Row b occupies [s_cum[b], s_cum[b + 1]); its keys are the
-// last of those positions, after kRowStartCost virtual ones when it has any.
+// last of those positions, after kRowStartCost virtual ones when it has any.  Shared-prefix mode
+// (pk > 0): a row of at least pk keys (a cascade row, flagged in s_casc) streams only its keys
+// after the first pk.
 __device__ __forceinline__ int build_offsets(int* s_cum, int* s_wsum, const int32_t* seq_lens,
-                                             const uint8_t* active, int batch, int cap) {
+                                             const uint8_t* active, int batch, int cap, int pk = 0,
+                                             uint8_t* s_casc = nullptr) {
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, nwaves = blockDim.x / kWave;
   int running = 0;
   for (int base = 0; base < batch; base += blockDim.x) {
     const int i = base + tid;
     int len = i < batch ? row_keys(seq_lens, active, i, cap) : 0;
+    const bool casc = pk > 0 && len >= pk;
+    if (s_casc != nullptr && i < batch) s_casc[i] = casc ? 1 : 0;
+    if (casc) len -= pk;
     if (len > 0) len += kRowStartCost;
     int x = len;
 #pragma unroll
@@ -155,9 +161,10 @@ __device__ __forceinline__ int locate_row(const int* s_cum, int batch, int64_t t
 }
 
 // A piece: keys [a, e) of row b, in range `first` .. first + nranges - 1 of the row's ranges, and
-// the row's appended slot.
+// the row's appended slot.  off: the key position of the row's first streamed key (the prefix
+// length for a cascade row, else 0), already added to a and e.
 struct RowPiece {
-  int b, a, e, first, nranges, slot;
+  int b, a, e, first, nranges, slot, off;
 };
 
 // Step plan: one workgroup writes the header, the offsets and every range's record.
@@ -307,12 +314,18 @@ __device__ __forceinline__ u32x4 pack_h8(const float (&x)[8]) {
 // kPrep: the pre-append is fused in as well (pp): the query rows and the appended K/V rows come
 // from fp32 projections, normalised, rotated and cast here (q is unused; ap.slots / ap.pool
 // give the store's slots and pool, ap.new_k / ap.new_v are unused).
-template <int D, int G, int HKV, int S, bool kAppend, bool kStream, bool kPrep = false>
+// kCascade: shared-prefix mode (px, px.pages > 0).  A row of at least px.pages pages (a cascade
+// row) streams only the pages after them; the workgroup that finishes the row then merges its
+// state with the prefix pass's states 0 .. nstates - 2 of each segment (seg = row * Hkv + kv head:
+// ml[((seg * nstates + s) * G + g) * 2 + {0,1}], o[((seg * nstates + s) * G + g) * D + dim], written
+// by an earlier launch on the stream) and writes fp16.  A row of exactly that length is its prefix
+// states alone.  Shorter rows are attended in full.  No step plan is read in this mode.
+template <int D, int G, int HKV, int S, bool kAppend, bool kStream, bool kPrep = false, bool kCascade = false>
 __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
     const int32_t* __restrict__ block_tables, int32_t max_pages, const int32_t* __restrict__ seq_lens,
     const uint8_t* __restrict__ active, int32_t batch, int32_t max_len, float scale_log2, DecodeWorkspace ws,
-    DecodeAppend ap, const int32_t* __restrict__ plan, DecodePrep pp) {
+    DecodeAppend ap, const int32_t* __restrict__ plan, DecodePrep pp, DecodePrefix px) {
   constexpr int LPH = kWave / HKV;  // lanes per kv head
   constexpr int ROW = HKV * D;      // fp16 elements per token row
   constexpr int HQ = HKV * G;
@@ -322,6 +335,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   static_assert(ROW == 2 * kWave * 8, "a token row is two 16-byte chunks per lane");
   static_assert(G % GR == 0, "merge rounds cover the group");
   static_assert(!(kAppend && kPrep), "one append mode");
+  static_assert(!(kCascade && (kAppend || kPrep)), "shared-prefix mode has no append");
   static_assert(!kPrep || (8 * LPH == D / 2), "a lane's two chunks are rotary partners");
   __shared__ int s_cum[kRowsMaxBatch + 1];  // rows' offsets in the virtual token list
   __shared__ int s_wsum[kRowsWaves];
@@ -329,6 +343,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   __shared__ float s_l[kRowsWaves][HQ];
   __shared__ f32x4 s_acc[kRowsWaves][HKV * GR][D4];
   __shared__ uint32_t s_ticket[2];
+  __shared__ uint8_t s_casc[kCascade ? kRowsMaxBatch : 1];  // kCascade: row b is a cascade row
   // kPrep: the appended token's fp16 K and V rows, prepared at the start of its piece
   __shared__ __attribute__((aligned(16))) f16 s_app[kPrep ? 2 : 1][kPrep ? ROW : 8];
   // kPrep: the piece's fp16 query, head g of every kv head in the layout of a token row
@@ -338,10 +353,41 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
   const int cap = min(max_pages * kRowsBlock, max_len);
+  const int pk = kCascade ? max(px.pages, 0) * kRowsBlock : 0;  // prefix keys of a cascade row
   const int64_t num_slots = num_pages * kRowsBlock;
   const int64_t nb = gridDim.x;
   const int64_t blk = nb % kRowsXcds == 0 ? (blockIdx.x % kRowsXcds) * (nb / kRowsXcds) + blockIdx.x / kRowsXcds
                                           : int64_t(blockIdx.x);
+  // kCascade: dims 4 d4 .. 4 d4 + 3 of query head qh of cascade row b, from the row's own state
+  // (M, L, unnormalised O) merged with the prefix states, 4 per round trip.
+  auto cascade_out = [&](int64_t b, int qh, int d4, float M, float L, f32x4 O) __attribute__((always_inline)) {
+    const int npx = px.nstates - 1;
+    const int64_t st0 = (b * HKV + qh / G) * px.nstates * G + qh % G;  // state s: st0 + s * G
+    for (int s0 = 0; s0 < npx; s0 += 4) {
+      f32x2 mlv[4];
+      f32x4 ov[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t st = st0 + int64_t(min(s0 + u, npx - 1)) * G;
+        mlv[u] = *reinterpret_cast<const f32x2*>(px.ml + st * 2);
+        ov[u] = *reinterpret_cast<const f32x4*>(px.o + st * D + 4 * d4);
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (s0 + u < npx) {
+          const float nm = fmaxf(M, mlv[u][0]);
+          const float a = exp2_fast(M - nm), c = exp2_fast(mlv[u][0] - nm);
+          L = fmaf(L, a, c * mlv[u][1]);
+          O = f32x4{fmaf(O[0], a, c * ov[u][0]), fmaf(O[1], a, c * ov[u][1]), fmaf(O[2], a, c * ov[u][2]),
+                    fmaf(O[3], a, c * ov[u][3])};
+          M = nm;
+        }
+      }
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    *reinterpret_cast<f16x4*>(out + (b * HQ + qh) * D + 4 * d4) =
+        f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
+  };
 
   // Plan header, this range's record and its first page ids: one round trip, issued first.  The
   // record is read before the header is checked; the entry point has checked that the buffer
@@ -351,7 +397,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   int rec_n = 0;
   int ids_pl = 0, cum_pf = 0;
   const int32_t* rec = nullptr;
-  if (plan != nullptr) {
+  if (!kCascade && plan != nullptr) {
     rec = plan + plan_rec0(batch) + blk * kPlanRec;
     planned = plan[0] == kPlanMagic && plan[1] == batch && plan[4] == int(nb) && plan[6] == cap &&
               (!kApp || plan[5] != 0);
@@ -446,9 +492,23 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     if (blockIdx.x == 0) {
       for (int b0 = 0; b0 < batch; b0 += kRowsThreads) {
         const int b = b0 + tid;
-        bool z = false;
-        if (b < batch) z = b0 == 0 ? (zero_live && zero_len == 0)
-                                   : ((active == nullptr || active[b] != 0) && row_keys(seq_lens, active, b, cap) == 0);
+        bool z = false, es = false;
+        if (b < batch) {
+          const bool live = b0 == 0 ? zero_live != 0 : (active == nullptr || active[b] != 0);
+          const int len = b0 == 0 ? zero_len : row_keys(seq_lens, active, b, cap);
+          z = live && len == 0;
+          es = kCascade && pk > 0 && len == pk;
+        }
+        if constexpr (kCascade) {
+          uint64_t em = __ballot(es);
+          while (em != 0) {  // this wave's cascade rows with no key after the prefix
+            const int j = __builtin_ctzll(em);
+            em &= em - 1;
+            const int64_t row = b0 + wave * kWave + j;
+            for (int i = lane; i < HQ * D4; i += kWave)
+              cascade_out(row, i / D4, i % D4, kNegBig, 0.f, f32x4{0.f, 0.f, 0.f, 0.f});
+          }
+        }
         uint64_t mask = __ballot(z);
         while (mask != 0) {  // this wave's rows without keys, one at a time
           const int j = __builtin_ctzll(mask);
@@ -462,7 +522,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
 
   // Unplanned (or a plan for other shapes): the offsets are built here, before anything else.
   // Planned: they go to LDS at the first merge barrier, for pieces the record does not describe.
-  if (!planned) T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap);
+  if (!planned) T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap, pk, kCascade ? s_casc : nullptr);
   bool have_cum = !planned;
   auto ensure_cum = [&]() __attribute__((always_inline)) {  // planned: s_cum valid after the next barrier
     if (!have_cum) {
@@ -485,7 +545,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   auto next_piece = [&](int prev) -> RowPiece {
     RowPiece P;
     P.b = batch;
-    P.a = P.e = P.first = P.slot = 0;
+    P.a = P.e = P.first = P.slot = P.off = 0;
     P.nranges = 1;
     int b = prev < 0 ? locate_row(s_cum, batch, t0) : prev + 1;
     for (; b < batch; ++b) {
@@ -500,6 +560,11 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       P.first = int(range_of(cb));
       P.nranges = int(range_of(int64_t(cb) + len - 1)) - P.first + 1;
       P.slot = kApp ? row_slot(ap.slots, active, b, num_slots) : -1;
+      if (kCascade && s_casc[b] != 0) {
+        P.off = pk;
+        P.a += pk;
+        P.e += pk;
+      }
       break;
     }
     P.b = __builtin_amdgcn_readfirstlane(P.b);
@@ -514,6 +579,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     P.first = min(max(pc[3], 0), int(nr) - 1);
     P.nranges = min(max(pc[4], 1), int(nr) - P.first);
     P.slot = pc[5];
+    P.off = 0;
     return P;
   };
 
@@ -527,6 +593,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const int64_t v_off = num_pages * kRowsBlock * int64_t(ROW);
 
   int pend_n = 0, pend_b0 = 0, pend_b1 = 0, pend_f0 = 0, pend_f1 = 0, pend_np0 = 0, pend_np1 = 0;
+  bool pend_c0 = false, pend_c1 = false;  // kCascade: the pending row is a cascade row
 
   int prev = -1;
   for (int pi = 0;; ++pi) {  // one piece (row segment) per iteration; uniform over the workgroup
@@ -785,7 +852,9 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
           const f32x4 a4 = s_acc[w][hg][d4];
           O = f32x4{fmaf(wt, a4[0], O[0]), fmaf(wt, a4[1], O[1]), fmaf(wt, a4[2], O[2]), fmaf(wt, a4[3], O[3])};
         }
-        if (whole) {
+        if (whole && kCascade && P.off > 0) {
+          cascade_out(b, qh, d4, M, L, O);
+        } else if (whole) {
           const float inv = L > 0.f ? 1.f / L : 0.f;
           *reinterpret_cast<f16x4*>(out + (int64_t(b) * HQ + qh) * D + 4 * d4) =
               f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
@@ -798,9 +867,9 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     }
     if (!whole) {  // only the first and the last piece of a range can be split
       if (pend_n == 0) {
-        pend_b0 = b; pend_f0 = P.first; pend_np0 = P.nranges;
+        pend_b0 = b; pend_f0 = P.first; pend_np0 = P.nranges; pend_c0 = P.off > 0;
       } else {
-        pend_b1 = b; pend_f1 = P.first; pend_np1 = P.nranges;
+        pend_b1 = b; pend_f1 = P.first; pend_np1 = P.nranges; pend_c1 = P.off > 0;
       }
       ++pend_n;
     }
@@ -873,6 +942,10 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
             }
           }
         }
+        if (kCascade && (k == 0 ? pend_c0 : pend_c1)) {
+          cascade_out(b, qh, d4, M, L, O);
+          continue;
+        }
         const float inv = L > 0.f ? 1.f / L : 0.f;
         *reinterpret_cast<f16x4*>(out + (int64_t(b) * HQ + qh) * D + 4 * d4) =
             f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
@@ -885,7 +958,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
 
 typedef void (*RowsKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, const int32_t*,
                            const uint8_t*, int32_t, int32_t, float, DecodeWorkspace, DecodeAppend, const int32_t*,
-                           DecodePrep);
+                           DecodePrep, DecodePrefix);
 
 constexpr int kRowsStages = 2;
 
@@ -897,10 +970,12 @@ static RowsKernel prep_rows() {
   else return nullptr;
 }
 
-static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream, bool prep = false) {
+static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream, bool prep = false,
+                            bool cascade = false) {
 #define IFN_ROWS_CASE(DD, GG, HH)                                                                  \
   if (d == DD && g == GG && hkv == HH) {                                                           \
     if (prep) return prep_rows<DD, GG, HH>();                                                      \
+    if (cascade) return decode_rows_kernel<DD, GG, HH, kRowsStages, false, true, false, true>;     \
     if (append) return decode_rows_kernel<DD, GG, HH, kRowsStages, true, true>;                    \
     return stream ? decode_rows_kernel<DD, GG, HH, kRowsStages, false, true>                       \
                   : decode_rows_kernel<DD, GG, HH, kRowsStages, false, false>;                     \
@@ -943,8 +1018,9 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
                        const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
-                       const DecodePrep* prep) {
-  RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached, prep != nullptr);
+                       const DecodePrep* prep, const DecodePrefix* px) {
+  if (px != nullptr && (ap.pool != nullptr || prep != nullptr)) return IFN_ERR_UNSUPPORTED;
+  RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached, prep != nullptr, px != nullptr);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   size_t off_ml, off_o;
   rows_ws_layout(batch, hq, d, blocks, &off_ml, &off_o);
@@ -954,9 +1030,10 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
   ws.ml = reinterpret_cast<float*>(wsb + off_ml);
   ws.o = reinterpret_cast<float*>(wsb + off_o);
   const DecodePrep pp = prep != nullptr ? *prep : DecodePrep{};
+  const DecodePrefix pf = px != nullptr ? *px : DecodePrefix{nullptr, nullptr, 0, 0};
   k<<<dim3(unsigned(blocks)), dim3(kRowsThreads), 0, stream>>>(out, q, pool, num_pages, block_tables, max_pages,
                                                                 seq_lens, active, batch, max_len, scale_log2, ws, ap,
-                                                                plan, pp);
+                                                                px != nullptr ? nullptr : plan, pp, pf);
   return ifn_launch_status();
 }
 
