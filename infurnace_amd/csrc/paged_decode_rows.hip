@@ -359,19 +359,29 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const int64_t blk = nb % kRowsXcds == 0 ? (blockIdx.x % kRowsXcds) * (nb / kRowsXcds) + blockIdx.x / kRowsXcds
                                           : int64_t(blockIdx.x);
   // kCascade: dims 4 d4 .. 4 d4 + 3 of query head qh of cascade row b, from the row's own state
-  // (M, L, unnormalised O) merged with the prefix states, 4 per round trip.
-  auto cascade_out = [&](int64_t b, int qh, int d4, float M, float L, f32x4 O) __attribute__((always_inline)) {
+  // (M, L, unnormalised O) merged with the prefix states, 4 per round trip.  The first 4 are loaded
+  // by px_load beforehand (into mlv / ov), so that their round trip overlaps the row's own merge.
+  struct PxBatch {
+    f32x2 ml[4];
+    f32x4 o[4];
+  };
+  auto px_load = [&](int64_t b, int qh, int d4, int s0, PxBatch& pb) __attribute__((always_inline)) {
     const int npx = px.nstates - 1;
     const int64_t st0 = (b * HKV + qh / G) * px.nstates * G + qh % G;  // state s: st0 + s * G
-    for (int s0 = 0; s0 < npx; s0 += 4) {
-      f32x2 mlv[4];
-      f32x4 ov[4];
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int64_t st = st0 + int64_t(min(s0 + u, npx - 1)) * G;
-        mlv[u] = *reinterpret_cast<const f32x2*>(px.ml + st * 2);
-        ov[u] = *reinterpret_cast<const f32x4*>(px.o + st * D + 4 * d4);
-      }
+    for (int u = 0; u < 4; ++u) {
+      const int64_t st = st0 + int64_t(min(s0 + u, npx - 1)) * G;
+      pb.ml[u] = *reinterpret_cast<const f32x2*>(px.ml + st * 2);
+      pb.o[u] = *reinterpret_cast<const f32x4*>(px.o + st * D + 4 * d4);
+    }
+  };
+  auto cascade_out = [&](int64_t b, int qh, int d4, float M, float L, f32x4 O, PxBatch& pb)
+                         __attribute__((always_inline)) {
+    const int npx = px.nstates - 1;
+    for (int s0 = 0; s0 < npx; s0 += 4) {
+      if (s0 > 0) px_load(b, qh, d4, s0, pb);
+      const f32x2* mlv = pb.ml;
+      const f32x4* ov = pb.o;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         if (s0 + u < npx) {
@@ -505,8 +515,11 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
             const int j = __builtin_ctzll(em);
             em &= em - 1;
             const int64_t row = b0 + wave * kWave + j;
-            for (int i = lane; i < HQ * D4; i += kWave)
-              cascade_out(row, i / D4, i % D4, kNegBig, 0.f, f32x4{0.f, 0.f, 0.f, 0.f});
+            for (int i = lane; i < HQ * D4; i += kWave) {
+              PxBatch pb;
+              px_load(row, i / D4, i % D4, 0, pb);
+              cascade_out(row, i / D4, i % D4, kNegBig, 0.f, f32x4{0.f, 0.f, 0.f, 0.f}, pb);
+            }
           }
         }
         uint64_t mask = __ballot(z);
@@ -836,6 +849,8 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       for (int idx = tid; idx < HKV * GR * D4; idx += kRowsThreads) {
         const int hg = idx / D4, d4 = idx % D4;
         const int qh = (hg / GR) * G + r * GR + hg % GR;
+        PxBatch pb;
+        if (kCascade && whole && P.off > 0) px_load(b, qh, d4, 0, pb);
         float mw[kRowsWaves];
         float M = kNegBig;
 #pragma unroll
@@ -853,7 +868,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
           O = f32x4{fmaf(wt, a4[0], O[0]), fmaf(wt, a4[1], O[1]), fmaf(wt, a4[2], O[2]), fmaf(wt, a4[3], O[3])};
         }
         if (whole && kCascade && P.off > 0) {
-          cascade_out(b, qh, d4, M, L, O);
+          cascade_out(b, qh, d4, M, L, O, pb);
         } else if (whole) {
           const float inv = L > 0.f ? 1.f / L : 0.f;
           *reinterpret_cast<f16x4*>(out + (int64_t(b) * HQ + qh) * D + 4 * d4) =
@@ -898,6 +913,9 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       const int gbase = lane & ~(GL - 1), gj = lane - gbase;
       for (int idx = tid; idx < HQ * D4; idx += kRowsThreads) {
         const int qh = idx / D4, d4 = idx % D4;
+        const bool casc = kCascade && (k == 0 ? pend_c0 : pend_c1);
+        PxBatch pb;
+        if (casc) px_load(b, qh, d4, 0, pb);  // with the partial states' first round trip
         float M = kNegBig, L = 0.f;
         f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
         for (int j0 = 0; j0 < np; j0 += GL) {
@@ -942,8 +960,8 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
             }
           }
         }
-        if (kCascade && (k == 0 ? pend_c0 : pend_c1)) {
-          cascade_out(b, qh, d4, M, L, O);
+        if (casc) {
+          cascade_out(b, qh, d4, M, L, O, pb);
           continue;
         }
         const float inv = L > 0.f ? 1.f / L : 0.f;
