@@ -82,6 +82,21 @@ def test_short_rows_inactive_rows_and_padding(dev):
     assert bool((out[7] == 0).all()), "an active row with no keys must be zero"
 
 
+@pytest.mark.parametrize("hq", [8, 16, 32])
+def test_rows_at_prefix_length_only(dev, hq):
+    """Every cascade row is exactly the prefix: no private key in the call, so the decode's token
+    list is empty and each output is the prefix states alone; then the same with rows shorter than
+    the prefix beside them (attended in full)."""
+    say(f"shared-prefix rows at the prefix length only hq={hq}")
+    rng = np.random.default_rng(40 + hq)
+    for suffix, short in (([0] * 6, []), ([0, 0, 0, 0, 0], [(1, 17), (3, 1)])):
+        pool, table, lens, q, prefix = _shared(rng, 9, suffix, hq, 8, 128, short_rows=short)
+        args = (to_dev(q, dev), to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev), None)
+        out = paged_attention(*args, shared_prefix_pages=to_dev(prefix, dev))
+        assert_attn_close(out, oracle.paged_attention(q, pool, table, lens), f"short rows {short}")
+        assert_attn_close(out, paged_attention(*args).cpu().numpy(), "vs ifn_paged_decode")
+
+
 def test_deterministic_and_workspace_reuse(dev):
     """Repeated calls are bit-identical; one workspace serves changing shapes."""
     say("shared-prefix determinism + workspace reuse")
