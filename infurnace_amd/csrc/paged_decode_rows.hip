@@ -31,6 +31,9 @@
 //    (row, workgroup) leaves the CU.  A row held by one workgroup is written directly; a row split
 //    over several workgroups is merged by the workgroup that arrives last (device-coherent
 //    16-byte state stores, one ticket per row, taken once at the end of the range).
+//  * Shared-prefix mode (kCascade): rows that begin with a prefix already attended by the prefix
+//    pass stream only their own pages, and the workgroup that finishes such a row merges the
+//    prefix pass's states into it before writing fp16.
 //  * Optional step plan (decode_plan_kernel): the split depends only on the lengths, the tables
 //    and the appended slots, which every layer of a decode step shares.  Built once per step, the
 //    plan holds the rows' offsets in the token list and, per range, its first pieces and first
@@ -359,8 +362,8 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const int64_t blk = nb % kRowsXcds == 0 ? (blockIdx.x % kRowsXcds) * (nb / kRowsXcds) + blockIdx.x / kRowsXcds
                                           : int64_t(blockIdx.x);
   // kCascade: dims 4 d4 .. 4 d4 + 3 of query head qh of cascade row b, from the row's own state
-  // (M, L, unnormalised O) merged with the prefix states, 4 per round trip.  The first 4 are loaded
-  // by px_load beforehand (into mlv / ov), so that their round trip overlaps the row's own merge.
+  // (M, L, unnormalised O) merged with the prefix states, 4 per round trip.  The caller loads the
+  // first 4 into pb with px_load before the row's own merge, so that their round trip overlaps it.
   struct PxBatch {
     f32x2 ml[4];
     f32x4 o[4];
