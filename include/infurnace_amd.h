@@ -233,10 +233,12 @@ size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num
  * ifn_paged_decode for a batch whose rows share leading pages (a prefix-cache
  * hit): prefix_pages[0 .. shared_pages) are pages that every row of at least
  * shared_pages * block_size keys holds, in that order, at the start of its
- * block table.  Three launches on `stream`: the shared pages are read once for
- * all rows (an MFMA pass of every row's queries over them, split over keys),
- * each row streams only its own pages, and a combine merges the partial
- * softmax states per (row, kv head).  Same arguments, output and rules as
+ * block table.  Launches on `stream`: the shared pages are read once for all
+ * rows (an MFMA pass of every row's queries over them, split over keys), then
+ * each row streams only its own pages and is merged with the shared pages'
+ * partial softmax states -- inside that decode launch when the token row
+ * (num_kv_heads x head_dim fp16) is 2 KiB, else by a third, combine launch per
+ * (row, kv head).  Same arguments, output and rules as
  * ifn_paged_decode otherwise; rows shorter than the prefix are attended in
  * full through their own table.  shared_pages == 0 is ifn_paged_decode with
  * cached page loads, for batches whose rows share pages anywhere in their
