@@ -595,6 +595,9 @@ def main() -> int:
     ap.add_argument("--profile-pass", action="store_true",
                     help="short run for rocprofv3 counter passes: no CPU baseline, no prefill leg, plus one "
                          "1 GiB elementwise copy (torch.neg) whose FETCH/WRITE counters calibrate HBM bytes")
+    ap.add_argument("--config5-only", action="store_true",
+                    help="counter runs of the shared-prefix path: only the config-5 legs (with churn, then "
+                         "without) and the 1 GiB calibration copy; prints their JSON object")
     args = ap.parse_args()
     if args.profile_pass:
         args.no_cpu_baseline = True
@@ -611,6 +614,20 @@ def main() -> int:
     lib = _capi.lib()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.config5_only:
+        hip5 = HipEvents()
+        stream5 = torch.cuda.current_stream(dev).cuda_stream
+        g5 = torch.Generator(device=dev).manual_seed(workloads.config5().seed)
+        res = run_config5_churn(lib, hip5, dev, g5, stream5, steps=2)
+        torch.cuda.empty_cache()
+        res["no_churn"] = run_decode_config(lib, hip5, dev, g5, stream5, workloads.config5(), layers=36, reps=1)
+        torch.cuda.empty_cache()
+        src = torch.empty(1 << 29, dtype=torch.float16, device=dev).normal_(generator=g5)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)  # reads 1 GiB, writes 1 GiB: the counters' calibration kernel
+        torch.cuda.synchronize()
+        print(json.dumps({"config5": res}), flush=True)
+        return 0
     w = workloads.config2()
     L, B, hq, hkv, d, P = w.num_layers, w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim, w.num_pages
     g = torch.Generator(device=dev).manual_seed(w.seed)
