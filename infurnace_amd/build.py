@@ -41,6 +41,10 @@ DEVICE_FLAGS = [
 # that are never NaN (masked keys are -inf), so fmaxf needs no NaN-quieting of its operands.
 FILE_FLAGS = {
     "paged_prefill_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
+    # The whole-row decode kernel's first nine arguments (plan, pool, tables, query, sizes, grid) are
+    # preloaded into scalar registers at dispatch, so its first loads (the step plan) do not wait
+    # for the kernel-argument loads.
+    "paged_decode_rows.hip": ["-mllvm", "-amdgpu-kernarg-preload-count=9"],
 }
 
 

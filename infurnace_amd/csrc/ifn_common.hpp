@@ -20,6 +20,7 @@ typedef short v4i16 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kWave = 64;          // CDNA wavefront width
 constexpr float kLog2e = 1.4426950408889634f;
@@ -179,13 +180,17 @@ __device__ __forceinline__ bool wave_arrive_last(uint32_t* counter, uint32_t las
 __device__ __forceinline__ void reset_ticket(uint32_t* counter) {
   __hip_atomic_store(counter, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// A ticket's current count, read at the device coherence point (no increment).
+__device__ __forceinline__ uint32_t ld_ticket(const uint32_t* counter) {
+  return __hip_atomic_load(const_cast<uint32_t*>(counter), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
 
 // Split-KV workspace of the decode kernels: tickets (zero between calls), then the partial
 // states (m in log2 units, l) and unnormalised outputs of split segments.
 struct DecodeWorkspace {
   uint32_t* count;  // one ticket per segment; every call returns the tickets it used to zero
   float* ml;        // [slot][heads][2]
-  float* o;         // [slot][heads][head_dim]
+  float* o;         // [slot][heads][head_dim]: fp32 O (per-segment kernel) or fp16 O / l (whole-row kernel)
 };
 
 // Shared-prefix (cascade) mode: the first `pages` pages of every row at least pages * block_size

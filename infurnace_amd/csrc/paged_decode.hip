@@ -783,10 +783,9 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
   }
   if (batch == 0) return IFN_OK;
   const int blocks = decode_blocks();
-  size_t off_ml, off_o;
-  const size_t need = rows ? rows_decode_ws_bytes(batch, num_q_heads, head_dim, blocks)
-                           : decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim,
-                                              int64_t(blocks) * kWavesPerBlock, &off_ml, &off_o);
+  // the size ifn_paged_decode_workspace_bytes reports is the requirement, whichever kernel runs
+  const size_t need = ifn_paged_decode_workspace_bytes(batch, num_q_heads, num_kv_heads, head_dim, block_size,
+                                                       max_seq_len);
   if (workspace == nullptr || workspace_bytes < need) return IFN_ERR_WORKSPACE;
   IFN_CHECK_ALIGN16(workspace);
   if (device_cu_count() < 1) return IFN_ERR_HIP;
@@ -802,6 +801,9 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
                               scale * kLog2e, workspace, blocks, ap, cached, static_cast<const int32_t*>(plan),
                               reinterpret_cast<hipStream_t>(stream), prep);
   }
+  size_t off_ml, off_o;
+  decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim, int64_t(blocks) * kWavesPerBlock,
+                   &off_ml, &off_o);
   DecodeWorkspace ws;
   uint8_t* wsb = static_cast<uint8_t*>(workspace);
   ws.count = reinterpret_cast<uint32_t*>(wsb);

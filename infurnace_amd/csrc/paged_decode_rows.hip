@@ -87,7 +87,9 @@ static inline size_t plan_words(int32_t batch, int blocks) { return size_t(plan_
 
 // Workspace: [tickets: kTicketBytes][ml][o].  Slot = row + range index: the workgroups holding a
 // row are consecutive ranges, so (row, range) -> row + range is unique and below batch + ranges.
-// A split state is (m, l) and the unnormalised output O, in fp32.
+// A split state is (m, l) in fp32 and the normalised output O / l in fp16 (a convex combination of
+// value rows, so fp16 keeps it to a relative 2^-11): the last arrival of a long row reads every
+// state of it, and halving the bytes it reads halves that step.
 static inline size_t rows_ws_layout(int32_t batch, int32_t hq, int32_t d, int64_t ranges, size_t* off_ml,
                                     size_t* off_o) {
   const size_t slots = size_t(batch) + size_t(ranges);
@@ -95,7 +97,7 @@ static inline size_t rows_ws_layout(int32_t batch, int32_t hq, int32_t d, int64_
   *off_ml = off;
   off = align256(off + slots * hq * 2 * sizeof(float));
   *off_o = off;
-  off = align256(off + slots * hq * d * sizeof(float));
+  off = align256(off + slots * hq * d * sizeof(uint16_t));
   return off;
 }
 
@@ -324,11 +326,14 @@ __device__ __forceinline__ u32x4 pack_h8(const float (&x)[8]) {
 // by an earlier launch on the stream) and writes fp16.  A row of exactly that length is its prefix
 // states alone.  Shorter rows are attended in full.  No step plan is read in this mode.
 template <int D, int G, int HKV, int S, bool kAppend, bool kStream, bool kPrep = false, bool kCascade = false>
+// The arguments the first loads depend on come first (plan, pool, tables, query, the sizes and the
+// grid), so that they can be preloaded into scalar registers at dispatch.  nb is gridDim.x.
 __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
-    f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
-    const int32_t* __restrict__ block_tables, int32_t max_pages, const int32_t* __restrict__ seq_lens,
-    const uint8_t* __restrict__ active, int32_t batch, int32_t max_len, float scale_log2, DecodeWorkspace ws,
-    DecodeAppend ap, const int32_t* __restrict__ plan, DecodePrep pp, DecodePrefix px) {
+    const int32_t* __restrict__ plan, const f16* __restrict__ pool, const int32_t* __restrict__ block_tables,
+    const f16* __restrict__ q, int32_t batch, int32_t max_pages, int32_t max_len, int32_t nb_arg,
+    int64_t num_pages, f16* __restrict__ out, const int32_t* __restrict__ seq_lens,
+    const uint8_t* __restrict__ active, float scale_log2, DecodeWorkspace ws, DecodeAppend ap, DecodePrep pp,
+    DecodePrefix px) {
   constexpr int LPH = kWave / HKV;  // lanes per kv head
   constexpr int ROW = HKV * D;      // fp16 elements per token row
   constexpr int HQ = HKV * G;
@@ -358,9 +363,10 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const int cap = min(max_pages * kRowsBlock, max_len);
   const int pk = kCascade ? max(px.pages, 0) * kRowsBlock : 0;  // prefix keys of a cascade row
   const int64_t num_slots = num_pages * kRowsBlock;
-  const int64_t nb = gridDim.x;
-  const int64_t blk = nb % kRowsXcds == 0 ? (blockIdx.x % kRowsXcds) * (nb / kRowsXcds) + blockIdx.x / kRowsXcds
-                                          : int64_t(blockIdx.x);
+  const int64_t nb = nb_arg;
+  // XCD remap, as a select (a branch here would make the first kernel-argument loads wait apart)
+  const int bid = int(blockIdx.x), nbi = nb_arg;
+  const int64_t blk = (nbi % kRowsXcds) == 0 ? (bid % kRowsXcds) * (nbi / kRowsXcds) + bid / kRowsXcds : bid;
   // kCascade: dims 4 d4 .. 4 d4 + 3 of query head qh of cascade row b, from the row's own state
   // (M, L, unnormalised O) merged with the prefix states, 4 per round trip.  The caller loads the
   // first 4 into pb with px_load before the row's own merge, so that their round trip overlaps it.
@@ -402,22 +408,29 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
   };
 
-  // Plan header, this range's record and its first page ids: one round trip, issued first.  The
-  // record is read before the header is checked; the entry point has checked that the buffer
-  // holds a record for every workgroup, so the read stays inside it.
+  // Plan header, this range's record (its piece count and first piece) and its first page ids: one
+  // round trip, issued first.  Every word is loaded before any is tested (the header check is a
+  // bitwise and, not a chain of dependent loads).  The record is read before the header is checked;
+  // the entry point has checked that the buffer holds a record for every workgroup and is 16-byte
+  // aligned, so the reads stay inside it.
   bool planned = false;
   int64_t T = 0;
   int rec_n = 0;
   int ids_pl = 0, cum_pf = 0;
+  i32x4 rec_a = i32x4{0, 0, 0, 0}, rec_b = i32x4{0, 0, 0, 0};  // rec[0 .. 7]: pieces, piece 0 (6 words), -
   const int32_t* rec = nullptr;
   if (!kCascade && plan != nullptr) {
     rec = plan + plan_rec0(batch) + blk * kPlanRec;
-    planned = plan[0] == kPlanMagic && plan[1] == batch && plan[4] == int(nb) && plan[6] == cap &&
-              (!kApp || plan[5] != 0);
-    T = plan[3];
-    rec_n = rec[0];
+    const i32x4 h0 = *reinterpret_cast<const i32x4*>(plan);      // magic, batch, ranges, T
+    const i32x4 h1 = *reinterpret_cast<const i32x4*>(plan + 4);  // grid, slots given, cap, 0
+    rec_a = *reinterpret_cast<const i32x4*>(rec);
+    rec_b = *reinterpret_cast<const i32x4*>(rec + 4);
     ids_pl = rec[64 + lane];
     cum_pf = plan[kPlanHdr + min(tid, batch)];
+    planned = (h0[0] == kPlanMagic) & (h0[1] == batch) & (h1[0] == int(nb)) & (h1[2] == cap) &
+              (!kApp | (h1[1] != 0));
+    T = h0[3];
+    rec_n = rec_a[0];
   }
 
   // Fused append: 16-byte chunks of every appended K and V row, spread over the grid.  No wave of
@@ -443,16 +456,17 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       app_slot = row_slot(ap.slots, active, int(app_first / (2 * kAppChunks)), num_slots);
     }
   }
-  // Active rows with no keys get zeros (workgroup 0, at its end); their lengths are requested now.
-  int zero_len = 1, zero_live = 0;
+  // Active rows with no keys get zeros (workgroup 0, at its end); their lengths and flags are
+  // requested now and only tested there, so nothing waits for them at launch.
+  int zero_sl = 1, zero_act = 0;
   if (blockIdx.x == 0 && tid < batch) {
-    zero_len = row_keys(seq_lens, active, tid, cap);
-    zero_live = active == nullptr || active[tid] != 0;
+    zero_sl = seq_lens[tid];
+    zero_act = active != nullptr ? int(active[tid]) : 1;
   }
   // kPrep: this wave's first item of the fallback store below, looked up at launch so that the end
   // of the kernel does not wait on it.
-  const int64_t fb_first = int64_t(blockIdx.x) + int64_t(gridDim.x) * (kRowsWaves - 1 - wave);
-  const int64_t fb_step = int64_t(gridDim.x) * kRowsWaves;
+  const int64_t fb_first = int64_t(blockIdx.x) + nb * (kRowsWaves - 1 - wave);
+  const int64_t fb_step = nb * kRowsWaves;
   auto fb_item = [&](int64_t it, int& pos, int& slot) __attribute__((always_inline)) -> bool {
     const int b = int(it >> 1);
     pos = pp.positions[b];
@@ -496,8 +510,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         f16* d0 = app_dst(app_first, app_slot);
         if (d0 != nullptr) st16(d0, app_data);
       }
-      for (int64_t it = app_first + int64_t(gridDim.x) * kRowsThreads; it < app_items;
-           it += int64_t(gridDim.x) * kRowsThreads) {
+      for (int64_t it = app_first + nb * kRowsThreads; it < app_items; it += nb * kRowsThreads) {
         f16* d = app_dst(it, row_slot(ap.slots, active, int(it / (2 * kAppChunks)), num_slots));
         if (d != nullptr) st16(d, ld16(app_src(it)));
       }
@@ -507,8 +520,8 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         const int b = b0 + tid;
         bool z = false, es = false;
         if (b < batch) {
-          const bool live = b0 == 0 ? zero_live != 0 : (active == nullptr || active[b] != 0);
-          const int len = b0 == 0 ? zero_len : row_keys(seq_lens, active, b, cap);
+          const bool live = b0 == 0 ? zero_act != 0 : (active == nullptr || active[b] != 0);
+          const int len = b0 == 0 ? (zero_act != 0 ? max(0, min(zero_sl, cap)) : 0) : row_keys(seq_lens, active, b, cap);
           z = live && len == 0;
           es = kCascade && pk > 0 && len == pk;
         }
@@ -587,7 +600,14 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     return P;
   };
   auto plan_piece = [&](int p) -> RowPiece {  // piece p < kPlanPieces of the record, clamped to the call
-    const int32_t* pc = rec + 1 + 6 * p;
+    int pc[6];
+    if (p == 0) {  // loaded with the header
+      pc[0] = rec_a[1]; pc[1] = rec_a[2]; pc[2] = rec_a[3];
+      pc[3] = rec_b[0]; pc[4] = rec_b[1]; pc[5] = rec_b[2];
+    } else {
+#pragma unroll
+      for (int j = 0; j < 6; ++j) pc[j] = rec[1 + 6 * p + j];
+    }
     RowPiece P;
     P.b = min(max(pc[0], 0), batch - 1);
     P.a = min(max(pc[1], 0), cap - 1);
@@ -599,10 +619,90 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     return P;
   };
 
-  // split partials: O [slot][HQ][D] and (m, l) [slot][HQ][2], slot < batch + gridDim.x
-  const uint32_t n_slots = uint32_t(batch) + gridDim.x;
-  const __amdgpu_buffer_rsrc_t r_o = make_rsrc(ws.o, n_slots * HQ * D * 4u);
+  // split partials: O [slot][HQ][D] and (m, l) [slot][HQ][2], slot < batch + grid
+  const uint32_t n_slots = uint32_t(batch) + uint32_t(nb);
+  const __amdgpu_buffer_rsrc_t r_o = make_rsrc(ws.o, n_slots * HQ * D * 2u);
   const __amdgpu_buffer_rsrc_t r_ml = make_rsrc(ws.ml, n_slots * HQ * 2u * 4u);
+
+  // Log-sum-exp merge of a split row's np states (slots slot0 .. slot0 + np - 1, in range order)
+  // for query head qh, dims 4 d4 .. 4 d4 + 3.  The D / 4 lanes of a query head (a lane group) share
+  // its (m, l) loads: lane j of the group loads state j's, the group reduces the maximum and the
+  // weights, and every lane reads a state's weight from its loader with a lane shuffle.  A lane
+  // issues one 16-byte O load per state, kMergeBatch states per round trip; merge_issue sends the
+  // first round trip (so that a caller can overlap it with other work), merge_finish the rest and
+  // the arithmetic.  Only the cnt states that exist are loaded (cnt is uniform): the merging CU's
+  // own bandwidth bounds this step, at Hq * D * 4 bytes per state.
+  constexpr int GL = D4 < kWave ? D4 : kWave;  // lanes sharing a query head
+  const int gbase = lane & ~(GL - 1), gj = lane - gbase;
+  struct MergeLd {
+    f32x2 ml;
+    f32x2 o[kMergeBatch];  // 4 fp16 dims of O / l
+  };
+  auto ml_off = [&](int64_t s, int qh) { return uint32_t((s * HQ + qh) * 2 * 4); };
+  auto o_off = [&](int64_t s, int qh, int d4) { return uint32_t(((s * HQ + qh) * D + 4 * d4) * 2); };
+  auto merge_issue = [&](int64_t slot0, int np, int qh, int d4, MergeLd& ld) __attribute__((always_inline)) {
+    const int cnt = min(GL, np);
+    ld.ml = ld_dev2(r_ml, ml_off(slot0 + min(gj, cnt - 1), qh));
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      ld.o[u] = f32x2{0.f, 0.f};
+      if (u < cnt) ld.o[u] = ld_dev2(r_o, o_off(slot0 + u, qh, d4));
+    }
+  };
+  auto merge_finish = [&](int64_t slot0, int np, int qh, int d4, MergeLd& ld, float& M, float& L, f32x4& O)
+                          __attribute__((always_inline)) {
+    for (int j0 = 0; j0 < np; j0 += GL) {
+      const int cnt = min(GL, np - j0);
+      if (j0 > 0) {
+        ld.ml = ld_dev2(r_ml, ml_off(slot0 + j0 + min(gj, cnt - 1), qh));
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u)
+          if (u < cnt) ld.o[u] = ld_dev2(r_o, o_off(slot0 + j0 + u, qh, d4));
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      const f32x2 ml = ld.ml;
+      const float mj = gj < cnt ? ml[0] : kNegBig;
+      float gm = mj;
+#pragma unroll
+      for (int o = 1; o < GL; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
+      const float nm = fmaxf(M, gm);
+      const float sc = exp2_fast(M - nm);
+      O = f32x4{O[0] * sc, O[1] * sc, O[2] * sc, O[3] * sc};
+      M = nm;
+      // state j's weight in the sum, applied to its l and to its O / l
+      const float wl = gj < cnt ? exp2_fast(mj - M) * ml[1] : 0.f;
+      float ls = wl;
+#pragma unroll
+      for (int o = 1; o < GL; o <<= 1) ls += __shfl_xor(ls, o);
+      L = fmaf(L, sc, ls);
+      for (int u0 = 0; u0 < cnt; u0 += kMergeBatch) {
+        if (u0 > 0) {
+#pragma unroll
+          for (int u = 0; u < kMergeBatch; ++u)
+            if (u0 + u < cnt) ld.o[u] = ld_dev2(r_o, o_off(slot0 + j0 + u0 + u, qh, d4));
+        }
+#pragma unroll
+        for (int u = 0; u < kMergeBatch; ++u) {
+          const float w = __shfl(wl, gbase + min(u0 + u, cnt - 1));
+          const f16x4 oh = __builtin_bit_cast(f16x4, ld.o[u]);
+          if (u0 + u < cnt)
+            O = f32x4{fmaf(w, float(oh[0]), O[0]), fmaf(w, float(oh[1]), O[1]), fmaf(w, float(oh[2]), O[2]),
+                      fmaf(w, float(oh[3]), O[3])};
+        }
+      }
+    }
+  };
+  // A merged row's output: fp16, or (cascade rows) merged with the prefix states first.
+  auto write_row = [&](int64_t b, int qh, int d4, float M, float L, f32x4 O, bool casc, PxBatch& pb)
+                       __attribute__((always_inline)) {
+    if (kCascade && casc) {
+      cascade_out(b, qh, d4, M, L, O, pb);
+      return;
+    }
+    const float inv = L > 0.f ? 1.f / L : 0.f;
+    *reinterpret_cast<f16x4*>(out + (b * HQ + qh) * D + 4 * d4) =
+        f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
+  };
 
   const int hd = lane / LPH, col = lane % LPH;
   const int off0 = hd * D + 8 * col, off1 = off0 + 8 * LPH;  // this lane's two chunks of a token row
@@ -610,6 +710,11 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
 
   int pend_n = 0, pend_b0 = 0, pend_b1 = 0, pend_f0 = 0, pend_f1 = 0, pend_np0 = 0, pend_np1 = 0;
   bool pend_c0 = false, pend_c1 = false;  // kCascade: the pending row is a cascade row
+
+  constexpr int kItems = HKV * GR * D4;  // wave-merge items per round: one per thread at most
+  static_assert(kItems <= kRowsThreads, "one merge item per thread and round");
+  auto item_qh = [&](int r) { const int hg = tid / D4; return (hg / GR) * G + r * GR + hg % GR; };
+  const int d4i = tid % D4;
 
   int prev = -1;
   for (int pi = 0;; ++pi) {  // one piece (row segment) per iteration; uniform over the workgroup
@@ -826,8 +931,11 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     }
 
     // Merge the 8 waves through LDS: (m, l) of every query head, then the accumulators in rounds of
-    // GR heads per kv head.  One thread per 4 output dims combines the waves' states.
+    // GR heads per kv head.  One thread per 4 output dims combines the waves' states (round r: item
+    // tid < Hkv * GR * D / 4, at most one per thread).
     ensure_cum();
+    const bool split = P.nranges != 1;      // the row is held by several ranges
+    const int64_t slot = int64_t(b) + blk;  // split-partial slot of (row b, this range)
     if (col == 0) {
 #pragma unroll
       for (int g = 0; g < G; ++g) {
@@ -835,8 +943,6 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         s_l[wave][hd * G + g] = l[g];
       }
     }
-    const bool whole = P.nranges == 1;     // this workgroup holds the whole row
-    const int64_t slot = int64_t(b) + blk;   // split-partial slot of (row b, this range)
 #pragma unroll
     for (int r = 0; r < G / GR; ++r) {
 #pragma unroll
@@ -849,11 +955,11 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         dst[2 * (col + LPH) + 1] = f32x4{acc[g][12], acc[g][13], acc[g][14], acc[g][15]};
       }
       __syncthreads();
-      for (int idx = tid; idx < HKV * GR * D4; idx += kRowsThreads) {
-        const int hg = idx / D4, d4 = idx % D4;
-        const int qh = (hg / GR) * G + r * GR + hg % GR;
+      if (tid < kItems) {
+        const int hg = tid / D4, d4 = d4i;
+        const int qh = item_qh(r);
         PxBatch pb;
-        if (kCascade && whole && P.off > 0) px_load(b, qh, d4, 0, pb);
+        if (kCascade && !split && P.off > 0) px_load(b, qh, d4, 0, pb);
         float mw[kRowsWaves];
         float M = kNegBig;
 #pragma unroll
@@ -870,20 +976,19 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
           const f32x4 a4 = s_acc[w][hg][d4];
           O = f32x4{fmaf(wt, a4[0], O[0]), fmaf(wt, a4[1], O[1]), fmaf(wt, a4[2], O[2]), fmaf(wt, a4[3], O[3])};
         }
-        if (whole && kCascade && P.off > 0) {
-          cascade_out(b, qh, d4, M, L, O, pb);
-        } else if (whole) {
+        if (!split) {
+          write_row(b, qh, d4, M, L, O, P.off > 0, pb);
+        } else {  // publish this range's state of the row; its ticket is taken at the end
           const float inv = L > 0.f ? 1.f / L : 0.f;
-          *reinterpret_cast<f16x4*>(out + (int64_t(b) * HQ + qh) * D + 4 * d4) =
-              f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
-        } else {
-          st_dev4(r_o, uint32_t(((slot * HQ + qh) * D + 4 * d4) * 4), O);
-          if (d4 == 0) st_dev2(r_ml, uint32_t((slot * HQ + qh) * 2 * 4), f32x2{M, L});
+          const f16x4 oh = f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
+          st_dev2(r_o, o_off(slot, qh, d4), __builtin_bit_cast(f32x2, oh));
+          if (d4 == 0) st_dev2(r_ml, ml_off(slot, qh), f32x2{M, L});
         }
       }
       __syncthreads();
     }
-    if (!whole) {  // only the first and the last piece of a range can be split
+    if (split) {
+      // only the first and the last piece of a range can be split
       if (pend_n == 0) {
         pend_b0 = b; pend_f0 = P.first; pend_np0 = P.nranges; pend_c0 = P.off > 0;
       } else {
@@ -902,83 +1007,48 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
                                              __HIP_MEMORY_SCOPE_AGENT);
     __syncthreads();
     compiler_fence();  // the merge loads below stay behind the ticket
-    for (int k = 0; k < pend_n; ++k) {
-      const int np = k == 0 ? pend_np0 : pend_np1;
-      if (s_ticket[k] != uint32_t(np - 1)) continue;
-      const int b = k == 0 ? pend_b0 : pend_b1;
-      const int64_t slot0 = int64_t(b) + (k == 0 ? pend_f0 : pend_f1);
-      // Log-sum-exp merge of the row's np states (slots slot0 .. slot0 + np - 1, in range order).
-      // The D / 4 lanes of a query head (a lane group) share its (m, l) loads: lane j of the
-      // group loads state j's, the group reduces the maximum and the weights, and every lane
-      // reads a state's weight from its loader with a lane shuffle.  A lane then issues one
-      // 16-byte O load per state, kMergeBatch states per round trip.
-      constexpr int GL = D4 < kWave ? D4 : kWave;  // lanes sharing a query head
-      const int gbase = lane & ~(GL - 1), gj = lane - gbase;
+    // The rows this workgroup arrived last at are merged together: both rows' first round trips go
+    // out before either is reduced.
+    const bool last0 = s_ticket[0] == uint32_t(pend_np0 - 1);
+    const bool last1 = pend_n > 1 && s_ticket[1] == uint32_t(pend_np1 - 1);
+    if (last0 || last1) {
+      const int64_t s00 = int64_t(pend_b0) + pend_f0, s10 = int64_t(pend_b1) + pend_f1;
       for (int idx = tid; idx < HQ * D4; idx += kRowsThreads) {
         const int qh = idx / D4, d4 = idx % D4;
-        const bool casc = kCascade && (k == 0 ? pend_c0 : pend_c1);
-        PxBatch pb;
-        if (casc) px_load(b, qh, d4, 0, pb);  // with the partial states' first round trip
-        float M = kNegBig, L = 0.f;
-        f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
-        for (int j0 = 0; j0 < np; j0 += GL) {
-          const int cnt = min(GL, np - j0);
-          const f32x2 ml = ld_dev2(r_ml, uint32_t(((slot0 + j0 + min(gj, cnt - 1)) * HQ + qh) * 2 * 4));
-          // The first kMergeBatch O slices go out with the (m, l) loads: their addresses do not
-          // depend on the weights, so a row of up to kMergeBatch states costs one round trip.  Only
-          // the cnt states that exist are loaded (cnt is uniform): the merging CU's own bandwidth
-          // bounds this step, at Hq * D * 4 bytes per state.
-          f32x4 oj[kMergeBatch];
-#pragma unroll
-          for (int u = 0; u < kMergeBatch; ++u) {
-            oj[u] = f32x4{0.f, 0.f, 0.f, 0.f};
-            if (u < cnt) oj[u] = ld_dev4(r_o, uint32_t(((slot0 + j0 + u) * HQ + qh) * D * 4 + d4 * 16));
-          }
-          __builtin_amdgcn_sched_barrier(0);
-          const float mj = gj < cnt ? ml[0] : kNegBig;
-          float gm = mj;
-#pragma unroll
-          for (int o = 1; o < GL; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
-          const float nm = fmaxf(M, gm);
-          const float sc = exp2_fast(M - nm);
-          O = f32x4{O[0] * sc, O[1] * sc, O[2] * sc, O[3] * sc};
-          M = nm;
-          const float wj = gj < cnt ? exp2_fast(mj - M) : 0.f;
-          float ls = wj * ml[1];
-#pragma unroll
-          for (int o = 1; o < GL; o <<= 1) ls += __shfl_xor(ls, o);
-          L = fmaf(L, sc, ls);
-          for (int u0 = 0; u0 < cnt; u0 += kMergeBatch) {
-            if (u0 > 0) {
-#pragma unroll
-              for (int u = 0; u < kMergeBatch; ++u)
-                if (u0 + u < cnt) oj[u] = ld_dev4(r_o, uint32_t(((slot0 + j0 + u0 + u) * HQ + qh) * D * 4 + d4 * 16));
-            }
-#pragma unroll
-            for (int u = 0; u < kMergeBatch; ++u) {
-              const float w = __shfl(wj, gbase + min(u0 + u, cnt - 1));
-              if (u0 + u < cnt)
-                O = f32x4{fmaf(w, oj[u][0], O[0]), fmaf(w, oj[u][1], O[1]), fmaf(w, oj[u][2], O[2]),
-                          fmaf(w, oj[u][3], O[3])};
-            }
-          }
+        PxBatch p0, p1;
+        MergeLd l0, l1;
+        if (last0) {
+          if (kCascade && pend_c0) px_load(pend_b0, qh, d4, 0, p0);  // with the first round trip
+          merge_issue(s00, pend_np0, qh, d4, l0);
         }
-        if (casc) {
-          cascade_out(b, qh, d4, M, L, O, pb);
-          continue;
+        if (last1) {
+          if (kCascade && pend_c1) px_load(pend_b1, qh, d4, 0, p1);
+          merge_issue(s10, pend_np1, qh, d4, l1);
         }
-        const float inv = L > 0.f ? 1.f / L : 0.f;
-        *reinterpret_cast<f16x4*>(out + (int64_t(b) * HQ + qh) * D + 4 * d4) =
-            f16x4{f16(O[0] * inv), f16(O[1] * inv), f16(O[2] * inv), f16(O[3] * inv)};
+        if (last0) {
+          float M = kNegBig, L = 0.f;
+          f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+          merge_finish(s00, pend_np0, qh, d4, l0, M, L, O);
+          write_row(pend_b0, qh, d4, M, L, O, pend_c0, p0);
+        }
+        if (last1) {
+          float M = kNegBig, L = 0.f;
+          f32x4 O = f32x4{0.f, 0.f, 0.f, 0.f};
+          merge_finish(s10, pend_np1, qh, d4, l1, M, L, O);
+          write_row(pend_b1, qh, d4, M, L, O, pend_c1, p1);
+        }
       }
-      if (tid == 0) reset_ticket(ws.count + b);
+      if (tid == 0) {
+        if (last0) reset_ticket(ws.count + pend_b0);
+        if (last1) reset_ticket(ws.count + pend_b1);
+      }
     }
   }
   finish();
 }
 
-typedef void (*RowsKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, const int32_t*,
-                           const uint8_t*, int32_t, int32_t, float, DecodeWorkspace, DecodeAppend, const int32_t*,
+typedef void (*RowsKernel)(const int32_t*, const f16*, const int32_t*, const f16*, int32_t, int32_t, int32_t, int32_t,
+                           int64_t, f16*, const int32_t*, const uint8_t*, float, DecodeWorkspace, DecodeAppend,
                            DecodePrep, DecodePrefix);
 
 constexpr int kRowsStages = 2;
@@ -1052,9 +1122,9 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
   ws.o = reinterpret_cast<float*>(wsb + off_o);
   const DecodePrep pp = prep != nullptr ? *prep : DecodePrep{};
   const DecodePrefix pf = px != nullptr ? *px : DecodePrefix{nullptr, nullptr, 0, 0};
-  k<<<dim3(unsigned(blocks)), dim3(kRowsThreads), 0, stream>>>(out, q, pool, num_pages, block_tables, max_pages,
-                                                                seq_lens, active, batch, max_len, scale_log2, ws, ap,
-                                                                px != nullptr ? nullptr : plan, pp, pf);
+  k<<<dim3(unsigned(blocks)), dim3(kRowsThreads), 0, stream>>>(px != nullptr ? nullptr : plan, pool, block_tables, q,
+                                                                batch, max_pages, max_len, blocks, num_pages, out,
+                                                                seq_lens, active, scale_log2, ws, ap, pp, pf);
   return ifn_launch_status();
 }
 
