@@ -48,7 +48,7 @@ constexpr int kRowsThreads = kRowsWaves * kWave;
 constexpr int kRowsMaxBatch = 4096;  // rows per call (LDS offset table)
 constexpr int kRowsBlock = 16;       // tokens per page compiled in
 constexpr int kRowsXcds = 8;         // MI355X: workgroups dispatched round-robin over 8 XCDs
-constexpr int kMergeBatch = 20;      // split states loaded per round trip of the final merge
+constexpr int kMergeBatch = 16;      // split states loaded per round trip of the final merge
 // Cost of starting a row, in tokens.  A range that holds the end of one row and the start of the
 // next pays a second start-up, a second merge of its waves and possibly two split merges, so the
 // split counts each non-empty row as kRowStartCost tokens longer (virtual tokens in front of it).
@@ -119,14 +119,15 @@ __device__ __forceinline__ int row_slot(const int32_t* slots, const uint8_t* act
 // last of those positions, after kRowStartCost virtual ones when it has any.  Shared-prefix mode
 // (pk > 0): a row of at least pk keys (a cascade row, flagged in s_casc) streams only its keys
 // after the first pk.
+// s_len (optional): the rows' keys, already in LDS (and published by a barrier).
 __device__ __forceinline__ int build_offsets(int* s_cum, int* s_wsum, const int32_t* seq_lens,
                                              const uint8_t* active, int batch, int cap, int pk = 0,
-                                             uint8_t* s_casc = nullptr) {
+                                             uint8_t* s_casc = nullptr, const int* s_len = nullptr) {
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave, nwaves = blockDim.x / kWave;
   int running = 0;
   for (int base = 0; base < batch; base += blockDim.x) {
     const int i = base + tid;
-    int len = i < batch ? row_keys(seq_lens, active, i, cap) : 0;
+    int len = i < batch ? (s_len != nullptr ? s_len[i] : row_keys(seq_lens, active, i, cap)) : 0;
     const bool casc = pk > 0 && len >= pk;
     if (s_casc != nullptr && i < batch) s_casc[i] = casc ? 1 : 0;
     if (casc) len -= pk;
@@ -174,6 +175,7 @@ struct RowPiece {
 
 // Step plan: one workgroup writes the header, the offsets and every range's record.
 constexpr int kPlanThreads = 1024;
+constexpr int kPlanTabWords = 16384;  // block tables up to this many entries are staged in LDS
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
     int32_t* __restrict__ plan, const int32_t* __restrict__ block_tables, int32_t max_pages,
     const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, const int32_t* __restrict__ slots,
@@ -182,12 +184,53 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   __shared__ int s_wsum[kPlanThreads / kWave];
   __shared__ int s_p0[3][kPlanThreads];  // first piece of range r: row, a, e (rows < 0: none)
   __shared__ int s_slot[kRowsMaxBatch];   // appended slot of each row (-1: none)
+  __shared__ int s_len[kRowsMaxBatch];    // keys of each row
+  __shared__ int s_tab[kPlanTabWords];    // the block table, when it fits
   const int tid = threadIdx.x;
   const int cap = min(max_pages * kRowsBlock, max_len);
   const int64_t num_slots = num_pages * kRowsBlock;
-  if (slots != nullptr)  // loaded beside the lengths; build_offsets' barriers publish them
-    for (int i = tid; i < batch; i += kPlanThreads) s_slot[i] = row_slot(slots, active, i, num_slots);
-  const int T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap);
+  // Every load the plan depends on goes out at launch, in one round trip: the rows' lengths, flags
+  // and slots and, when it fits in LDS (config 2: 32 KB), the whole block table -- so that the page
+  // ids of the ranges' first windows come from LDS instead of a second round trip.
+  const int64_t tab_words = int64_t(batch) * max_pages;
+  const bool tab_lds = tab_words <= kPlanTabWords;
+  constexpr int kRowsPer = kRowsMaxBatch / kPlanThreads, kTabPer = kPlanTabWords / kPlanThreads;
+  // Unconditional loads (indices clamped, absent arrays read through a stand-in), selected after
+  // every load is out: a load under a condition makes the compiler wait for it at the join.
+  const uint8_t* act_src = active != nullptr ? active : reinterpret_cast<const uint8_t*>(seq_lens);
+  const int32_t* slot_src = slots != nullptr ? slots : seq_lens;
+  int r_len[kRowsPer], r_slot[kRowsPer], r_tab[kTabPer];
+  uint8_t r_act[kRowsPer];
+#pragma unroll
+  for (int k = 0; k < kRowsPer; ++k) {
+    const int i = min(tid + k * kPlanThreads, batch - 1);
+    r_len[k] = seq_lens[i];
+    r_act[k] = act_src[i];
+    r_slot[k] = slot_src[i];
+  }
+  if (tab_lds) {
+#pragma unroll
+    for (int k = 0; k < kTabPer; ++k) r_tab[k] = block_tables[min(int64_t(tid + k * kPlanThreads), tab_words - 1)];
+  }
+#pragma unroll
+  for (int k = 0; k < kRowsPer; ++k) {
+    const int i = tid + k * kPlanThreads;
+    if (i < batch) {
+      const bool act = active == nullptr || r_act[k] != 0;
+      const int sl = slots != nullptr ? r_slot[k] : -1;
+      s_len[i] = act ? max(0, min(r_len[k], cap)) : 0;           // row_keys
+      s_slot[i] = act && sl >= 0 && sl < num_slots ? sl : -1;  // row_slot
+    }
+  }
+  if (tab_lds) {
+#pragma unroll
+    for (int k = 0; k < kTabPer; ++k) {
+      const int i = tid + k * kPlanThreads;
+      if (i < tab_words) s_tab[i] = r_tab[k];
+    }
+  }
+  __syncthreads();
+  const int T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap, 0, nullptr, s_len);
   const int nr = int(range_count(nb, T));
   if (tid == 0) {
     plan[0] = kPlanMagic;
@@ -260,7 +303,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
       const int b = s_p0[0][r];
       const int pg0 = b >= 0 ? s_p0[1][r] / kRowsBlock : 0;
       const int npg = b >= 0 ? (s_p0[2][r] - 1) / kRowsBlock - pg0 + 1 : 1;
-      id[k] = block_tables[int64_t(max(b, 0)) * max_pages + pg0 + min(lane, npg - 1)];
+      const int64_t at = int64_t(max(b, 0)) * max_pages + pg0 + min(lane, npg - 1);
+      id[k] = tab_lds ? s_tab[at] : block_tables[at];
     }
 #pragma unroll
     for (int k = 0; k < kIdBatch; ++k) {
@@ -625,69 +669,53 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const __amdgpu_buffer_rsrc_t r_ml = make_rsrc(ws.ml, n_slots * HQ * 2u * 4u);
 
   // Log-sum-exp merge of a split row's np states (slots slot0 .. slot0 + np - 1, in range order)
-  // for query head qh, dims 4 d4 .. 4 d4 + 3.  The D / 4 lanes of a query head (a lane group) share
-  // its (m, l) loads: lane j of the group loads state j's, the group reduces the maximum and the
-  // weights, and every lane reads a state's weight from its loader with a lane shuffle.  A lane
-  // issues one 16-byte O load per state, kMergeBatch states per round trip; merge_issue sends the
-  // first round trip (so that a caller can overlap it with other work), merge_finish the rest and
-  // the arithmetic.  Only the cnt states that exist are loaded (cnt is uniform): the merging CU's
-  // own bandwidth bounds this step, at Hq * D * 4 bytes per state.
-  constexpr int GL = D4 < kWave ? D4 : kWave;  // lanes sharing a query head
-  const int gbase = lane & ~(GL - 1), gj = lane - gbase;
+  // for query head qh, dims 4 d4 .. 4 d4 + 3.  Every lane loads each state's (m, l) itself (the lanes
+  // of a query head read the same 8 bytes, one request) and its 4 dims of O / l, kMergeBatch states
+  // per round trip, and reduces them on its own: no lane exchanges, whose latency would sit on the
+  // last workgroup's path.  merge_issue sends the first round trip (so that a caller can overlap it
+  // with other work), merge_finish the rest and the arithmetic.  Only the cnt states that exist are
+  // loaded (cnt is uniform).
   struct MergeLd {
-    f32x2 ml;
+    f32x2 ml[kMergeBatch];
     f32x2 o[kMergeBatch];  // 4 fp16 dims of O / l
   };
   auto ml_off = [&](int64_t s, int qh) { return uint32_t((s * HQ + qh) * 2 * 4); };
   auto o_off = [&](int64_t s, int qh, int d4) { return uint32_t(((s * HQ + qh) * D + 4 * d4) * 2); };
-  auto merge_issue = [&](int64_t slot0, int np, int qh, int d4, MergeLd& ld) __attribute__((always_inline)) {
-    const int cnt = min(GL, np);
-    ld.ml = ld_dev2(r_ml, ml_off(slot0 + min(gj, cnt - 1), qh));
+  auto merge_load = [&](int64_t s0, int cnt, int qh, int d4, MergeLd& ld) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) {
-      ld.o[u] = f32x2{0.f, 0.f};
-      if (u < cnt) ld.o[u] = ld_dev2(r_o, o_off(slot0 + u, qh, d4));
+      if (u < cnt) {
+        ld.ml[u] = ld_dev2(r_ml, ml_off(s0 + u, qh));
+        ld.o[u] = ld_dev2(r_o, o_off(s0 + u, qh, d4));
+      }
     }
+  };
+  auto merge_issue = [&](int64_t slot0, int np, int qh, int d4, MergeLd& ld) __attribute__((always_inline)) {
+    merge_load(slot0, min(kMergeBatch, np), qh, d4, ld);
   };
   auto merge_finish = [&](int64_t slot0, int np, int qh, int d4, MergeLd& ld, float& M, float& L, f32x4& O)
                           __attribute__((always_inline)) {
-    for (int j0 = 0; j0 < np; j0 += GL) {
-      const int cnt = min(GL, np - j0);
-      if (j0 > 0) {
-        ld.ml = ld_dev2(r_ml, ml_off(slot0 + j0 + min(gj, cnt - 1), qh));
-#pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u)
-          if (u < cnt) ld.o[u] = ld_dev2(r_o, o_off(slot0 + j0 + u, qh, d4));
-      }
+    for (int j0 = 0; j0 < np; j0 += kMergeBatch) {
+      const int cnt = min(kMergeBatch, np - j0);
+      if (j0 > 0) merge_load(slot0 + j0, cnt, qh, d4, ld);
       __builtin_amdgcn_sched_barrier(0);
-      const f32x2 ml = ld.ml;
-      const float mj = gj < cnt ? ml[0] : kNegBig;
-      float gm = mj;
+      float gm = kNegBig;
 #pragma unroll
-      for (int o = 1; o < GL; o <<= 1) gm = fmaxf(gm, __shfl_xor(gm, o));
+      for (int u = 0; u < kMergeBatch; ++u)
+        if (u < cnt) gm = fmaxf(gm, ld.ml[u][0]);
       const float nm = fmaxf(M, gm);
       const float sc = exp2_fast(M - nm);
       O = f32x4{O[0] * sc, O[1] * sc, O[2] * sc, O[3] * sc};
+      L *= sc;
       M = nm;
-      // state j's weight in the sum, applied to its l and to its O / l
-      const float wl = gj < cnt ? exp2_fast(mj - M) * ml[1] : 0.f;
-      float ls = wl;
 #pragma unroll
-      for (int o = 1; o < GL; o <<= 1) ls += __shfl_xor(ls, o);
-      L = fmaf(L, sc, ls);
-      for (int u0 = 0; u0 < cnt; u0 += kMergeBatch) {
-        if (u0 > 0) {
-#pragma unroll
-          for (int u = 0; u < kMergeBatch; ++u)
-            if (u0 + u < cnt) ld.o[u] = ld_dev2(r_o, o_off(slot0 + j0 + u0 + u, qh, d4));
-        }
-#pragma unroll
-        for (int u = 0; u < kMergeBatch; ++u) {
-          const float w = __shfl(wl, gbase + min(u0 + u, cnt - 1));
+      for (int u = 0; u < kMergeBatch; ++u) {
+        if (u < cnt) {
+          const float w = exp2_fast(ld.ml[u][0] - M) * ld.ml[u][1];  // weight of O / l: e^(m - M) l
           const f16x4 oh = __builtin_bit_cast(f16x4, ld.o[u]);
-          if (u0 + u < cnt)
-            O = f32x4{fmaf(w, float(oh[0]), O[0]), fmaf(w, float(oh[1]), O[1]), fmaf(w, float(oh[2]), O[2]),
-                      fmaf(w, float(oh[3]), O[3])};
+          L += w;
+          O = f32x4{fmaf(w, float(oh[0]), O[0]), fmaf(w, float(oh[1]), O[1]), fmaf(w, float(oh[2]), O[2]),
+                    fmaf(w, float(oh[3]), O[3])};
         }
       }
     }
