@@ -9,10 +9,11 @@
  * reference's write-before-read rule (docs/architecture.md:249-250).
  *
  * The library never allocates device memory.  Scratch space is a
- * caller-provided workspace.  Its first 256 KiB are split-KV tickets, whose
- * last 4 bytes are an error flag: a kernel sets that uint32 to 1 when one of
- * its bounded waits gave up (its result may then be wrong); only the caller
- * reads and clears it.  No C++ exception crosses this boundary: every
+ * caller-provided workspace.  Its first 256 KiB are split-KV tickets; they
+ * must be zero when the workspace is created, and every call returns the
+ * tickets it used to zero.  No kernel waits on another workgroup (a split is
+ * merged by whichever workgroup arrives last), so no call can stall on the
+ * device.  No C++ exception crosses this boundary: every
  * entry point returns IFN_OK (0) or a negative IFN_ERR_* code, checked on the
  * host before any launch (shape, alignment and workspace checks) or after it
  * (hipGetLastError).  Entry points hold no mutable global state, so distinct

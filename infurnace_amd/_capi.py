@@ -22,10 +22,6 @@ IFN_ERR_ALIGNMENT = -3
 IFN_ERR_WORKSPACE = -4
 IFN_ERR_HIP = -5
 
-# The workspace's error flag: the last 4 bytes of its 256 KiB ticket area (a uint32 a kernel sets to
-# 1 when a bounded wait gave up and its result may be wrong; only the caller clears it).
-WORKSPACE_ERROR_FLAG_OFFSET = (256 << 10) - 4
-
 _p = ctypes.c_void_p
 _i32 = ctypes.c_int32
 _i64 = ctypes.c_int64

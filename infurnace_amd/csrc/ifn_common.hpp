@@ -98,14 +98,7 @@ __host__ __device__ constexpr int64_t ceil_div(int64_t a, int64_t b) { return (a
 // is created; each call returns the tickets it used to zero.  Partial results follow it.
 constexpr size_t kTicketBytes = size_t(256) << 10;
 constexpr int64_t kTicketWords = int64_t(kTicketBytes / sizeof(uint32_t));
-constexpr int64_t kMaxTickets = kTicketWords - 1;  // tickets one call may use
-// The ticket area's last word is an error flag: a kernel sets it (to 1) when a bounded wait gave
-// up and its result may be wrong.  Nothing clears it but the caller (the Python wrappers' validate
-// mode reads, reports and clears it).
-constexpr int64_t kErrorFlagWord = kTicketWords - 1;
-__device__ __forceinline__ void raise_error_flag(uint32_t* tickets) {
-  __hip_atomic_store(tickets + kErrorFlagWord, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+constexpr int64_t kMaxTickets = kTicketWords - 1;  // tickets one call may use (the last word is spare)
 
 // Device-coherent (agent scope) scalar store / load.  They compile to global_store/load
 // with the sc1 bit: written through to, and read from, the device coherence point, so

@@ -1013,6 +1013,7 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   DecodeKernel k = rows ? nullptr : pick_decode(head_dim, g, DecodeMode::kCascade);
   CombineKernel kc = pick_combine(head_dim);
   if ((!rows && k == nullptr) || kc == nullptr) return IFN_ERR_UNSUPPORTED;
+  if (!wide_prefill_supported(num_q_heads, num_kv_heads, head_dim)) return IFN_ERR_UNSUPPORTED;  // prefix pass
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);

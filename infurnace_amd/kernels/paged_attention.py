@@ -57,12 +57,23 @@ class DecodePlan:
     nothing else; a plan built once per step lets each layer's launch start its
     page loads one round trip after launch.  It is valid only for calls with the
     tensors it was built from, unchanged: the wrappers check that the same
-    tensors and shapes are passed (any layer of the same pool), not their
-    contents.
+    tensors and shapes are passed (any layer of the same pool), and with
+    ``validate=True`` also their contents (the plan is rebuilt and compared byte
+    for byte).
     """
 
-    def __init__(self, buf, nbytes: int, key: tuple):
-        self.buf, self.nbytes, self.key = buf, nbytes, key
+    def __init__(self, buf, nbytes: int, key: tuple, rebuild=None):
+        self.buf, self.nbytes, self.key, self._rebuild = buf, nbytes, key, rebuild
+
+    def check_current(self) -> None:
+        """Validate mode: raise unless a plan built now from the same tensors is identical
+        (their contents were not changed since this one was built)."""
+        if self.buf is None or self._rebuild is None:
+            return
+        fresh = self._rebuild()
+        if not torch.equal(fresh.buf, self.buf):
+            raise PagedAttentionError("stale DecodePlan: the tables, lengths, mask or slots it was built from "
+                                      "have changed since; build a new plan for this step")
 
     def ptr_for(self, key: tuple, need_slots: bool):
         """The plan's device address for a call with ``key``; None when these shapes need no plan."""
@@ -121,21 +132,49 @@ def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, 
     nbytes = lib.ifn_paged_decode_plan_bytes(n, hq, hkv, d, bs, max_pages, msl)
     if nbytes == 0:
         return DecodePlan(None, 0, key)
-    buf = torch.empty(nbytes, dtype=torch.uint8, device=dev)
+    # zero-filled, so that words the kernel leaves unwritten compare equal between two plans
+    buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
     _capi.call("ifn_paged_decode_plan", buf.data_ptr(), nbytes, ptr(block_tables), max_pages, ptr(sequence_lengths),
                ptr(active_mask), ptr(slot_mapping), P, n, hq, hkv, d, bs, msl, current_stream(dev))
-    return DecodePlan(buf, nbytes, key)
+
+    def rebuild():
+        return decode_plan(query_shape, kv_pool, block_tables, sequence_lengths, active_mask, slot_mapping,
+                           layer=layer, block_size=block_size, max_seq_len=max_seq_len)
+    return DecodePlan(buf, nbytes, key, rebuild)
 
 
-def check_error_flag(ws: torch.Tensor, what: str) -> None:
-    """Validate mode: synchronise, and raise if a kernel that used ``ws`` set its error flag (a
-    bounded wait gave up, so the result may be wrong); the flag is cleared first."""
-    torch.cuda.synchronize(ws.device)
-    off = _capi.WORKSPACE_ERROR_FLAG_OFFSET
-    flag = ws[off:off + 4]
-    if bool(flag.any()):
-        flag.zero_()
-        raise PagedAttentionError(f"{what}: a workgroup's bounded wait gave up; the result may be wrong")
+def _row_keys(sequence_lengths: torch.Tensor, active_mask, msl: int) -> torch.Tensor:
+    """Keys each decode row attends (0 for inactive rows), on the device."""
+    keys = sequence_lengths.to(torch.int64).clamp(0, msl)
+    if active_mask is not None:
+        keys = keys * active_mask.to(torch.bool)
+    return keys
+
+
+def _validate_pages(table: torch.Tensor, keys: torch.Tensor, num_pages: int, bs: int, what: str) -> None:
+    """Validate mode: every table entry a row reads (its first ceil(keys / bs) entries) names a page of
+    the pool.  The kernels read an entry outside the pool as a page without keys; here it raises.
+    ``table`` is [rows, max_pages], ``keys`` [rows] (int64, on the device)."""
+    need = (keys + bs - 1) // bs
+    used = torch.arange(table.shape[1], device=table.device)[None, :] < need[:, None]
+    bad = used & ((table < 0) | (table >= num_pages))
+    if bool(bad.any()):
+        row, col = (int(x) for x in bad.nonzero()[0])
+        raise PagedAttentionError(f"{what}: block table row {row} entry {col} = {int(table[row, col])} "
+                                  f"is not a page of the {num_pages}-page pool")
+
+
+def _validate_shared_prefix(table: torch.Tensor, keys: torch.Tensor, pages: torch.Tensor, bs: int) -> None:
+    """Validate mode: every row of at least S * bs keys starts its table with the S declared pages."""
+    sp = pages.shape[0]
+    if sp == 0:
+        return
+    casc = keys >= sp * bs
+    bad = casc[:, None] & (table[:, :sp] != pages[None, :])
+    if bool(bad.any()):
+        row, col = (int(x) for x in bad.nonzero()[0])
+        raise PagedAttentionError(f"shared_prefix_pages: row {row} of {int(keys[row])} keys has page "
+                                  f"{int(table[row, col])} at entry {col}, not the declared {int(pages[col])}")
 
 
 def _check(name: str, t, shape: tuple, dtypes: tuple, device) -> None:
@@ -169,19 +208,25 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
     (int32 [S] on the device) declares that every row of at least
     S * block_size keys starts its table with these S pages (a prefix-cache
     hit); they are then read once for the whole batch instead of once per row.
-    The declaration is trusted, not checked.  Without it the decode streams its
+    The declaration is trusted unless ``validate``.  Without it the decode streams its
     pages (non-temporal loads, each page expected to be read by one row); an
     empty ``shared_prefix_pages`` declares rows that share pages outside a
     common leading run, and the decode then keeps pages in the caches.
     ``plan`` (decode only, from ``decode_plan`` over the same tensors) is the
     step's precomputed split; the result is bit-identical without it.
 
+    ``validate=True`` (a debug mode: it synchronises) checks, before the launch,
+    what the kernels otherwise trust: that every table entry a row reads names a
+    page of the pool, that ``shared_prefix_pages`` heads the table of every row
+    long enough to include it, and that ``plan`` is current (rebuilt and compared
+    byte for byte); it raises ``PagedAttentionError`` on a mismatch.  The launch
+    itself, and so the result, is the same as without it.
+
     Prefill (``query_start`` given): ``query`` [T, Hq, D] of one sequence,
     ``block_tables`` int32 [max_pages] or [1, max_pages]; ``sequence_lengths`` is
     unused on the device (keys = query_start + T) and, when it is a host value,
     must equal query_start + T.  ``active_mask`` of one False row makes the call
-    a no-op.  ``validate`` (prefill) synchronises after the launch and raises when
-    a workgroup's bounded wait gave up (the workspace's error flag).
+    a no-op.
     """
     pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
     dev = pool_layer.device
@@ -222,6 +267,11 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
             raise PagedAttentionError("max_seq_len must be non-negative")
         if n == 0:
             return out
+        if validate:
+            keys = _row_keys(sequence_lengths, active_mask, msl)
+            _validate_pages(block_tables, keys, P, bs, "paged_attention")
+            if plan is not None:
+                plan.check_current()
         if shared_prefix_pages is not None:
             if not isinstance(shared_prefix_pages, torch.Tensor) or shared_prefix_pages.ndim != 1:
                 raise PagedAttentionError("shared_prefix_pages must be a rank-1 int32 tensor")
@@ -229,6 +279,8 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
             _check("shared_prefix_pages", shared_prefix_pages, (sp,), (torch.int32,), dev)
             if sp > max_pages:
                 raise PagedAttentionError(f"{sp} shared pages exceed the table's {max_pages} columns")
+            if validate:
+                _validate_shared_prefix(block_tables, keys, shared_prefix_pages, bs)
             nbytes = lib.ifn_paged_decode_shared_prefix_workspace_bytes(n, hq, hkv, d, bs, sp)
             ws = workspace_for(dev, stream, nbytes)
             _capi.call("ifn_paged_decode_shared_prefix", ptr(out), ptr(query), ptr(pool_layer), P,
@@ -276,12 +328,13 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
             return out
     if n == 0:
         return out
+    if validate:
+        _validate_pages(table[None, :], torch.full((1,), total, dtype=torch.int64, device=dev), P, bs,
+                        "paged_attention (prefill)")
     nbytes = lib.ifn_paged_prefill_workspace_bytes(n, query_start, hq, hkv, d, bs)
     ws = workspace_for(dev, stream, nbytes)
     _capi.call("ifn_paged_prefill", ptr(out), ptr(query), ptr(pool_layer), P, ptr(table), max_pages,
                query_start, n, hq, hkv, d, bs, float(scale), ptr(ws), ws.numel(), stream)
-    if validate:
-        check_error_flag(ws, "paged_attention (prefill)")
     return out
 
 
@@ -290,7 +343,8 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
                         sequence_lengths: torch.Tensor, active_mask: torch.Tensor | None,
                         slot_mapping: torch.Tensor, new_k: torch.Tensor, new_v: torch.Tensor, *, layer: int = 0,
                         scale: float | None = None, out: torch.Tensor | None = None, block_size: int = 16,
-                        max_seq_len: int | None = None, plan: DecodePlan | None = None) -> torch.Tensor:
+                        max_seq_len: int | None = None, plan: DecodePlan | None = None,
+                        validate: bool = False) -> torch.Tensor:
     """One decode step's append and attention in one launch (``ifn_paged_decode_append``).
 
     Same result, in ``out`` and in the pool, as ``store_kv(kv_pool, slot_mapping, active_mask,
@@ -298,7 +352,8 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
     sequence_lengths, active_mask, layer=layer, ...)`` -- the store of model.py:191-196 and the
     attention of :196-200.  ``new_k``/``new_v`` are fp16 [B, Hkv, D], ``slot_mapping`` int32 [B].
     An appended slot must not be read by another row of the call (true of any paged KV state).
-    ``plan``: the step's ``decode_plan`` built with this ``slot_mapping``.
+    ``plan``: the step's ``decode_plan`` built with this ``slot_mapping``.  ``validate`` as for
+    ``paged_attention``, plus the slots (as ``store_kv(..., validate=True)``).
     """
     from .kv_store import _check_index, _check_rows
     if slot_mapping is None:
@@ -339,6 +394,12 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
         raise PagedAttentionError("max_seq_len must be non-negative")
     if n == 0:
         return out
+    if validate:
+        from .kv_store import _debug_validate
+        _debug_validate(sm, active_mask, P * bs)
+        _validate_pages(block_tables, _row_keys(sequence_lengths, active_mask, msl), P, bs, "store_kv_and_decode")
+        if plan is not None:
+            plan.check_current()
     stream = current_stream(dev)
     lib = _capi.lib()
     nbytes = lib.ifn_paged_decode_workspace_bytes(n, hq, hkv, d, bs, msl)
@@ -366,7 +427,8 @@ def store_kv_and_prefill(query: torch.Tensor, kv_pool: torch.Tensor, block_table
     the table's slots for positions query_start .. query_start + T - 1 followed by
     ``paged_attention(query, ..., query_start=query_start)`` -- the store of model.py:134-138 and
     the attention of :116-132.  One launch when query_start % 32 == 0, else the store and the
-    attention as two launches.
+    attention as two launches.  ``validate``: every table entry the chunk's keys use names a page
+    of the pool (checked before the launch; a debug mode that synchronises).
     """
     from .kv_store import _check_rows
     pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
@@ -403,13 +465,14 @@ def store_kv_and_prefill(query: torch.Tensor, kv_pool: torch.Tensor, block_table
         raise PagedAttentionError(f"scale must be positive, got {scale}")
     if n == 0:
         return out
+    if validate:
+        _validate_pages(table[None, :], torch.full((1,), query_start + n, dtype=torch.int64, device=dev), P, bs,
+                        "store_kv_and_prefill")
     stream = current_stream(dev)
     lib = _capi.lib()
     nbytes = lib.ifn_paged_prefill_workspace_bytes(n, query_start, hq, hkv, d, bs)
     ws = workspace_for(dev, stream, nbytes)
     _capi.call("ifn_paged_prefill_append", ptr(out), ptr(query), ptr(pool_layer), P, ptr(table), max_pages,
                query_start, n, ptr(new_k), ptr(new_v), hq, hkv, d, bs, float(scale), ptr(ws), ws.numel(), stream)
-    if validate:
-        check_error_flag(ws, "store_kv_and_prefill")
     return out
 

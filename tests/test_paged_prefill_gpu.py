@@ -161,25 +161,3 @@ def test_invalid_page_contributes_no_keys(dev):
     bad[2] = -1
     out = paged_attention(to_dev(q, dev), to_dev(pool, dev), to_dev(bad, dev), None, None, query_start=start)
     assert_attn_close(out, ref.astype(np.float32), "page id -1")
-
-
-def test_validate_reports_and_clears_the_error_flag(dev):
-    """Validate mode reads the workspace's error flag (set by a kernel whose bounded wait gave up),
-    raises, and clears it.  The flag is planted from the host: no kernel is made to time out."""
-    from infurnace_amd import _capi
-    from infurnace_amd.kernels import PagedAttentionError
-    from infurnace_amd.kernels.paged_attention import workspace_for
-    say("prefill validate / error flag")
-    rng = np.random.default_rng(26)
-    pool, table = _seq(rng, 1024, 16, 8, 128)
-    q = rng.standard_normal((256, 16, 128), dtype=np.float32).astype(np.float16)
-    P, T, Q = to_dev(pool, dev), to_dev(table, dev), to_dev(q, dev)
-    ok = paged_attention(Q, P, T, None, None, query_start=768, validate=True)
-    ws = workspace_for(dev, torch.cuda.current_stream(dev).cuda_stream, 0)
-    off = _capi.WORKSPACE_ERROR_FLAG_OFFSET
-    ws[off] = 1
-    with pytest.raises(PagedAttentionError):
-        paged_attention(Q, P, T, None, None, query_start=768, validate=True)
-    assert not bool(ws[off:off + 4].any())
-    again = paged_attention(Q, P, T, None, None, query_start=768, validate=True)
-    assert torch.equal(ok.view(torch.int16), again.view(torch.int16))
