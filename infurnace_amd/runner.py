@@ -133,13 +133,10 @@ class _Step:
             return o
         q16 = qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope, self.positions, self.slot_mapping,
                                   self.active, kv, layer=layer, eps=eps)
-        if self.query_start is not None:
+        if self.query_start is not None:  # a prefill chunk
             o = paged_attention(q16, kv, self.block_tables, None, None, layer=layer, query_start=self.query_start,
                                 out=out)
-        elif self.shared_prefix is None:
-            o = paged_attention(q16, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
-                                max_seq_len=self.max_len, out=out, plan=self._decode_plan(q16))
-        else:
+        else:  # a decode step over a shared prefix
             o = paged_attention(q16, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
                                 max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
         self._launched()

@@ -12,7 +12,8 @@ import numpy as np
 import pytest
 import torch
 
-from gpu_util import assert_attn_close, oracle_decode, say, to_dev
+import oracle
+from gpu_util import assert_attn_close, compact_for_oracle, say, to_dev
 from infurnace_amd import workloads
 from infurnace_amd.kernels import (decode_plan, paged_attention, qk_norm_rope_append, qk_norm_rope_store_and_decode,
                                    rope_table)
@@ -102,7 +103,11 @@ def test_fused_prep_edge_rows(dev):
 
 def test_fused_prep_config2_full_size(dev):
     """Config 2 (B=32, ragged contexts up to 4096, 16384 pages) at full size, planned as the runner
-    calls it, and three rows against the oracle."""
+    calls it; every row against the oracle's own pipeline.  The oracle copies the pages the rows
+    read before the launch, runs its own pre-append (orc_qk_norm_rope_append) from the fp32
+    projections into that copy at the rows' slots, then its attention: nothing it reads comes
+    from the GPU's pre-append.  The appended K rows must match the oracle's within one fp16 ulp
+    and the V rows bit for bit."""
     say("fused prep+decode config 2")
     w = workloads.config2()
     rng = np.random.default_rng(2)
@@ -117,11 +122,23 @@ def test_fused_prep_config2_full_size(dev):
              v=rng.standard_normal((B, hkv, d)).astype(np.float32),
              qw=(1 + 0.1 * rng.standard_normal(d)).astype(np.float32),
              kw=(1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
+    lens = c["lens"]
+    sub, t2 = compact_for_oracle(pool, w.block_tables, lens)  # before the launches append into `pool`
     p1, o1, p2, o2, q16 = _both(dev, c, planned=True)
     _assert_same(p1, o1, p2, o2, "config 2")
-    rows = [0, 7, 31]
-    ref = oracle_decode(p2, w.block_tables, w.seq_lens, q16, rows)
-    assert_attn_close(o2[rows], ref, "config 2 fused prep vs oracle")
+    pos = c["pos"]
+    slots_sub = np.asarray([t2[b, pos[b] // 16] * 16 + pos[b] % 16 for b in range(B)], np.int32)
+    rope = rope_table(MAX_POS, d, 1e6).numpy()
+    q16_orc = oracle.qk_norm_rope_append(c["q"], c["k"], c["v"], c["qw"], c["kw"], rope, pos, slots_sub, None, sub)
+    ref = oracle.paged_attention_rows(q16_orc, sub, t2, lens)
+    assert_attn_close(o2, ref, "config 2 fused prep vs the oracle pipeline")
+    got_k = p2[0].reshape(-1, hkv, d)[torch.as_tensor(w.append_slots.astype(np.int64), device=dev)].cpu().numpy()
+    got_v = p2[1].reshape(-1, hkv, d)[torch.as_tensor(w.append_slots.astype(np.int64), device=dev)].cpu().numpy()
+    exp_k = sub[0].reshape(-1, hkv, d)[slots_sub]
+    exp_v = sub[1].reshape(-1, hkv, d)[slots_sub]
+    assert np.array_equal(got_v.view(np.uint16), exp_v.view(np.uint16)), "appended V rows differ from the oracle"
+    ulps = np.abs(got_k.view(np.uint16).astype(np.int32) - exp_k.view(np.uint16).astype(np.int32))
+    assert int(ulps.max()) <= 1, "appended K rows differ from the oracle by more than one fp16 ulp"
 
 
 def test_fused_prep_unsupported_shape_runs_two_launches(dev):
