@@ -38,6 +38,8 @@
  *   block_tables         int32 [batch][max_pages_per_seq]
  *   decode query/out     [batch][num_q_heads][head_dim]
  *   prefill query/out    [num_q_tokens][num_q_heads][head_dim]
+ * Queries and K/V must be finite: the prefill is compiled assuming its scores
+ * are never NaN, and its output is unspecified for NaN or Inf inputs.
  * Query head h reads kv head h / (num_q_heads / num_kv_heads) (GQA, as
  * tinygrad's scaled_dot_product_attention(enable_gqa=True) at model.py:200).
  */
@@ -211,9 +213,11 @@ int ifn_paged_decode_append_planned(void* out, const void* query, void* kv_pool_
  * ifn_paged_decode_noalloc_max_bytes() bytes per GPU (16 MiB), held until
  * the process ends.  Calls whose ifn_paged_decode_workspace_bytes exceed it
  * return IFN_ERR_WORKSPACE.  The first call on a device resolves the array's
- * address and zeroes its counters (a small kernel on `stream`, ordered before
- * the decode).  Every call on a GPU shares that GPU's array, so calls that
- * overlap on one GPU (two streams or host threads) race: serialise them.
+ * address on the host; the array is zero from load (static storage), so no
+ * call puts anything on `stream` but the decode itself, and a call made under
+ * graph capture records only that.  Every call on a GPU shares that GPU's
+ * array, so calls that overlap on one GPU (two streams, host threads or graph
+ * replays) race: serialise them.
  * Output is bit-identical to ifn_paged_decode's.
  * Replaces: nothing in the reference (no counterpart); it serves the callers
  * that cannot allocate, with ifn_paged_decode's semantics.

@@ -38,7 +38,9 @@ DEVICE_FLAGS = [
 # Per-source extras for the prefill kernel.  It rescales its fp32 accumulators with VALU work
 # inside the key loop; with the accumulators in AGPRs the compiler copies all of them to VGPRs and
 # back every iteration, so its MFMAs are selected in the VGPR form.  Its maxima run over scores
-# that are never NaN (masked keys are -inf), so fmaxf needs no NaN-quieting of its operands.
+# that are never NaN for finite inputs (masked keys are -inf), so fmaxf needs no NaN-quieting of
+# its operands.  The precondition -- finite queries and K/V -- is part of the documented interface
+# (the header's layout notes); with a NaN or Inf among the inputs the prefill output is unspecified.
 FILE_FLAGS = {
     "paged_prefill_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
     # The whole-row decode kernel's first nine arguments (plan, pool, tables, query, sizes, grid) are

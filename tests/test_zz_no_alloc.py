@@ -77,3 +77,53 @@ def test_noalloc_rejects_batches_beyond_its_scratch(dev):
     stream = torch.cuda.current_stream(dev).cuda_stream
     assert L.ifn_paged_decode_noalloc(t.data_ptr(), t.data_ptr(), t.data_ptr(), 1, i.data_ptr(), 256, i.data_ptr(),
                                       None, B, hq, 8, 128, 16, 4096, 0.0, stream) == _capi.IFN_ERR_WORKSPACE
+
+
+def test_noalloc_per_segment_kernel_repeated(dev):
+    """Token rows other than 2 KiB take the per-segment kernel, which also keeps its tickets and
+    partial states in the static scratch: repeated calls (leftover tickets would show up as a
+    wrong merge) equal ifn_paged_decode bit for bit."""
+    L = _capi.lib()
+    g = torch.Generator(device=dev).manual_seed(11)
+    for hq, hkv, d in ((8, 2, 128), (8, 4, 64)):
+        say(f"noalloc per-segment hq={hq} hkv={hkv} d={d}")
+        lens = [900, 1, 64, 2000, 333, 17]
+        pool, q, bt, sl, mp = _inputs(dev, g, lens, hq, hkv, d, 400)
+        for rep in range(3):
+            ref, got = _pair(L, dev, pool, q, bt, sl, None, mp, hq, hkv, d, mp * 16)
+            assert torch.equal(ref.view(torch.int16), got.view(torch.int16)), f"rep {rep}: noalloc differs"
+
+
+def test_noalloc_under_graph_capture(dev):
+    """A call captured into a HIP graph (the callers this entry point is for) records only the
+    decode; every replay, with eager work and synchronisations between replays, equals the
+    workspace entry point's output bit for bit."""
+    L = _capi.lib()
+    g = torch.Generator(device=dev).manual_seed(12)
+    say("noalloc under graph capture")
+    lens = [300, 1200, 45, 700]
+    pool, q, bt, sl, mp = _inputs(dev, g, lens, 16, 8, 128, 300)
+    B, P, msl = q.shape[0], pool.shape[1], mp * 16
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    nb = L.ifn_paged_decode_workspace_bytes(B, 16, 8, 128, 16, msl)
+    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    ref = torch.empty_like(q)
+    assert L.ifn_paged_decode(ref.data_ptr(), q.data_ptr(), pool.data_ptr(), P, bt.data_ptr(), mp, sl.data_ptr(),
+                              None, B, 16, 8, 128, 16, msl, 0.0, ws.data_ptr(), nb, stream) == 0
+    got = torch.full_like(q, 7.0)
+    graph = torch.cuda.CUDAGraph()
+    torch.cuda.synchronize()
+    with torch.cuda.graph(graph):
+        s = torch.cuda.current_stream(dev).cuda_stream
+        assert L.ifn_paged_decode_noalloc(got.data_ptr(), q.data_ptr(), pool.data_ptr(), P, bt.data_ptr(), mp,
+                                          sl.data_ptr(), None, B, 16, 8, 128, 16, msl, 0.0, s) == 0
+    for rep in range(4):
+        got.fill_(7.0)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(ref.view(torch.int16), got.view(torch.int16)), f"replay {rep} differs"
+        other = torch.full_like(q, 7.0)  # eager work between replays
+        assert L.ifn_paged_decode_noalloc(other.data_ptr(), q.data_ptr(), pool.data_ptr(), P, bt.data_ptr(), mp,
+                                          sl.data_ptr(), None, B, 16, 8, 128, 16, msl, 0.0, stream) == 0
+        torch.cuda.synchronize()
+        assert torch.equal(ref.view(torch.int16), other.view(torch.int16))
