@@ -20,10 +20,11 @@ Reported:
   append_batched   the bandwidth-sized append (28 layers x 2048 tokens, one
                    launch) against 8 TB/s
   config1          the CPU-runnable case: one token's append + decode, µs per call
-  cpu_baseline     the CPU oracle (plain C port of the same algorithm) on all the
-                   host cores this process may use (one thread per block of rows),
-                   on a bounded sample of the same decode workload; the one-thread
-                   figure beside it
+  cpu_baseline     torch-CPU float32 SDPA (enable_gqa) over each row's gathered pages,
+                   on all the host cores this process may use, on a bounded sample of
+                   the same decode workload (value); the CPU oracle (plain C port of
+                   the same algorithm, rows split over the same threads, and on one
+                   thread) beside it as c_port
 """
 from __future__ import annotations
 
@@ -96,9 +97,15 @@ def _compact(pool_layer, table, lens, bs=16):
 
 
 def run_cpu_baseline(w, pool_layer, q, seconds: float) -> dict:
-    """The oracle on config-2 decode rows of one layer: all rows per pass, rows split over the host
-    threads (one block of rows each), repeated for about ``seconds``; then the same on one thread
-    for about a third of that."""
+    """The config-2 decode of one layer on the host cores, two ways, for about ``seconds`` in all.
+
+    value: torch-CPU float32 scaled_dot_product_attention(enable_gqa=True) per row -- the contiguous
+    SDPA of model.py:196-200 -- after gathering the row's pages (index_select) and upcasting them, on
+    all the process's host threads; the CPU plan of BASELINE.md.  c_port: the oracle (plain C port of
+    the same algorithm) on all rows per pass, rows split over the same threads, then on one thread."""
+    import torch
+    import torch.nn.functional as F
+
     import oracle
     sub, t2 = _compact(pool_layer, w.block_tables, w.seq_lens)
     qn = q.cpu().numpy()
@@ -114,10 +121,32 @@ def run_cpu_baseline(w, pool_layer, q, seconds: float) -> dict:
             if time.perf_counter() - t0 >= budget:
                 return passes, time.perf_counter() - t0
 
-    passes, dt = timed(lambda: oracle.paged_attention_rows(qn, sub, t2, w.seq_lens, threads=threads), seconds)
+    # torch-CPU SDPA over the gathered pages
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(threads)
+    sub_t = torch.from_numpy(sub)                       # [2, pages, 16, Hkv, D] fp16
+    q_t = torch.from_numpy(qn).float()                  # [B, Hq, D]
+    tables = [torch.from_numpy(np.ascontiguousarray(t2[b, :-(-int(L) // 16)]).astype(np.int64))
+              for b, L in enumerate(w.seq_lens)]
+    hkv, d = w.num_kv_heads, w.head_dim
+
+    def sdpa_pass():
+        for b, L in enumerate(w.seq_lens):
+            L = int(L)
+            kv = sub_t.index_select(1, tables[b]).reshape(2, -1, hkv, d)[:, :L].float()  # [2, L, Hkv, D]
+            k, v = kv[0].transpose(0, 1)[None], kv[1].transpose(0, 1)[None]          # [1, Hkv, L, D]
+            F.scaled_dot_product_attention(q_t[b][None, :, None, :], k, v, enable_gqa=True)
+
+    with torch.inference_mode():
+        passes_t, dt_t = timed(sdpa_pass, seconds / 2)
+    torch.set_num_threads(prev_threads)
+    bytes_t = passes_t * sum(row_bytes)
+
+    # the C port
+    passes, dt = timed(lambda: oracle.paged_attention_rows(qn, sub, t2, w.seq_lens, threads=threads), seconds / 3)
     nbytes = passes * sum(row_bytes)
     rows1, bytes1, t0 = 0, 0, time.perf_counter()
-    while time.perf_counter() - t0 < seconds / 3:
+    while time.perf_counter() - t0 < seconds / 6:
         b = rows1 % w.batch
         oracle.paged_attention(qn[b:b + 1], sub, t2[b:b + 1], w.seq_lens[b:b + 1])
         rows1 += 1
@@ -127,11 +156,14 @@ def run_cpu_baseline(w, pool_layer, q, seconds: float) -> dict:
         affinity = len(os.sched_getaffinity(0))
     except AttributeError:
         affinity = os.cpu_count() or 1
-    return {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
-            "sample": f"CPU oracle (oracle/ifn_oracle.c, scalar C) on all 32 config-2 decode rows of layer 0, "
-                      f"{passes} passes ({nbytes / 1e6:.1f} MB algorithmic) in {dt:.1f} s, rows split over "
-                      f"{threads} threads",
-            "single_thread_GB/s": round(bytes1 / dt1 / 1e9, 4),
+    return {"value": round(bytes_t / dt_t / 1e9, 4), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"torch {torch.__version__} CPU: per config-2 decode row of layer 0, index_select of its "
+                      f"pages, fp32 upcast, scaled_dot_product_attention(enable_gqa=True); {passes_t} passes over "
+                      f"all 32 rows ({bytes_t / 1e6:.1f} MB algorithmic) in {dt_t:.1f} s on {threads} threads",
+            "c_port": {"value": round(nbytes / dt / 1e9, 4), "unit": "GB/s", "cores": threads,
+                       "sample": f"CPU oracle (oracle/ifn_oracle.c, scalar C) on all 32 rows, {passes} passes "
+                                 f"({nbytes / 1e6:.1f} MB) in {dt:.1f} s, rows split over {threads} threads",
+                       "single_thread_GB/s": round(bytes1 / dt1 / 1e9, 4)},
             "affinity_cores": affinity, "cpu_model": _cpu_model()}
 
 
