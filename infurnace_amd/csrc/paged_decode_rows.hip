@@ -49,6 +49,7 @@ constexpr int kRowsMaxBatch = 4096;  // rows per call (LDS offset table)
 constexpr int kRowsBlock = 16;       // tokens per page compiled in
 constexpr int kRowsXcds = 8;         // MI355X: workgroups dispatched round-robin over 8 XCDs
 constexpr int kMergeBatch = 16;      // split states loaded per round trip of the final merge
+constexpr int kBurst = 4;            // a wave's run of at most this many tokens is requested at once
 // Cost of starting a row, in tokens.  A range that holds the end of one row and the start of the
 // next pays a second start-up, a second merge of its waves and possibly two split merges, so the
 // split counts each non-empty row as kRowStartCost tokens longer (virtual tokens in front of it).
@@ -904,6 +905,24 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     // This wave's tokens i0 .. i1 - 1 through the ring; with_prep: the piece's preparation (kPrep)
     // runs on every wave between the first requests and the first token.
     auto ring = [&](int i0, int i1, bool with_prep) __attribute__((always_inline)) {
+      // A short run (at most kBurst tokens: short calls, row heads and tails) requests every token
+      // at once -- one round trip instead of one per S - 1 tokens.  The requests are unconditional
+      // (indices clamped), so the waits count exactly here too.  (Not with kPrep, whose prepared
+      // rows are live across the first requests.)
+      if (!kPrep && i1 > i0 && i1 - i0 <= kBurst) {
+        u32x4 kq[kBurst][2], vq[kBurst][2];
+        bool okq[kBurst];
+#pragma unroll
+        for (int s = 0; s < kBurst; ++s) issue(min(i0 + s, i1 - 1), kq[s], vq[s], okq[s]);
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int s = 0; s < kBurst; ++s)
+          if (i0 + s < i1) {
+            shift(i0 + s);
+            consume(kq[s], vq[s], okq[s]);
+          }
+        return;
+      }
       if (i1 > i0) {
 #pragma unroll
         for (int s = 0; s < S - 1; ++s) issue(min(i0 + s, i1 - 1), kb_[s], vb_[s], okb[s]);
