@@ -20,6 +20,7 @@ Reported:
   append_batched   the bandwidth-sized append (28 layers x 2048 tokens, one
                    launch) against 8 TB/s
   config1          the CPU-runnable case: one token's append + decode, µs per call
+  page_size_sweep  config 2's planned decode over 16-, 32- and 64-token pages (same bytes)
   cpu_baseline     torch-CPU float32 SDPA (enable_gqa) over each row's gathered pages,
                    on all the host cores this process may use, on a bounded sample of
                    the same decode workload (value); the CPU oracle (plain C port of
@@ -455,6 +456,74 @@ def run_decode_config(lib, hip, dev, g, stream, w, layers: int, reps: int) -> di
     return res
 
 
+def run_page_size_sweep(lib, hip, dev, g, stream, layers: int = 8, reps: int = 10) -> dict:
+    """The page-size choice (docs/roadmap.md:327): config 2's lengths and query shapes over pools of
+    the same bytes per layer (16384 x 16, 8192 x 32, 4096 x 64 tokens), each row's pages consecutive
+    ids of one seeded permutation; planned decode, HIP events around every launch, `layers` distinct
+    layer pools so that launches read cold HBM."""
+    import torch
+    w = workloads_mod().config2()
+    B, hq, hkv, d = w.batch, w.num_q_heads, w.num_kv_heads, w.head_dim
+    lens = w.seq_lens.astype(np.int32)
+    max_len = int(lens.max())
+    scale = 1.0 / np.sqrt(d)
+    sl = torch.from_numpy(lens).to(dev)
+    q = torch.randn((layers, B, hq, d), generator=g, device=dev, dtype=torch.float16)
+    out = torch.empty((B, hq, d), dtype=torch.float16, device=dev)
+    res = {"workload": "config 2 lengths (B=32, U[128,4096]), 1 GiB of K/V per layer at every page size, planned decode",
+           "layers_timed": layers, "reps": reps, "us_per_layer": {}}
+    for bs in (16, 32, 64):
+        P = 16384 * 16 // bs
+        rng = np.random.default_rng(w.seed)
+        perm = rng.permutation(P).astype(np.int32)
+        pages = -(-lens // bs)
+        table = np.zeros((B, int(-(-max_len // bs))), np.int32)
+        off = 0
+        for b in range(B):
+            table[b, :pages[b]] = perm[off:off + pages[b]]
+            off += int(pages[b])
+        bt = torch.from_numpy(table).to(dev)
+        max_pages = table.shape[1]
+        pool = torch.empty((layers, 2, P, bs, hkv, d), dtype=torch.float16, device=dev)
+        for layer in range(layers):
+            pool[layer].normal_(generator=g)
+        lb = pool[0].numel() * 2
+        ws_bytes = lib.ifn_paged_decode_workspace_bytes(B, hq, hkv, d, bs, max_len)
+        ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+        pb = lib.ifn_paged_decode_plan_bytes(B, hq, hkv, d, bs, max_pages, max_len)
+        plan = torch.zeros(max(pb, 256), dtype=torch.uint8, device=dev)
+        if lib.ifn_paged_decode_plan(plan.data_ptr(), pb, bt.data_ptr(), max_pages, sl.data_ptr(), None, None, P, B, hq,
+                                     hkv, d, bs, max_len, stream):
+            raise RuntimeError(f"page size {bs}: plan failed")
+
+        def one(layer, evs=None, j=0):
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[2 * j], stream)
+            rc = lib.ifn_paged_decode_planned(out.data_ptr(), q[layer].data_ptr(), pool.data_ptr() + layer * lb, P,
+                                              bt.data_ptr(), max_pages, sl.data_ptr(), None, B, hq, hkv, d, bs,
+                                              max_len, scale, plan.data_ptr(), pb, ws.data_ptr(), ws_bytes, stream)
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[2 * j + 1], stream)
+            if rc:
+                raise RuntimeError(f"page size {bs}: decode failed: {rc}")
+
+        for layer in range(layers):
+            one(layer)
+        torch.cuda.synchronize()
+        n = layers * reps
+        evs = hip.create(2 * n)
+        for r in range(reps):
+            for layer in range(layers):
+                one(layer, evs, r * layers + layer)
+        torch.cuda.synchronize()
+        us = float(np.mean([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(n)])) * 1e3
+        hip.destroy(evs)
+        res["us_per_layer"][str(bs)] = round(us, 2)
+        del pool
+        torch.cuda.empty_cache()
+    return res
+
+
 def run_config1(lib, hip, dev, stream, reps: int = 200) -> dict:
     """Config 1 (the CPU-runnable case): one token's append at position 511 and single-row decode over
     512 tokens, timed as two launches (ifn_store_kv + ifn_paged_decode) and as one fused launch
@@ -849,6 +918,9 @@ def main() -> int:
         extra["config5"]["no_churn"] = run_decode_config(lib, hip, dev, g, stream, workloads.config5(), layers=36,
                                                          reps=3)
         torch.cuda.empty_cache()
+        print("[bench] page-size sweep (16/32/64-token pages) ...", file=sys.stderr, flush=True)
+        extra["page_size_sweep"] = run_page_size_sweep(lib, hip, dev, g, stream)
+        torch.cuda.empty_cache()
     else:
         cpu_pool = pool[0]
     config1 = run_config1(lib, hip, dev, stream)
@@ -908,6 +980,7 @@ def main() -> int:
         "config1": config1,
         "config4": extra.get("config4"),
         "config5": extra.get("config5"),
+        "page_size_sweep": extra.get("page_size_sweep"),
         "cpu_baseline": cpu,
     }
     print(json.dumps(result), flush=True)

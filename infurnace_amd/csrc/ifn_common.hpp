@@ -323,19 +323,22 @@ int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int
 
 // Whole-row decode (paged_decode_rows.hip), used by the decode entry points when the token row
 // (num_kv_heads x head_dim fp16) is 2 KiB and its (head_dim, group) is compiled; and its step plan.
-bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t max_pages, int32_t max_len);
+// block_size: tokens per page (16 for every compiled shape; 32 and 64 for the Qwen3 decode shapes);
+// append: the fused-append variant is needed.
+bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t max_pages, int32_t max_len,
+                           int32_t block_size = 16, bool append = false);
 size_t rows_decode_ws_bytes(int32_t batch, int32_t hq, int32_t d, int blocks);
 size_t rows_plan_bytes(int32_t batch, int blocks);
 int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
                      const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
-                     int blocks, hipStream_t stream);
+                     int blocks, hipStream_t stream, int32_t block_size = 16);
 // prep (non-null): the fused pre-append variant; ap then carries the slots and the pool, and q is unused.
 // px (non-null): shared-prefix mode (DecodePrefix), without append or plan.
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
                        const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
-                       const DecodePrep* prep = nullptr, const DecodePrefix* px = nullptr);
+                       const DecodePrep* prep = nullptr, const DecodePrefix* px = nullptr, int32_t block_size = 16);
 bool rows_prep_supported(int32_t hq, int32_t hkv, int32_t d);
 
 }  // namespace ifn

@@ -764,9 +764,11 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
   if (batch < 0 || num_pages < 1 || max_pages_per_seq < 1 || num_q_heads < 1 ||
       num_kv_heads < 1 || head_dim < 1 || max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
     return IFN_ERR_INVALID_ARGUMENT;
-  if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
-  const bool rows = rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len);
+  const bool rows = rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len,
+                                          block_size, append && prep == nullptr);
+  // pages of other sizes than 16 tokens: the whole-row kernel, where it compiles them, only
+  if (block_size != kBlock && (!rows || prep != nullptr)) return IFN_ERR_UNSUPPORTED;
   DecodeKernel k = rows ? nullptr
                         : pick_decode(head_dim, num_q_heads / num_kv_heads,
                                       append ? DecodeMode::kAppend
@@ -799,7 +801,7 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
                               static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
                               seq_lens, active_mask, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
                               scale * kLog2e, workspace, blocks, ap, cached, static_cast<const int32_t*>(plan),
-                              reinterpret_cast<hipStream_t>(stream), prep);
+                              reinterpret_cast<hipStream_t>(stream), prep, nullptr, block_size);
   }
   size_t off_ml, off_o;
   decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim, int64_t(blocks) * kWavesPerBlock,
@@ -849,10 +851,11 @@ extern "C" int ifn_paged_decode_append(void* out, const void* query, void* kv_po
 extern "C" size_t ifn_paged_decode_plan_bytes(int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                                               int32_t head_dim, int32_t block_size, int32_t max_pages_per_seq,
                                               int32_t max_seq_len) {
-  if (batch < 1 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 || block_size != ifn::kBlock ||
+  if (batch < 1 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 || block_size < 1 ||
       num_q_heads % num_kv_heads != 0 || max_pages_per_seq < 1 || max_seq_len < 0)
     return 0;
-  if (!ifn::rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len))
+  if (!ifn::rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len,
+                                  block_size))
     return 0;
   return ifn::rows_plan_bytes(batch, ifn::decode_blocks());
 }
@@ -867,16 +870,17 @@ extern "C" int ifn_paged_decode_plan(void* plan, size_t plan_bytes, const int32_
   if (batch < 0 || num_pages < 1 || max_pages_per_seq < 1 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 ||
       max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
     return IFN_ERR_INVALID_ARGUMENT;
-  if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
+  if (block_size < 1) return IFN_ERR_INVALID_ARGUMENT;
   if (batch == 0) return IFN_OK;
-  if (!rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len))
-    return IFN_OK;  // these shapes decode without a plan; the planned entry points ignore it
+  if (!rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len, block_size))
+    return block_size == kBlock ? IFN_OK : IFN_ERR_UNSUPPORTED;  // 16: these shapes decode without a plan
   const int blocks = decode_blocks();
   if (plan == nullptr || plan_bytes < rows_plan_bytes(batch, blocks)) return IFN_ERR_WORKSPACE;
   IFN_CHECK_ALIGN16(plan);
   if (device_cu_count() < 1) return IFN_ERR_HIP;
   return rows_plan_launch(static_cast<int32_t*>(plan), block_tables, max_pages_per_seq, seq_lens, active_mask,
-                          slot_mapping, num_pages, batch, max_seq_len, blocks, reinterpret_cast<hipStream_t>(stream));
+                          slot_mapping, num_pages, batch, max_seq_len, blocks, reinterpret_cast<hipStream_t>(stream),
+                          block_size);
 }
 
 extern "C" int ifn_paged_decode_planned(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,

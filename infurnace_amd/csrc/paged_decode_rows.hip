@@ -177,6 +177,7 @@ struct RowPiece {
 // Step plan: one workgroup writes the header, the offsets and every range's record.
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanTabWords = 16384;  // block tables up to this many entries are staged in LDS
+template <int PB>  // tokens per page
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
     int32_t* __restrict__ plan, const int32_t* __restrict__ block_tables, int32_t max_pages,
     const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, const int32_t* __restrict__ slots,
@@ -188,8 +189,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
   __shared__ int s_len[kRowsMaxBatch];    // keys of each row
   __shared__ int s_tab[kPlanTabWords];    // the block table, when it fits
   const int tid = threadIdx.x;
-  const int cap = min(max_pages * kRowsBlock, max_len);
-  const int64_t num_slots = num_pages * kRowsBlock;
+  const int cap = min(max_pages * PB, max_len);
+  const int64_t num_slots = num_pages * PB;
   // Every load the plan depends on goes out at launch, in one round trip: the rows' lengths, flags
   // and slots and, when it fits in LDS (config 2: 32 KB), the whole block table -- so that the page
   // ids of the ranges' first windows come from LDS instead of a second round trip.
@@ -302,8 +303,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
     for (int k = 0; k < kIdBatch; ++k) {
       const int r = min(r0 + k * kPlanWaves, nb - 1);
       const int b = s_p0[0][r];
-      const int pg0 = b >= 0 ? s_p0[1][r] / kRowsBlock : 0;
-      const int npg = b >= 0 ? (s_p0[2][r] - 1) / kRowsBlock - pg0 + 1 : 1;
+      const int pg0 = b >= 0 ? s_p0[1][r] / PB : 0;
+      const int npg = b >= 0 ? (s_p0[2][r] - 1) / PB - pg0 + 1 : 1;
       const int64_t at = int64_t(max(b, 0)) * max_pages + pg0 + min(lane, npg - 1);
       id[k] = tab_lds ? s_tab[at] : block_tables[at];
     }
@@ -370,9 +371,11 @@ __device__ __forceinline__ u32x4 pack_h8(const float (&x)[8]) {
 // ml[((seg * nstates + s) * G + g) * 2 + {0,1}], o[((seg * nstates + s) * G + g) * D + dim], written
 // by an earlier launch on the stream) and writes fp16.  A row of exactly that length is its prefix
 // states alone.  Shorter rows are attended in full.  No step plan is read in this mode.
-template <int D, int G, int HKV, int S, bool kAppend, bool kStream, bool kPrep = false, bool kCascade = false>
 // The arguments the first loads depend on come first (plan, pool, tables, query, the sizes and the
-// grid), so that they can be preloaded into scalar registers at dispatch.  nb is gridDim.x.
+// grid), so that they can be preloaded into scalar registers at dispatch.  nb is gridDim.x.  PB:
+// tokens per page.
+template <int D, int G, int HKV, int S, bool kAppend, bool kStream, bool kPrep = false, bool kCascade = false,
+          int PB = kRowsBlock>
 __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     const int32_t* __restrict__ plan, const f16* __restrict__ pool, const int32_t* __restrict__ block_tables,
     const f16* __restrict__ q, int32_t batch, int32_t max_pages, int32_t max_len, int32_t nb_arg,
@@ -405,9 +408,9 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
   const int lane = tid % kWave;
-  const int cap = min(max_pages * kRowsBlock, max_len);
-  const int pk = kCascade ? max(px.pages, 0) * kRowsBlock : 0;  // prefix keys of a cascade row
-  const int64_t num_slots = num_pages * kRowsBlock;
+  const int cap = min(max_pages * PB, max_len);
+  const int pk = kCascade ? max(px.pages, 0) * PB : 0;  // prefix keys of a cascade row
+  const int64_t num_slots = num_pages * PB;
   const int64_t nb = nb_arg;
   // XCD remap, as a select (a branch here would make the first kernel-argument loads wait apart)
   const int bid = int(blockIdx.x), nbi = nb_arg;
@@ -735,7 +738,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
 
   const int hd = lane / LPH, col = lane % LPH;
   const int off0 = hd * D + 8 * col, off1 = off0 + 8 * LPH;  // this lane's two chunks of a token row
-  const int64_t v_off = num_pages * kRowsBlock * int64_t(ROW);
+  const int64_t v_off = num_pages * PB * int64_t(ROW);
 
   int pend_n = 0, pend_b0 = 0, pend_b1 = 0, pend_f0 = 0, pend_f1 = 0, pend_np0 = 0, pend_np1 = 0;
   bool pend_c0 = false, pend_c1 = false;  // kCascade: the pending row is a cascade row
@@ -777,7 +780,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         app_pos = pos;
         k_maker = wave == G;
         v_maker = wave == G + 1;
-        app_page = block_tables[int64_t(b) * max_pages + pos / kRowsBlock];  // read when the token comes up
+        app_page = block_tables[int64_t(b) * max_pages + pos / PB];  // read when the token comes up
       }
       if (q_maker || k_maker) {
         load_pairs<D>(pp.rope + int64_t(pos_ok ? pos : 0) * D, col, pc, psn);
@@ -818,8 +821,8 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         qv[g][1] = *reinterpret_cast<const f16x8*>(&s_q[g][off1]);
       }
     };
-    const int pg0 = a / kRowsBlock;
-    const int npg = (e - 1) / kRowsBlock - pg0 + 1;
+    const int pg0 = a / PB;
+    const int npg = (e - 1) / PB - pg0 + 1;
     const int32_t* bt = block_tables + int64_t(b) * max_pages + pg0;
     int ids0 = pi == 0 && from_plan ? ids_pl : bt[min(lane, npg - 1)];
     int ids1 = bt[min(lane + kWave, npg - 1)];
@@ -828,7 +831,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     // this wave's tokens: positions a + wave + 8 i, i < nw
     const int rem = e - a - wave;
     const int nw = rem > 0 ? (rem + kRowsWaves - 1) / kRowsWaves : 0;
-    auto rel_page = [&](int i) { return (a + wave + kRowsWaves * i) / kRowsBlock - pg0; };
+    auto rel_page = [&](int i) { return (a + wave + kRowsWaves * i) / PB - pg0; };
     auto page_of = [&](int i) -> int {
       const int rp = rel_page(i);
       return (rp >> 6) == cur_w ? __builtin_amdgcn_readlane(ids0, rp & 63) : __builtin_amdgcn_readlane(ids1, rp & 63);
@@ -844,7 +847,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       const int p = a + wave + kRowsWaves * i;
       const int phys = page_of(i);
       ok = phys >= 0 && int64_t(phys) < num_pages;
-      const int64_t tok = int64_t(ok ? phys : 0) * kRowsBlock + p % kRowsBlock;
+      const int64_t tok = int64_t(ok ? phys : 0) * PB + p % PB;
       const f16* kb = pool + tok * ROW;
       const f16* vb = pool + v_off + tok * ROW;
       if constexpr (kAppend) {
@@ -964,7 +967,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
         const int phys = app_page;
         bool ok = phys >= 0 && int64_t(phys) < num_pages;
         u32x4 kr[2], vr[2];
-        if (ok && int64_t(phys) * kRowsBlock + app_pos % kRowsBlock == slot_b) {
+        if (ok && int64_t(phys) * PB + app_pos % PB == slot_b) {
           kr[0] = *reinterpret_cast<const u32x4*>(&s_app[0][off0]);
           kr[1] = *reinterpret_cast<const u32x4*>(&s_app[0][off1]);
           vr[0] = *reinterpret_cast<const u32x4*>(&s_app[1][off0]);
@@ -1109,7 +1112,7 @@ static RowsKernel prep_rows() {
 }
 
 static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream, bool prep = false,
-                            bool cascade = false) {
+                            bool cascade = false, int pb = kRowsBlock) {
 #define IFN_ROWS_CASE(DD, GG, HH)                                                                  \
   if (d == DD && g == GG && hkv == HH) {                                                           \
     if (prep) return prep_rows<DD, GG, HH>();                                                      \
@@ -1118,9 +1121,23 @@ static RowsKernel pick_rows(int d, int g, int hkv, bool append, bool stream, boo
     return stream ? decode_rows_kernel<DD, GG, HH, kRowsStages, false, true>                       \
                   : decode_rows_kernel<DD, GG, HH, kRowsStages, false, false>;                     \
   }
-  IFN_ROWS_CASE(128, 1, 8) IFN_ROWS_CASE(128, 2, 8) IFN_ROWS_CASE(128, 4, 8)
-  IFN_ROWS_CASE(64, 1, 16) IFN_ROWS_CASE(64, 2, 16)
-  IFN_ROWS_CASE(256, 1, 4) IFN_ROWS_CASE(256, 2, 4)
+  // Pages of 32 and 64 tokens (the page-size choice is benchmarked on them): Qwen3 decode shapes,
+  // plain (streaming or cached loads) and fused-append variants.
+#define IFN_ROWS_PAGES(DD, GG, HH, PP)                                                                           \
+  if (d == DD && g == GG && hkv == HH && pb == PP) {                                                             \
+    if (prep || cascade) return nullptr;                                                                         \
+    if (append) return decode_rows_kernel<DD, GG, HH, kRowsStages, true, true, false, false, PP>;                \
+    return stream ? decode_rows_kernel<DD, GG, HH, kRowsStages, false, true, false, false, PP>                   \
+                  : decode_rows_kernel<DD, GG, HH, kRowsStages, false, false, false, false, PP>;                 \
+  }
+  if (pb == kRowsBlock) {
+    IFN_ROWS_CASE(128, 1, 8) IFN_ROWS_CASE(128, 2, 8) IFN_ROWS_CASE(128, 4, 8)
+    IFN_ROWS_CASE(64, 1, 16) IFN_ROWS_CASE(64, 2, 16)
+    IFN_ROWS_CASE(256, 1, 4) IFN_ROWS_CASE(256, 2, 4)
+  }
+  IFN_ROWS_PAGES(128, 2, 8, 32) IFN_ROWS_PAGES(128, 4, 8, 32)
+  IFN_ROWS_PAGES(128, 2, 8, 64) IFN_ROWS_PAGES(128, 4, 8, 64)
+#undef IFN_ROWS_PAGES
 #undef IFN_ROWS_CASE
   return nullptr;
 }
@@ -1129,12 +1146,13 @@ bool rows_prep_supported(int32_t hq, int32_t hkv, int32_t d) {
   return hkv >= 1 && hq % hkv == 0 && pick_rows(d, hq / hkv, hkv, false, true, true) != nullptr;
 }
 
-bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t max_pages, int32_t max_len) {
+bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t max_pages, int32_t max_len,
+                           int32_t block_size, bool append) {
   // the virtual token list must fit int32: batch * (cap + kRowStartCost) < 2^31
-  const int64_t cap = std::min<int64_t>(int64_t(max_pages) * kRowsBlock, max_len);
+  const int64_t cap = std::min<int64_t>(int64_t(max_pages) * block_size, max_len);
   return batch >= 1 && batch <= kRowsMaxBatch && hq % hkv == 0 && batch <= kMaxTickets &&
          int64_t(batch) * (cap + kRowStartCost) < (int64_t(1) << 31) &&
-         pick_rows(d, hq / hkv, hkv, false, true) != nullptr;
+         pick_rows(d, hq / hkv, hkv, append, true, false, false, block_size) != nullptr;
 }
 
 size_t rows_decode_ws_bytes(int32_t batch, int32_t hq, int32_t d, int blocks) {
@@ -1146,9 +1164,12 @@ size_t rows_plan_bytes(int32_t batch, int blocks) { return plan_words(batch, blo
 
 int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
                      const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
-                     int blocks, hipStream_t stream) {
-  decode_plan_kernel<<<dim3(1), dim3(kPlanThreads), 0, stream>>>(plan, block_tables, max_pages, seq_lens, active,
-                                                                  slots, num_pages, batch, max_len, blocks);
+                     int blocks, hipStream_t stream, int32_t block_size) {
+  auto k = block_size == 64 ? decode_plan_kernel<64> : block_size == 32 ? decode_plan_kernel<32>
+                                                                         : decode_plan_kernel<kRowsBlock>;
+  if (block_size != kRowsBlock && block_size != 32 && block_size != 64) return IFN_ERR_UNSUPPORTED;
+  k<<<dim3(1), dim3(kPlanThreads), 0, stream>>>(plan, block_tables, max_pages, seq_lens, active, slots, num_pages,
+                                                batch, max_len, blocks);
   return ifn_launch_status();
 }
 
@@ -1156,9 +1177,9 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
                        const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
-                       const DecodePrep* prep, const DecodePrefix* px) {
+                       const DecodePrep* prep, const DecodePrefix* px, int32_t block_size) {
   if (px != nullptr && (ap.pool != nullptr || prep != nullptr)) return IFN_ERR_UNSUPPORTED;
-  RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached, prep != nullptr, px != nullptr);
+  RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached, prep != nullptr, px != nullptr, block_size);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   size_t off_ml, off_o;
   rows_ws_layout(batch, hq, d, blocks, &off_ml, &off_o);

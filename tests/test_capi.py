@@ -69,7 +69,8 @@ def test_paged_decode_host_validation():
 
     assert call(out=None) == _capi.IFN_ERR_INVALID_ARGUMENT
     assert call(hq=12, hkv=8) == _capi.IFN_ERR_INVALID_ARGUMENT
-    assert call(bs=32) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(bs=24) == _capi.IFN_ERR_UNSUPPORTED  # page sizes compiled: 16, and 32 / 64 for Qwen3 shapes
+    assert call(bs=32, hq=8, hkv=8) == _capi.IFN_ERR_UNSUPPORTED  # group 1 has 16-token pages only
     assert call(hq=24) == _capi.IFN_ERR_UNSUPPORTED  # group 3 not compiled
     assert call(d=96) == _capi.IFN_ERR_UNSUPPORTED
     assert call(q=A + 4) == _capi.IFN_ERR_ALIGNMENT
@@ -135,7 +136,8 @@ def test_shared_prefix_decode_host_validation():
     assert call(S=-1) == _capi.IFN_ERR_INVALID_ARGUMENT
     assert call(S=257) == _capi.IFN_ERR_INVALID_ARGUMENT  # more shared pages than table columns
     assert call(hq=12, hkv=8) == _capi.IFN_ERR_INVALID_ARGUMENT
-    assert call(bs=32) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(bs=24) == _capi.IFN_ERR_UNSUPPORTED  # page sizes compiled: 16, and 32 / 64 for Qwen3 shapes
+    assert call(bs=32, hq=8, hkv=8) == _capi.IFN_ERR_UNSUPPORTED  # group 1 has 16-token pages only
     assert call(d=256, hq=16) == _capi.IFN_ERR_UNSUPPORTED  # the prefix pass (MFMA) covers D 64 and 128
     assert call(q=A + 4) == _capi.IFN_ERR_ALIGNMENT
     assert call(B=0) == _capi.IFN_OK
