@@ -364,6 +364,34 @@ int ifn_paged_decode_prep_append(void* out, const float* q, const float* k, cons
                                  void* stream);
 
 /*
+ * One prefill chunk of one layer from the fp32 projections, in one launch:
+ * the pre-append of ifn_qk_norm_rope_append (q/k RMSNorm and rotary, k/v cast
+ * to fp16 and stored) and the causal attention of ifn_paged_prefill over the
+ * result.  Token t of the chunk has position query_start + t, for its rotary
+ * angle and for its cache slot block_table[p / 16] * 16 + p % 16 (slots whose
+ * page id is outside the pool are not written, and their keys are not
+ * attended).  q: fp32 [num_q_tokens][num_q_heads][head_dim]; k, v: fp32
+ * [num_q_tokens][num_kv_heads][head_dim]; the other arguments as in those two
+ * calls.  `out` and the pool are bit-identical to ifn_qk_norm_rope_append(...)
+ * with positions query_start + t and those slots, followed by
+ * ifn_paged_prefill(...) on the fp16 query; the fp16 query itself is not
+ * written.  Requires query_start % 32 == 0 (else IFN_ERR_UNSUPPORTED: run the
+ * two calls), query_start + num_q_tokens <= max_positions, every pointer
+ * 16-byte aligned, and the shapes ifn_paged_prefill compiles.  Same workspace
+ * as ifn_paged_prefill.
+ * Replaces: model.py:109-138 (norm, rope, attention and cache write of a
+ * prefill chunk) as docs/architecture.md:245-246's store_kv then
+ * paged_attention.
+ */
+int ifn_paged_prefill_prep_append(void* out, const float* q, const float* k, const float* v,
+                                  const float* q_norm_weight, const float* k_norm_weight,
+                                  const float* rope_table, int32_t max_positions, void* kv_pool_layer,
+                                  int64_t num_pages, const int32_t* block_table, int32_t max_pages,
+                                  int32_t query_start, int32_t num_q_tokens, int32_t num_q_heads,
+                                  int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float eps,
+                                  float scale, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Zero the K and V of each listed page in every layer of the full pool
  * [num_layers][2][num_pages][block_size][num_kv_heads][head_dim].  Ids outside
  * [0, num_pages) are skipped.

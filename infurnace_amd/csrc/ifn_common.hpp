@@ -268,6 +268,24 @@ struct PrefillAppend {
   f16* pool;  // the layer's pool (the memory the kernel reads)
 };
 
+// Fused pre-append (prefill chunk): the chunk's fp32 projections are normalised, rotated and cast
+// inside the prefill launch, as ifn_qk_norm_rope_append would do before it.  Token t of the chunk has
+// position query_start + t, for its rotary angle and for its cache slot (the table's page
+// (query_start + t) / 16).  Each wave first writes the K and V rows of the chunk's key tiles it will
+// read itself to the pool (workgroups sharing a tile write identical bytes), then reads them back
+// like any other page.  Requires query_start % 32 == 0, query_start + T <= max_pos and 16-byte
+// aligned q, k, v, weights and table.
+struct PrefillPrep {
+  const float* q;         // [T][Hq][D]
+  const float* k;         // [T][Hkv][D]
+  const float* v;         // [T][Hkv][D]
+  const float* q_norm_w;  // [D]
+  const float* k_norm_w;  // [D]
+  const float* rope;      // [max_pos][D]: cos of the D/2 angles, then their sin
+  f16* pool;              // the layer's pool (written, then read)
+  float eps;
+};
+
 // Shared-prefix mode of the prefill kernels: every query row sees keys [0, key_len) (no causal
 // mask) and each key split writes its result unnormalised, as the state (m, l, O), for a later
 // merge: ml[((seg * stride + split) * G + g) * 2 + {0,1}], o[((seg * stride + split) * G + g) * D + dim]
@@ -314,7 +332,7 @@ size_t wide_prefill_ws_bytes(int32_t T, int32_t query_start, int32_t hq, int32_t
 int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* table,
                         int32_t query_start, int32_t T, int32_t hq, int32_t hkv, int32_t d, float scale_log2,
                         void* workspace, size_t workspace_bytes, const PrefillAppend& ap, int cus,
-                        hipStream_t stream);
+                        hipStream_t stream, const PrefillPrep* prep = nullptr);
 // The shared-prefix pass on that kernel (same contract as prefix_pass / prefix_pass_splits).
 int wide_prefix_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus);
 int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,

@@ -153,3 +153,43 @@ extern "C" int ifn_paged_prefill_append(void* out, const void* query, void* kv_p
                             ifn::PrefillAppend{static_cast<const ifn::f16*>(new_k), static_cast<const ifn::f16*>(new_v),
                                                static_cast<ifn::f16*>(kv_pool_layer)});
 }
+
+extern "C" int ifn_paged_prefill_prep_append(void* out, const float* q, const float* k, const float* v,
+                                             const float* q_norm_weight, const float* k_norm_weight,
+                                             const float* rope_table, int32_t max_positions, void* kv_pool_layer,
+                                             int64_t num_pages, const int32_t* block_table, int32_t max_pages,
+                                             int32_t query_start, int32_t num_q_tokens, int32_t num_q_heads,
+                                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size, float eps,
+                                             float scale, void* workspace, size_t workspace_bytes, void* stream) {
+  using namespace ifn;
+  if (out == nullptr || q == nullptr || k == nullptr || v == nullptr || q_norm_weight == nullptr ||
+      k_norm_weight == nullptr || rope_table == nullptr || kv_pool_layer == nullptr || block_table == nullptr)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (num_pages < 1 || max_pages < 1 || query_start < 0 || num_q_tokens < 0 || num_q_heads < 1 ||
+      num_kv_heads < 1 || head_dim < 2 || head_dim % 2 != 0 || num_q_heads % num_kv_heads != 0 ||
+      max_positions < 1 || !(eps >= 0.f))
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (block_size != kPBlock) return IFN_ERR_UNSUPPORTED;
+  if (!wide_prefill_supported(num_q_heads, num_kv_heads, head_dim)) return IFN_ERR_UNSUPPORTED;
+  if (query_start % 32 != 0) return IFN_ERR_UNSUPPORTED;  // a key tile must be wholly before or in the chunk
+  IFN_CHECK_ALIGN16(out);
+  IFN_CHECK_ALIGN16(q);
+  IFN_CHECK_ALIGN16(k);
+  IFN_CHECK_ALIGN16(v);
+  IFN_CHECK_ALIGN16(q_norm_weight);
+  IFN_CHECK_ALIGN16(k_norm_weight);
+  IFN_CHECK_ALIGN16(rope_table);
+  IFN_CHECK_ALIGN16(kv_pool_layer);
+  if (num_q_tokens == 0) return IFN_OK;
+  if (int64_t(query_start) + num_q_tokens > int64_t(max_pages) * kPBlock)
+    return IFN_ERR_INVALID_ARGUMENT;  // keys past the end of the block table
+  if (int64_t(query_start) + num_q_tokens > max_positions) return IFN_ERR_INVALID_ARGUMENT;  // past the table
+  const int cus = device_cu_count();
+  if (cus < 1) return IFN_ERR_HIP;
+  if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
+  const PrefillPrep prep{q, k, v, q_norm_weight, k_norm_weight, rope_table, static_cast<f16*>(kv_pool_layer), eps};
+  return wide_prefill_launch(static_cast<f16*>(out), nullptr, static_cast<const f16*>(kv_pool_layer), num_pages,
+                             block_table, query_start, num_q_tokens, num_q_heads, num_kv_heads, head_dim,
+                             scale * kLog2e, workspace, workspace_bytes, PrefillAppend{nullptr, nullptr, nullptr}, cus,
+                             reinterpret_cast<hipStream_t>(stream), &prep);
+}

@@ -28,6 +28,10 @@
 //    lazy rescale of the running maximum (slack 2^8); row sums add the fp16 probabilities.
 //  * Epilogue: the W key groups merge log-sum-exp style through LDS, each wave finishing its share
 //    of the output; then the key-split merge and the fp16 stores.
+//  * Fused pre-append (kPrep): the chunk's queries, keys and values arrive as fp32 projections.
+//    Each wave first normalises, rotates and casts the K and V rows of the chunk tiles it will
+//    read and writes them to the pool, and the workgroup prepares its own queries straight into the
+//    LDS staging; the attention then runs as in the plain kernel.
 #include "ifn_common.hpp"
 
 namespace ifn {
@@ -188,11 +192,64 @@ __device__ __forceinline__ void pin_probs(f16x8 (&p)[RT][2]) {
 #endif
 }
 
-template <int D, int G, int RT, int W, bool kAppend>
+// ---- fused pre-append of a prefill chunk --------------------------------------------------
+// A row of D fp32 dims is normalised and rotated by D / 16 lanes, lane e of the row's group holding
+// the rotary pairs 8 e .. 8 e + 7: dims 8 e .. 8 e + 7 (x1) and D / 2 + 8 e .. (x2).
+// ifn_qk_norm_rope_append holds pair p in lane p of a wave and adds the pairs' squares with a
+// butterfly over lane offsets 1, 2, 4, ..; here the butterfly's first three levels are this lane's
+// own eight pairs, paired the same way, and the remaining levels lane offsets 1, 2, 4 within the
+// row's group.  The same additions of the same operands give the same sum, bit for bit (for D = 64
+// that kernel's last level adds its idle lanes' zeros to a non-negative sum, which changes
+// nothing); the per-pair arithmetic is the shared norm_rope_pair, so q and k are identical to its.
+template <int D>
+struct PrepRows {
+  static constexpr int kLanes = D / 16;         // lanes per row
+  static constexpr int kRows = kWave / kLanes;  // rows per wave pass
+};
+struct Pairs8 {
+  f32x4 a[2];  // element 8 e .. 8 e + 7 of the row's first half
+  f32x4 b[2];  // element D / 2 + 8 e .. of its second half
+};
+template <int D>
+__device__ __forceinline__ Pairs8 load_pairs8(const float* row, int e) {
+  const f32x4* p = reinterpret_cast<const f32x4*>(row + 8 * e);
+  const f32x4* s = reinterpret_cast<const f32x4*>(row + D / 2 + 8 * e);
+  return Pairs8{{p[0], p[1]}, {s[0], s[1]}};
+}
+__device__ __forceinline__ u32x4 pack_f16x8(const f32x4& lo, const f32x4& hi) {
+  return __builtin_bit_cast(u32x4, f16x8{f16(lo[0]), f16(lo[1]), f16(lo[2]), f16(lo[3]), f16(hi[0]), f16(hi[1]),
+                                          f16(hi[2]), f16(hi[3])});
+}
+// x normalised with the weights w and rotated by the table row cs ([cos | sin]); fp16 results as
+// two 16-byte chunks: dims 8 e .. (lo) and D / 2 + 8 e .. (hi).  Every lane of a row's group calls it.
+template <int D>
+__device__ __forceinline__ void norm_rope_row(const Pairs8& x, const Pairs8& w, const Pairs8& cs, float eps,
+                                              u32x4& lo, u32x4& hi) {
+  float s[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s[j] = pair_sq(x.a[j / 4][j % 4], x.b[j / 4][j % 4]);
+  float ss = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
+#pragma unroll
+  for (int o = 1; o < PrepRows<D>::kLanes; o <<= 1) ss += __shfl_xor(ss, o);
+  const float rs = rms_inv(ss, D, eps);
+  f32x4 y1[2], y2[2];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    float a = x.a[j / 4][j % 4], b = x.b[j / 4][j % 4];
+    norm_rope_pair(a, b, rs, w.a[j / 4][j % 4], w.b[j / 4][j % 4], cs.a[j / 4][j % 4], cs.b[j / 4][j % 4]);
+    y1[j / 4][j % 4] = a;
+    y2[j / 4][j % 4] = b;
+  }
+  lo = pack_f16x8(y1[0], y1[1]);
+  hi = pack_f16x8(y2[0], y2[1]);
+}
+
+template <int D, int G, int RT, int W, bool kAppend, bool kPrep>
 __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
     const int32_t* __restrict__ table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb,
-    int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap, PrefixOut px) {
+    int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap, PrefixOut px, PrefillPrep pp) {
+  static_assert(!(kAppend && kPrep), "one form of the fused append");
   using C = WideCfg<D, G, RT, W>;
   constexpr int kKS = C::kKSteps;
   constexpr int kDT = C::kDT;
@@ -234,7 +291,9 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
   const int64_t tok_stride = int64_t(num_kv_heads) * D;
   const int64_t v_off = num_pages * kWBlock * tok_stride;
   const int64_t page_elems = int64_t(kWBlock) * tok_stride;
-  const f16* head_pool = pool + int64_t(kvh) * D;
+  // (kPrep: the pool is read through the pointer it is written through, so no read is assumed to
+  // be independent of the pre-append's stores)
+  const f16* head_pool = (kPrep ? static_cast<const f16*>(pp.pool) : pool) + int64_t(kvh) * D;
 
   if constexpr (kAppend)
     wide_store_chunk(ap.pool, num_pages, table, query_start, T, num_kv_heads, D, ap.new_k, ap.new_v,
@@ -280,12 +339,69 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
   // chunk as zeros), for the LDS staging below.
   lds_u8* const qlds = (lds_u8*)(smem) + C::kTileBytes;
   u32x4 qst[C::kQInstr];
+  if constexpr (!kPrep) {
 #pragma unroll
-  for (int n = 0; n < C::kQInstr; ++n) {
-    const int slot = n * kWave + lane, rho = C::kQRowsPerWave * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
-    const int qi = q0 + rho % kQw;
-    const u32x4 v = ld16(q + (int64_t(min(qi, T - 1)) * hq + kvh * G + rho / kQw) * D + 8 * c);
-    qst[n] = qi < T ? v : u32x4{0u, 0u, 0u, 0u};
+    for (int n = 0; n < C::kQInstr; ++n) {
+      const int slot = n * kWave + lane, rho = C::kQRowsPerWave * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
+      const int qi = q0 + rho % kQw;
+      const u32x4 v = ld16(q + (int64_t(min(qi, T - 1)) * hq + kvh * G + rho / kQw) * D + 8 * c);
+      qst[n] = qi < T ? v : u32x4{0u, 0u, 0u, 0u};
+    }
+  } else {
+    using PR = PrepRows<D>;
+    const int e = lane % PR::kLanes, sub = lane / PR::kLanes;
+    // (1) This wave's tiles of the chunk (keys at or past query_start; query_start % 32 == 0): K
+    // normalised and rotated, V cast, both written to the pool at the table's slots.  Rows past the
+    // chunk and rows of an invalid page are not written (the attention reads zeros there).
+    const Pairs8 wk = load_pairs8<D>(pp.k_norm_w, e);
+    for (int i = 0; i < iters; ++i) {
+      const int kt = tile_of(i) * kWTile;
+      if (kt < query_start) continue;  // (uniform) a tile of earlier keys
+#pragma unroll
+      for (int op = 0; op < kWTile / PR::kRows; ++op) {
+        const int pos = kt + op * PR::kRows + sub;
+        const int t = pos - query_start;
+        const int tc = min(t, T - 1);
+        const int64_t src = (int64_t(tc) * num_kv_heads + kvh) * D;
+        const Pairs8 xk = load_pairs8<D>(pp.k + src, e);
+        const Pairs8 xv = load_pairs8<D>(pp.v + src, e);
+        const Pairs8 cs = load_pairs8<D>(pp.rope + int64_t(query_start + tc) * D, e);
+        const int page = table[(query_start + tc) / kWBlock];
+        u32x4 klo, khi;
+        norm_rope_row<D>(xk, wk, cs, pp.eps, klo, khi);
+        if (t < T && page >= 0 && int64_t(page) < num_pages) {
+          f16* kd = pp.pool + (int64_t(page) * kWBlock + pos % kWBlock) * tok_stride + int64_t(kvh) * D;
+          f16* vd = kd + v_off;
+          *reinterpret_cast<u32x4*>(kd + 8 * e) = klo;
+          *reinterpret_cast<u32x4*>(kd + D / 2 + 8 * e) = khi;
+          *reinterpret_cast<u32x4*>(vd + 8 * e) = pack_f16x8(xv.a[0], xv.a[1]);
+          *reinterpret_cast<u32x4*>(vd + D / 2 + 8 * e) = pack_f16x8(xv.b[0], xv.b[1]);
+        }
+      }
+    }
+    // (2) The workgroup's queries, normalised and rotated into the LDS staging (chunk c of row rho
+    // at c ^ (rho % 8)); wave grp prepares rows kQRowsPerWave grp .. (a row past the chunk as zeros).
+    const Pairs8 wq = load_pairs8<D>(pp.q_norm_w, e);
+#pragma unroll
+    for (int op = 0; op < (C::kQRowsPerWave + PR::kRows - 1) / PR::kRows; ++op) {
+      const int rw = op * PR::kRows + sub;
+      const int rho = C::kQRowsPerWave * grp + min(rw, C::kQRowsPerWave - 1);
+      const int qi = q0 + rho % kQw;
+      const int qc = min(qi, T - 1);
+      const Pairs8 xq = load_pairs8<D>(pp.q + (int64_t(qc) * hq + kvh * G + rho / kQw) * D, e);
+      const Pairs8 cs = load_pairs8<D>(pp.rope + int64_t(query_start + qc) * D, e);
+      u32x4 lo, hi;
+      norm_rope_row<D>(xq, wq, cs, pp.eps, lo, hi);
+      if (qi >= T) lo = hi = u32x4{0u, 0u, 0u, 0u};
+      if (rw < C::kQRowsPerWave) {
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((e ^ (rho % 8)) * 16)) = lo;
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(
+            qlds + rho * 2 * D + (((PR::kLanes + e) ^ (rho % 8)) * 16)) = hi;
+      }
+    }
+    // The pool stores are complete before any of this wave's K or V requests (it reads back only
+    // rows it wrote itself; the memory clobber keeps the compiler from hoisting them).
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
   // The window arrives before the first tiles' K and V are requested.
   asm volatile("" ::"v"(win_k.ids) : "memory");
@@ -341,7 +457,9 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
       // (page and key count are uniform; readfirstlane keeps the descriptor in scalar registers)
       const bool ok = ((fl >> h) & 1) != 0;
       const int page = __builtin_amdgcn_readfirstlane(ok ? (h == 0 ? pa : pb) : 0);
-      const int keys = __builtin_amdgcn_readfirstlane(ok ? min(max(total - (kt + 16 * h), 0), 16) : 0);
+      // (kPrep: keys from key_end on -- hidden from every row here -- read as zeros, so a tile this
+      // wave did not prepare is never read)
+      const int keys = __builtin_amdgcn_readfirstlane(ok ? min(max((kPrep ? key_end : total) - (kt + 16 * h), 0), 16) : 0);
       t.r[h] = __builtin_amdgcn_make_buffer_rsrc(const_cast<f16*>(head_pool + base + int64_t(page) * page_elems), 0,
                                                  keys * int(tok_stride) * 2, 0x00020000);
       t.add[h] = 0;
@@ -655,10 +773,13 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
 #pragma unroll
     for (int j = 0; j < C::kVInstr; ++j) vst[j] = v_load(v_tile(0, p0), j);
     // Q through LDS: Q^T as the B operand, K-step s = dims 16 s + 8 half .. + 7 of row 32 rt + col
+    // (kPrep: the staging is written already)
+    if constexpr (!kPrep) {
 #pragma unroll
-    for (int n = 0; n < C::kQInstr; ++n) {
-      const int slot = n * kWave + lane, rho = C::kQRowsPerWave * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
-      *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((c ^ (rho % 8)) * 16)) = qst[n];
+      for (int n = 0; n < C::kQInstr; ++n) {
+        const int slot = n * kWave + lane, rho = C::kQRowsPerWave * grp + slot / C::kRowChunks, c = slot % C::kRowChunks;
+        *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((c ^ (rho % 8)) * 16)) = qst[n];
+      }
     }
     __syncthreads();
 #pragma unroll
@@ -882,13 +1003,17 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
 }
 
 typedef void (*WideKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t, int32_t, int32_t,
-                           int32_t, float, PrefillWorkspace, PrefillAppend, PrefixOut);
+                           int32_t, float, PrefillWorkspace, PrefillAppend, PrefixOut, PrefillPrep);
+
+enum class WideMode { kPlain, kAppend, kPrep };
 
 // (row tiles and waves: 2 and 4 for every shape; 1 and 8 for head dim 128)
-static WideKernel pick_wide(int d, int g, int rt, int w, bool append) {
+static WideKernel pick_wide(int d, int g, int rt, int w, WideMode mode) {
 #define IFN_WIDE_CASE(DD, GG, RR, WW)                                                                \
   if (d == DD && g == GG && rt == RR && w == WW)                                                     \
-    return append ? prefill_wide_kernel<DD, GG, RR, WW, true> : prefill_wide_kernel<DD, GG, RR, WW, false>;
+    return mode == WideMode::kAppend ? prefill_wide_kernel<DD, GG, RR, WW, true, false>              \
+           : mode == WideMode::kPrep ? prefill_wide_kernel<DD, GG, RR, WW, false, true>              \
+                                     : prefill_wide_kernel<DD, GG, RR, WW, false, false>;
   IFN_WIDE_CASE(64, 1, 2, 4) IFN_WIDE_CASE(64, 2, 2, 4) IFN_WIDE_CASE(64, 4, 2, 4) IFN_WIDE_CASE(64, 8, 2, 4)
   IFN_WIDE_CASE(128, 1, 2, 4) IFN_WIDE_CASE(128, 2, 2, 4) IFN_WIDE_CASE(128, 4, 2, 4) IFN_WIDE_CASE(128, 8, 2, 4)
   IFN_WIDE_CASE(128, 1, 1, 8) IFN_WIDE_CASE(128, 2, 1, 8) IFN_WIDE_CASE(128, 4, 1, 8) IFN_WIDE_CASE(128, 8, 1, 8)
@@ -897,7 +1022,7 @@ static WideKernel pick_wide(int d, int g, int rt, int w, bool append) {
 }
 
 bool wide_prefill_supported(int32_t hq, int32_t hkv, int32_t d) {
-  return hkv >= 1 && hq % hkv == 0 && pick_wide(d, hq / hkv, 2, 4, false) != nullptr;
+  return hkv >= 1 && hq % hkv == 0 && pick_wide(d, hq / hkv, 2, 4, WideMode::kPlain) != nullptr;
 }
 
 size_t wide_prefill_ws_bytes(int32_t T, int32_t query_start, int32_t hq, int32_t hkv, int32_t d, int cus) {
@@ -907,10 +1032,12 @@ size_t wide_prefill_ws_bytes(int32_t T, int32_t query_start, int32_t hq, int32_t
 int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* table,
                         int32_t query_start, int32_t T, int32_t hq, int32_t hkv, int32_t d, float scale_log2,
                         void* workspace, size_t workspace_bytes, const PrefillAppend& ap, int cus,
-                        hipStream_t stream) {
+                        hipStream_t stream, const PrefillPrep* prep) {
   const WidePlan p = plan_wide(T, query_start, hq, hkv, d, cus);
-  WideKernel k = pick_wide(d, hq / hkv, p.rt, p.w, ap.pool != nullptr);
+  const WideMode mode = prep != nullptr ? WideMode::kPrep : ap.pool != nullptr ? WideMode::kAppend : WideMode::kPlain;
+  WideKernel k = pick_wide(d, hq / hkv, p.rt, p.w, mode);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
+  if (prep != nullptr && (ap.pool != nullptr || query_start % kWTile != 0)) return IFN_ERR_UNSUPPORTED;
   if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
   // (the fused append indexes the chunk's K and V rows with 32-bit byte offsets)
   if (ap.pool != nullptr && int64_t(T) * hkv * d * 2 >= int64_t(1) << 31) return IFN_ERR_UNSUPPORTED;
@@ -925,7 +1052,7 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
   }
   k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(unsigned(p.w * kWave)), 0, stream>>>(
       out, q, pool, num_pages, table, query_start, T, hkv, int(p.n_qb), p.nsplit, scale_log2, ws, ap,
-      PrefixOut{nullptr, nullptr, 0, 0});
+      PrefixOut{nullptr, nullptr, 0, 0}, prep != nullptr ? *prep : PrefillPrep{});
   return ifn_launch_status();
 }
 
@@ -938,13 +1065,13 @@ int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int
                      int32_t stride, int cus, hipStream_t stream) {
   if (key_len < 1) return IFN_ERR_INVALID_ARGUMENT;
   const WidePlan p = plan_wide(batch, 0, hq, hkv, d, cus, key_len);
-  WideKernel k = pick_wide(d, hq / hkv, p.rt, p.w, false);
+  WideKernel k = pick_wide(d, hq / hkv, p.rt, p.w, WideMode::kPlain);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
   if (p.n_qb * hkv * p.nsplit > int64_t(1) << 31 || stride < p.nsplit) return IFN_ERR_UNSUPPORTED;
   k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(unsigned(p.w * kWave)), 0, stream>>>(
       nullptr, q, pool, num_pages, prefix_pages, 0, batch, hkv, int(p.n_qb), p.nsplit, scale_log2,
       PrefillWorkspace{nullptr, nullptr, nullptr}, PrefillAppend{nullptr, nullptr, nullptr},
-      PrefixOut{px_ml, px_o, key_len, stride});
+      PrefixOut{px_ml, px_o, key_len, stride}, PrefillPrep{});
   return ifn_launch_status();
 }
 

@@ -25,7 +25,8 @@ from .. import _capi
 from ._common import KVStoreError, PagedAttentionError, check_pool, current_stream, ptr
 from ._carrier import accepts_carriers
 
-__all__ = ["qk_norm_rope_append", "qk_norm_rope_store_and_decode", "rope_table", "zero_pages", "copy_pages"]
+__all__ = ["qk_norm_rope_append", "qk_norm_rope_store_and_decode", "qk_norm_rope_append_and_prefill", "rope_table",
+           "zero_pages", "copy_pages"]
 
 
 def rope_table(max_positions: int, head_dim: int, base: float, device=None) -> torch.Tensor:
@@ -232,4 +233,90 @@ def qk_norm_rope_store_and_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
         return paged_attention(q16, kv_pool, block_tables, sequence_lengths, active_mask, layer=layer, scale=scale,
                                out=out, block_size=block_size, max_seq_len=max_seq_len, plan=plan)
     _capi.check("ifn_paged_decode_prep_append", status)
+    return out
+
+
+def qk_norm_rope_append_and_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, q_norm_weight: torch.Tensor,
+                                    k_norm_weight: torch.Tensor, rope: torch.Tensor, kv_pool: torch.Tensor,
+                                    block_table: torch.Tensor, *, query_start: int, layer: int = 0,
+                                    eps: float = 1e-6, scale: float | None = None, out: torch.Tensor | None = None,
+                                    block_size: int = 16, validate: bool = False) -> torch.Tensor:
+    """A prefill chunk of one layer from fp32 projections: pre-append and attention in one launch.
+
+    ``ifn_paged_prefill_prep_append``: the same ``out`` and pool as ``qk_norm_rope_append(q, k, v,
+    ..., positions, slots, None, kv_pool, layer=layer, eps=eps)`` with positions query_start + t and
+    their slots in ``block_table``, followed by ``paged_attention(q16, kv_pool, block_table, None,
+    None, query_start=query_start)`` -- the norm / rope / attention / cache write of a prefill
+    chunk, model.py:109-138.  q fp32 [T, Hq, D], k / v fp32 [T, Hkv, D].  A chunk the fused kernel
+    does not take (query_start not a multiple of 32, an unaligned input) runs the two launches
+    instead.  ``validate``: every table entry the chunk's keys use names a page of the pool
+    (checked before the launch; a debug mode that synchronises).
+    """
+    from .paged_attention import _check, _validate_pages, paged_attention, workspace_for
+    pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
+    dev = pool_layer.device
+    if bs != block_size:
+        raise PagedAttentionError(f"kv_pool block_size {bs} != block_size argument {block_size}")
+    if not isinstance(q, torch.Tensor) or q.ndim != 3:
+        raise PagedAttentionError("q must be a rank-3 [T, Hq, D] tensor")
+    n, hq = q.shape[0], q.shape[1]
+    if hq % hkv:
+        raise PagedAttentionError(f"num_q_heads {hq} is not a multiple of num_kv_heads {hkv}")
+    _f32("q", q, (n, hq, d), dev)
+    _f32("k", k, (n, hkv, d), dev)
+    _f32("v", v, (n, hkv, d), dev)
+    _f32("q_norm_weight", q_norm_weight, (d,), dev)
+    _f32("k_norm_weight", k_norm_weight, (d,), dev)
+    if not isinstance(rope, torch.Tensor) or rope.ndim != 2:
+        raise KVStoreError("rope must be the rank-2 table of rope_table()")
+    _f32("rope", rope, (rope.shape[0], d), dev)
+    if not (eps >= 0 and math.isfinite(eps)):
+        raise KVStoreError("eps must be a finite non-negative number")
+    query_start = int(query_start)
+    if query_start < 0:
+        raise PagedAttentionError(f"query_start must be non-negative, got {query_start}")
+    if query_start + n > rope.shape[0]:
+        raise PagedAttentionError(f"positions up to {query_start + n - 1} are past the rope table's "
+                                  f"{rope.shape[0]} rows")
+    if not isinstance(block_table, torch.Tensor):
+        raise PagedAttentionError("block_table must be a torch.Tensor")
+    table = block_table.reshape(-1) if block_table.ndim == 2 and block_table.shape[0] == 1 else block_table
+    if table.ndim != 1:
+        raise PagedAttentionError("block_table must be [max_pages] or [1, max_pages]")
+    max_pages = table.shape[0]
+    _check("block_table", table, (max_pages,), (torch.int32,), dev)
+    if query_start + n > max_pages * bs:
+        raise PagedAttentionError(f"query_start + T = {query_start + n} exceeds the table's {max_pages * bs} slots")
+    if out is None:
+        out = torch.empty((n, hq, d), dtype=torch.float16, device=dev)
+    else:
+        _check("out", out, (n, hq, d), (torch.float16,), dev)
+    if scale is None:
+        scale = 1.0 / math.sqrt(d)
+    if not scale > 0:
+        raise PagedAttentionError(f"scale must be positive, got {scale}")
+    if n == 0:
+        return out
+    if validate:
+        _validate_pages(table[None, :], torch.full((1,), query_start + n, dtype=torch.int64, device=dev), P, bs,
+                        "qk_norm_rope_append_and_prefill")
+    stream = current_stream(dev)
+    lib = _capi.lib()
+    status = _capi.IFN_ERR_UNSUPPORTED
+    aligned = all(t.data_ptr() % 16 == 0 for t in (q, k, v, q_norm_weight, k_norm_weight, rope, out, pool_layer))
+    if query_start % 32 == 0 and aligned:
+        nbytes = lib.ifn_paged_prefill_workspace_bytes(n, query_start, hq, hkv, d, bs)
+        ws = workspace_for(dev, stream, nbytes)
+        status = lib.ifn_paged_prefill_prep_append(
+            ptr(out), ptr(q), ptr(k), ptr(v), ptr(q_norm_weight), ptr(k_norm_weight), ptr(rope), rope.shape[0],
+            ptr(pool_layer), P, ptr(table), max_pages, query_start, n, hq, hkv, d, bs, float(eps), float(scale),
+            ptr(ws), ws.numel(), stream)
+    if status == _capi.IFN_ERR_UNSUPPORTED:
+        pos = torch.arange(query_start, query_start + n, dtype=torch.int32, device=dev)
+        slots = table[torch.div(pos, bs, rounding_mode="floor").long()] * bs + pos % bs
+        q16 = qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope, pos, slots.to(torch.int32), None,
+                                  kv_pool, layer=layer, eps=eps)
+        return paged_attention(q16, kv_pool, table, None, None, layer=layer, query_start=query_start, scale=scale,
+                               out=out, block_size=block_size)
+    _capi.check("ifn_paged_prefill_prep_append", status)
     return out
