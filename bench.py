@@ -263,6 +263,82 @@ def run_prefill(lib, hip, dev, g, stream) -> dict:
             "two_launch_us_per_layer": round(float((ms + st_ms).sum(1).mean() * 1e3), 2)}
 
 
+def run_prefill_prep(lib, hip, dev, g, stream) -> dict:
+    """Config 3 from fp32 projections: per chunk-layer, the pre-append (q/k RMSNorm + rotary + fp16
+    cast + append) and the causal attention, as two launches (ifn_qk_norm_rope_append then
+    ifn_paged_prefill) and as one (ifn_paged_prefill_prep_append); HIP events around each
+    chunk-layer's launches."""
+    import torch
+    from infurnace_amd import workloads
+    from infurnace_amd.kernels import rope_table
+    w = workloads.config3()
+    L, hq, hkv, d, C = w.num_layers, w.num_q_heads, w.num_kv_heads, w.head_dim, w.chunk
+    pool = torch.zeros((L, 2, w.num_pages, 16, hkv, d), dtype=torch.float16, device=dev)
+    q = torch.randn((L, 4, C, hq, d), generator=g, device=dev)
+    k = torch.randn((L, 4, C, hkv, d), generator=g, device=dev)
+    v = torch.randn((L, 4, C, hkv, d), generator=g, device=dev)
+    wt = 1 + 0.1 * torch.randn(d, generator=g, device=dev)
+    rope = rope_table(w.prompt_len, d, 1e6, device=dev)
+    table = torch.from_numpy(w.block_table).to(dev)
+    pos = np.arange(w.prompt_len)
+    positions = torch.from_numpy(pos.astype(np.int32)).to(dev)
+    slots = torch.from_numpy((w.block_table.astype(np.int64)[pos // 16] * 16 + pos % 16).astype(np.int32)).to(dev)
+    q16 = torch.empty((C, hq, d), dtype=torch.float16, device=dev)
+    out = torch.empty((C, hq, d), dtype=torch.float16, device=dev)
+    ws_bytes = max(lib.ifn_paged_prefill_workspace_bytes(C, c * C, hq, hkv, d, 16) for c in range(4))
+    ws = torch.zeros(ws_bytes, dtype=torch.uint8, device=dev)
+    lb = pool[0].numel() * 2
+    scale = 1.0 / np.sqrt(d)
+
+    def two(layer, c):
+        rc = lib.ifn_qk_norm_rope_append(q16.data_ptr(), q[layer, c].data_ptr(), k[layer, c].data_ptr(),
+                                         v[layer, c].data_ptr(), wt.data_ptr(), wt.data_ptr(), rope.data_ptr(),
+                                         rope.shape[0], positions.data_ptr() + 4 * c * C, slots.data_ptr() + 4 * c * C,
+                                         None, pool.data_ptr() + layer * lb, w.num_pages, C, hq, hkv, d, 16, 1e-6,
+                                         stream)
+        rc |= lib.ifn_paged_prefill(out.data_ptr(), q16.data_ptr(), pool.data_ptr() + layer * lb, w.num_pages,
+                                    table.data_ptr(), w.block_table.shape[0], c * C, C, hq, hkv, d, 16, scale,
+                                    ws.data_ptr(), ws_bytes, stream)
+        if rc:
+            raise RuntimeError(f"two-launch prefill chunk failed: {rc}")
+
+    def one(layer, c):
+        rc = lib.ifn_paged_prefill_prep_append(out.data_ptr(), q[layer, c].data_ptr(), k[layer, c].data_ptr(),
+                                               v[layer, c].data_ptr(), wt.data_ptr(), wt.data_ptr(), rope.data_ptr(),
+                                               rope.shape[0], pool.data_ptr() + layer * lb, w.num_pages,
+                                               table.data_ptr(), w.block_table.shape[0], c * C, C, hq, hkv, d, 16,
+                                               1e-6, scale, ws.data_ptr(), ws_bytes, stream)
+        if rc:
+            raise RuntimeError(f"fused prefill chunk failed: {rc}")
+
+    def timed(fn):
+        for layer in range(L):
+            for c in range(4):
+                fn(layer, c)
+        torch.cuda.synchronize()
+        evs = hip.create(2 * L * 4)
+        for layer in range(L):
+            for c in range(4):
+                j = layer * 4 + c
+                hip.hip.hipEventRecord(evs[2 * j], stream)
+                fn(layer, c)
+                hip.hip.hipEventRecord(evs[2 * j + 1], stream)
+        torch.cuda.synchronize()
+        ms = np.asarray([hip.elapsed_ms(evs[2 * j], evs[2 * j + 1]) for j in range(L * 4)]).reshape(L, 4)
+        hip.destroy(evs)
+        return ms
+
+    ms2 = timed(two)
+    ms1 = timed(one)
+    return {"prep_workload": "config 3 from fp32 projections: q/k RMSNorm + rotary + fp16 cast + append, then "
+                             "causal attention, per chunk-layer",
+            "prep_entry": "ifn_paged_prefill_prep_append (one launch per chunk-layer)",
+            "prep_fused_us_per_chunk_layer": [round(float(x), 2) for x in ms1.mean(0) * 1e3],
+            "prep_fused_us_per_layer": round(float(ms1.sum(1).mean() * 1e3), 2),
+            "prep_two_launch_us_per_chunk_layer": [round(float(x), 2) for x in ms2.mean(0) * 1e3],
+            "prep_two_launch_us_per_layer": round(float(ms2.sum(1).mean() * 1e3), 2)}
+
+
 def run_pre_append(lib, hip, dev, g, stream) -> dict:
     """Fused pre-append (q/k RMSNorm + rotary + fp16 cast + slot append) on config-3 chunks:
     512 tokens per launch, 28 layers with distinct inputs, HIP events around every launch."""
@@ -902,6 +978,7 @@ def main() -> int:
     pre_append = None
     if not args.no_prefill:
         prefill = run_prefill(lib, hip, dev, g, stream)
+        prefill.update(run_prefill_prep(lib, hip, dev, g, stream))
         pre_append = run_pre_append(lib, hip, dev, g, stream)
 
     extra = {}

@@ -352,46 +352,68 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     const int e = lane % PR::kLanes, sub = lane / PR::kLanes;
     // (1) This wave's tiles of the chunk (keys at or past query_start; query_start % 32 == 0): K
     // normalised and rotated, V cast, both written to the pool at the table's slots.  Rows past the
-    // chunk and rows of an invalid page are not written (the attention reads zeros there).
-    const Pairs8 wk = load_pairs8<D>(pp.k_norm_w, e);
-    for (int i = 0; i < iters; ++i) {
-      const int kt = tile_of(i) * kWTile;
-      if (kt < query_start) continue;  // (uniform) a tile of earlier keys
+    // chunk and rows of an invalid page are not written (the attention reads zeros there).  The
+    // work is a list of jobs (one wave pass of kRows rows each): the wave's tiles from the first one
+    // in the chunk on (tile_of is increasing), kWTile / kRows jobs per tile.  A job's loads are
+    // issued one job ahead, before the previous job's arithmetic and stores.  The queries' loads go
+    // first, so they are in flight meanwhile.
+    constexpr int kOps = kWTile / PR::kRows;
+    const int first_tile = split * W + grp, tile_step = W * nsplit;  // tile_of(i) = first_tile + i tile_step
+    const int qs_tile = query_start / kWTile;
+    const int i0 = qs_tile > first_tile ? int(ceil_div(qs_tile - first_tile, tile_step)) : 0;
+    const int nj = iters > i0 ? (iters - i0) * kOps : 0;
+    struct Job {
+      Pairs8 k, v, cs;
+      int page;
+    };
+    auto job_pos = [&](int j) __attribute__((always_inline)) {  // key position of this lane's row of job j
+      return tile_of(i0 + j / kOps) * kWTile + (j % kOps) * PR::kRows + sub;
+    };
+    auto job_load = [&](int j) __attribute__((always_inline)) -> Job {
+      const int tc = min(job_pos(min(j, nj - 1)) - query_start, T - 1);  // (past the list: a valid row again)
+      const int64_t src = (int64_t(tc) * num_kv_heads + kvh) * D;
+      return Job{load_pairs8<D>(pp.k + src, e), load_pairs8<D>(pp.v + src, e),
+                 load_pairs8<D>(pp.rope + int64_t(query_start + tc) * D, e), table[(query_start + tc) / kWBlock]};
+    };
+    // the queries' inputs (step 2)
+    constexpr int kQOps = (C::kQRowsPerWave + PR::kRows - 1) / PR::kRows;
+    Pairs8 xq[kQOps], csq[kQOps];
 #pragma unroll
-      for (int op = 0; op < kWTile / PR::kRows; ++op) {
-        const int pos = kt + op * PR::kRows + sub;
-        const int t = pos - query_start;
-        const int tc = min(t, T - 1);
-        const int64_t src = (int64_t(tc) * num_kv_heads + kvh) * D;
-        const Pairs8 xk = load_pairs8<D>(pp.k + src, e);
-        const Pairs8 xv = load_pairs8<D>(pp.v + src, e);
-        const Pairs8 cs = load_pairs8<D>(pp.rope + int64_t(query_start + tc) * D, e);
-        const int page = table[(query_start + tc) / kWBlock];
+    for (int op = 0; op < kQOps; ++op) {
+      const int rho = C::kQRowsPerWave * grp + min(op * PR::kRows + sub, C::kQRowsPerWave - 1);
+      const int qc = min(q0 + rho % kQw, T - 1);
+      xq[op] = load_pairs8<D>(pp.q + (int64_t(qc) * hq + kvh * G + rho / kQw) * D, e);
+      csq[op] = load_pairs8<D>(pp.rope + int64_t(query_start + qc) * D, e);
+    }
+    const Pairs8 wk = load_pairs8<D>(pp.k_norm_w, e);
+    if (nj > 0) {
+      Job cur = job_load(0);
+      for (int j = 0; j < nj; ++j) {
+        const Job nxt = job_load(j + 1);
+        const int pos = job_pos(j);
         u32x4 klo, khi;
-        norm_rope_row<D>(xk, wk, cs, pp.eps, klo, khi);
-        if (t < T && page >= 0 && int64_t(page) < num_pages) {
-          f16* kd = pp.pool + (int64_t(page) * kWBlock + pos % kWBlock) * tok_stride + int64_t(kvh) * D;
+        norm_rope_row<D>(cur.k, wk, cur.cs, pp.eps, klo, khi);
+        if (pos - query_start < T && cur.page >= 0 && int64_t(cur.page) < num_pages) {
+          f16* kd = pp.pool + (int64_t(cur.page) * kWBlock + pos % kWBlock) * tok_stride + int64_t(kvh) * D;
           f16* vd = kd + v_off;
           *reinterpret_cast<u32x4*>(kd + 8 * e) = klo;
           *reinterpret_cast<u32x4*>(kd + D / 2 + 8 * e) = khi;
-          *reinterpret_cast<u32x4*>(vd + 8 * e) = pack_f16x8(xv.a[0], xv.a[1]);
-          *reinterpret_cast<u32x4*>(vd + D / 2 + 8 * e) = pack_f16x8(xv.b[0], xv.b[1]);
+          *reinterpret_cast<u32x4*>(vd + 8 * e) = pack_f16x8(cur.v.a[0], cur.v.a[1]);
+          *reinterpret_cast<u32x4*>(vd + D / 2 + 8 * e) = pack_f16x8(cur.v.b[0], cur.v.b[1]);
         }
+        cur = nxt;
       }
     }
     // (2) The workgroup's queries, normalised and rotated into the LDS staging (chunk c of row rho
     // at c ^ (rho % 8)); wave grp prepares rows kQRowsPerWave grp .. (a row past the chunk as zeros).
     const Pairs8 wq = load_pairs8<D>(pp.q_norm_w, e);
 #pragma unroll
-    for (int op = 0; op < (C::kQRowsPerWave + PR::kRows - 1) / PR::kRows; ++op) {
+    for (int op = 0; op < kQOps; ++op) {
       const int rw = op * PR::kRows + sub;
       const int rho = C::kQRowsPerWave * grp + min(rw, C::kQRowsPerWave - 1);
       const int qi = q0 + rho % kQw;
-      const int qc = min(qi, T - 1);
-      const Pairs8 xq = load_pairs8<D>(pp.q + (int64_t(qc) * hq + kvh * G + rho / kQw) * D, e);
-      const Pairs8 cs = load_pairs8<D>(pp.rope + int64_t(query_start + qc) * D, e);
       u32x4 lo, hi;
-      norm_rope_row<D>(xq, wq, cs, pp.eps, lo, hi);
+      norm_rope_row<D>(xq[op], wq, csq[op], pp.eps, lo, hi);
       if (qi >= T) lo = hi = u32x4{0u, 0u, 0u, 0u};
       if (rw < C::kQRowsPerWave) {
         *reinterpret_cast<__attribute__((address_space(3))) u32x4*>(qlds + rho * 2 * D + ((e ^ (rho % 8)) * 16)) = lo;

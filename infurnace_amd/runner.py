@@ -50,8 +50,8 @@ import numpy as np
 import torch
 
 from .cache import BlockPool, KVCacheError, KVManager, PagedKVCache, PoolExhausted, PrefixCache
-from .kernels import (decode_plan, paged_attention, qk_norm_rope_append, qk_norm_rope_append_and_prefill,
-                      qk_norm_rope_store_and_decode, store_kv, store_kv_and_decode, store_kv_and_prefill)
+from .kernels import (decode_plan, paged_attention, qk_norm_rope_append, qk_norm_rope_store_and_decode, store_kv,
+                      store_kv_and_decode, store_kv_and_prefill)
 
 __all__ = ["PagedKVRunner", "RunnerError"]
 
@@ -118,9 +118,10 @@ class _Step:
                           eps: float = 1e-6, out: torch.Tensor | None = None) -> torch.Tensor:
         """The same from fp32 projections: q/k RMSNorm + rotary, fp16 cast and append.
 
-        A decode step without a shared prefix, and a prefill chunk starting at a multiple of 32
-        tokens, do all of it and the attention in one launch (``qk_norm_rope_store_and_decode`` /
-        ``qk_norm_rope_append_and_prefill``); otherwise the pre-append is its own launch.
+        A decode step without a shared prefix does all of it and the attention in one launch
+        (``qk_norm_rope_store_and_decode``); otherwise the pre-append is its own launch.  (A prefill
+        chunk keeps two launches: ``qk_norm_rope_append_and_prefill`` does it in one, but every
+        workgroup then prepares the chunk rows it reads itself, which measures slower.)
         """
         if self.closed:
             raise RunnerError("this step is closed: a later step has begun")
@@ -132,12 +133,12 @@ class _Step:
                                               plan=self._decode_plan(q))
             self._launched()
             return o
-        if self.query_start is not None:  # a prefill chunk (positions query_start + t, the table's slots)
-            o = qk_norm_rope_append_and_prefill(q, k, v, q_norm_weight, k_norm_weight, rope, kv, self.block_tables,
-                                                query_start=self.query_start, layer=layer, eps=eps, out=out)
+        q16 = qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope, self.positions, self.slot_mapping,
+                                  self.active, kv, layer=layer, eps=eps)
+        if self.query_start is not None:  # a prefill chunk
+            o = paged_attention(q16, kv, self.block_tables, None, None, layer=layer, query_start=self.query_start,
+                                out=out)
         else:  # a decode step over a shared prefix
-            q16 = qk_norm_rope_append(q, k, v, q_norm_weight, k_norm_weight, rope, self.positions,
-                                      self.slot_mapping, self.active, kv, layer=layer, eps=eps)
             o = paged_attention(q16, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
                                 max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
         self._launched()

@@ -6,8 +6,8 @@ leave the same bytes in the pool as ``qk_norm_rope_append`` (positions query_sta
 slots) and produce the same output as that followed by ``paged_attention(..., query_start=...)`` --
 bit for bit.  The two-launch path is pinned against the oracle elsewhere
 (tests/test_kv_prep_gpu.py, tests/test_paged_prefill_gpu.py); one case here also checks the fused
-result against the oracle pipeline directly (attention atol 2e-3 / rtol 1e-2, K within one fp16 ulp,
-V bit-exact).
+result against the oracle pipeline directly (attention atol 2e-3 / rtol 1e-2, K at most one fp16
+value apart or within 1e-6, V bit-exact).
 """
 import numpy as np
 import pytest
@@ -72,6 +72,14 @@ def _both(dev, c, rope):
     return p1, out1, p2, out2
 
 
+def _steps(a16, b16):
+    """Distance in representable fp16 values (0: equal, 1: neighbours, also across a power of two)."""
+    def ordinal(x):
+        i = x.view(np.int16).astype(np.int64)
+        return np.where(i < 0, -(i & 0x7FFF), i)
+    return np.abs(ordinal(a16) - ordinal(b16))
+
+
 def _assert_same(p1, out1, p2, out2, what):
     assert torch.equal(p1.view(torch.int16), p2.view(torch.int16)), f"{what}: pools differ"
     assert torch.equal(out1.view(torch.int16), out2.view(torch.int16)), f"{what}: outputs differ"
@@ -127,8 +135,9 @@ def test_fused_prefill_prep_config3_prompt(dev):
 
 def test_fused_prefill_prep_matches_oracle_pipeline(dev):
     """The fused chunk against the oracle's pre-append then the oracle's causal attention over the
-    oracle's pool (host copies): K within one fp16 ulp (the two sum the squares in different
-    orders), V bit-exact, the attention within atol 2e-3 / rtol 1e-2."""
+    oracle's pool (host copies): K at most one fp16 value apart (the two sum the squares in
+    different orders, so the fp32 results can round to neighbouring fp16 values) or within 1e-6
+    where the rotation cancels, V bit-exact, the attention within atol 2e-3 / rtol 1e-2."""
     say("fused prep+prefill vs oracle pipeline")
     hq, hkv, d, start, T = 16, 8, 128, 320, 200
     rng = np.random.default_rng(17)
@@ -146,10 +155,10 @@ def test_fused_prefill_prep_matches_oracle_pipeline(dev):
     ref = oracle.paged_attention(ref_q[None], ref_pool, c["table"][None], np.asarray([start + T], np.int32))[0]
     assert_attn_close(out, ref, "fused prep+prefill vs oracle")
     got = pool.cpu().numpy()
-    kk = got[0].astype(np.float64)
-    kr = ref_pool[0].astype(np.float64)
-    ulp = np.maximum(np.spacing(np.abs(ref_pool[0])).astype(np.float64), 2.0 ** -24)
-    assert (np.abs(kk - kr) / ulp).max() <= 1.0
+    # adjacent fp16 values at most -- or within 1e-6 where the rotation's two products nearly cancel
+    # (their fp32 roundings, ~6e-8 of O(1) terms, then decide the last bits of a small result)
+    near = np.abs(got[0].astype(np.float64) - ref_pool[0].astype(np.float64)) <= 1e-6
+    assert ((_steps(got[0], ref_pool[0]) <= 1) | near).all()
     assert np.array_equal(got[1].view(np.uint16), ref_pool[1].view(np.uint16))
 
 

@@ -3,8 +3,7 @@
 The step runs q/k RMSNorm + rotary, the fp16 cast and the append from fp32 projections, then the
 attention (model.py:183-200 for decode, :109-138 for a prefill chunk).  It has three branches:
 
-* a prefill chunk: one fused launch (``qk_norm_rope_append_and_prefill``) when it starts at a multiple
-  of 32 tokens, else ``qk_norm_rope_append`` then causal ``paged_attention(query_start=...)``;
+* a prefill chunk: ``qk_norm_rope_append`` then causal ``paged_attention(query_start=...)``;
 * a decode step without a shared prefix: one fused launch (``qk_norm_rope_store_and_decode``);
 * a decode step over a shared prefix: ``qk_norm_rope_append`` then the shared-prefix decode.
 
