@@ -7,10 +7,11 @@
 //         [position][cos | sin] table (:19-27, applied at :186-187);
 //   k, v: cast to fp16 and stored at slot_mapping[t] (:190-196 decode, :134-137 prefill);
 //   q:    written as fp16 for paged attention.
-// One workgroup per token; a wavefront handles a (token, head) row at a time, lane l owning
-// the rotary pairs (i, i + D/2) for i = l, l + 64, ..., so the RMS reduction is one wave sum
-// and the rotation never leaves the lane.  Every load and store is a contiguous 256-byte
-// (fp32) or 128-byte (fp16) run.
+// Head dims 64 and 128 (16-byte aligned arrays) take qk_norm_rope_rows_kernel: 8 rotary pairs per
+// lane, rows spread over whole wavefronts.  Other shapes take qk_norm_rope_append_kernel: one
+// workgroup per token; a wavefront handles a (token, head) row at a time, lane l owning the
+// rotary pairs (i, i + D/2) for i = l, l + 64, ..., so the RMS reduction is one wave sum and the
+// rotation never leaves the lane.  The two give the same bits.
 //
 // ifn_zero_pages / ifn_copy_pages are the paged forms of clear_slot
 // (src/infurnace/executor/tinygrad/buffers.py:67-81): zero, or copy, whole pages in every layer.
@@ -108,6 +109,79 @@ __global__ __launch_bounds__(kPrepThreads) void qk_norm_rope_append_kernel(
   }
 }
 
+// The same step with rows spread over whole wavefronts, for head_dim 64 or 128 and 16-byte aligned
+// arrays: D / 16 lanes per row, each holding 8 rotary pairs (PrepRows), so a wave pass covers
+// 64 / (D / 16) rows.  Rows are numbered token-major (token t, then its Hq q heads, Hkv k heads,
+// Hkv v heads); wave w takes kPrepPasses consecutive passes and requests all their rows and
+// positions, then their rotary rows, before it computes.  q and k equal the
+// one-token-per-workgroup kernel's bit for bit (the same sum of squares, see PrepRows; the same
+// per-pair arithmetic), v is the same cast.
+constexpr int kPrepRowsThreads = 256;
+constexpr int kPrepPasses = 2;
+
+template <int D>
+__global__ __launch_bounds__(kPrepRowsThreads) void qk_norm_rope_rows_kernel(
+    f16* __restrict__ q_out, const float* __restrict__ q, const float* __restrict__ k,
+    const float* __restrict__ v, const float* __restrict__ q_norm_w, const float* __restrict__ k_norm_w,
+    const float* __restrict__ rope, int32_t max_pos, const int32_t* __restrict__ positions,
+    const int32_t* __restrict__ slot_mapping, const uint8_t* __restrict__ active, f16* __restrict__ pool,
+    int64_t num_slots, int32_t T, int32_t hq, int32_t hkv, float eps) {
+  using PR = PrepRows<D>;
+  const int lane = threadIdx.x % kWave;
+  const int e = lane % PR::kLanes, sub = lane / PR::kLanes;
+  const int64_t wave = int64_t(blockIdx.x) * (kPrepRowsThreads / kWave) + threadIdx.x / kWave;
+  const int rows_per_token = hq + 2 * hkv;
+  const int64_t nrows = int64_t(T) * rows_per_token;
+  int64_t row[kPrepPasses];
+  int tok[kPrepPasses], head[kPrepPasses], pos[kPrepPasses];
+  Pairs8 x[kPrepPasses], cs[kPrepPasses];
+#pragma unroll
+  for (int p = 0; p < kPrepPasses; ++p) {
+    row[p] = (wave * kPrepPasses + p) * PR::kRows + sub;
+    const int64_t rc = min(row[p], nrows - 1);  // (past the end: a valid row again, not stored)
+    tok[p] = int(rc / rows_per_token);
+    head[p] = int(rc - int64_t(tok[p]) * rows_per_token);
+    const float* src = head[p] < hq ? q + (int64_t(tok[p]) * hq + head[p]) * D
+                       : head[p] < hq + hkv ? k + (int64_t(tok[p]) * hkv + (head[p] - hq)) * D
+                                            : v + (int64_t(tok[p]) * hkv + (head[p] - hq - hkv)) * D;
+    x[p] = load_pairs8<D>(src, e);
+    pos[p] = positions[tok[p]];
+  }
+  const Pairs8 wq = load_pairs8<D>(q_norm_w, e);
+  const Pairs8 wk = load_pairs8<D>(k_norm_w, e);
+#pragma unroll
+  for (int p = 0; p < kPrepPasses; ++p) {
+    const bool pos_ok = pos[p] >= 0 && pos[p] < max_pos;
+    cs[p] = load_pairs8<D>(rope + int64_t(pos_ok ? pos[p] : 0) * D, e);
+  }
+#pragma unroll
+  for (int p = 0; p < kPrepPasses; ++p) {
+    const int t = tok[p], h = head[p];
+    const bool pos_ok = pos[p] >= 0 && pos[p] < max_pos;
+    const int kind = h < hq ? 0 : (h < hq + hkv ? 1 : 2);  // 0 = q, 1 = k, 2 = v (uniform per row)
+    u32x4 lo, hi;
+    // every lane of the wave takes part in the butterfly (rows of any kind), v rows are only cast
+    norm_rope_row<D>(x[p], kind == 0 ? wq : wk, cs[p], eps, lo, hi);
+    if (kind == 2) {
+      lo = pack_f16x8(x[p].a[0], x[p].a[1]);
+      hi = pack_f16x8(x[p].b[0], x[p].b[1]);
+    }
+    if (row[p] >= nrows) continue;
+    f16* dst;
+    if (kind == 0) {
+      dst = q_out + (int64_t(t) * hq + h) * D;
+      if (!pos_ok) lo = hi = u32x4{0u, 0u, 0u, 0u};
+    } else {
+      const int64_t slot = slot_mapping[t];
+      if (!(pos_ok && (active == nullptr || active[t] != 0) && slot >= 0 && slot < num_slots)) continue;
+      // pool layer: [2][slot][hkv][D]; V is num_slots rows after K
+      dst = pool + (int64_t(kind - 1) * num_slots + slot) * hkv * D + int64_t(kind == 1 ? h - hq : h - hq - hkv) * D;
+    }
+    *reinterpret_cast<u32x4*>(dst + 8 * e) = lo;
+    *reinterpret_cast<u32x4*>(dst + D / 2 + 8 * e) = hi;
+  }
+}
+
 // One thread block per (layer, K|V, listed page): 16-byte stores (and loads) over the page.
 template <bool kCopy>
 __global__ __launch_bounds__(256) void page_op_kernel(uint8_t* __restrict__ pool, int64_t num_pages,
@@ -171,8 +245,25 @@ extern "C" int ifn_qk_norm_rope_append(void* q_out, const float* q, const float*
     return IFN_ERR_INVALID_ARGUMENT;
   if (head_dim > 256) return IFN_ERR_UNSUPPORTED;
   if (num_tokens == 0) return IFN_OK;
+  const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  auto aligned = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; };
+  if ((head_dim == 64 || head_dim == 128) && aligned(q_out) && aligned(q) && aligned(k) && aligned(v) &&
+      aligned(q_norm_weight) && aligned(k_norm_weight) && aligned(rope_table) && aligned(kv_pool_layer)) {
+    const int64_t rows = int64_t(num_tokens) * (num_q_heads + 2 * num_kv_heads);
+    const int per_pass = kWave / (head_dim / 16);
+    const int64_t waves = ceil_div(rows, int64_t(per_pass) * kPrepPasses);
+    const int64_t blocks = ceil_div(waves, kPrepRowsThreads / kWave);
+    if (blocks < (int64_t(1) << 31)) {
+      auto rk = head_dim == 128 ? qk_norm_rope_rows_kernel<128> : qk_norm_rope_rows_kernel<64>;
+      rk<<<dim3(unsigned(blocks)), dim3(kPrepRowsThreads), 0, s>>>(
+          static_cast<f16*>(q_out), q, k, v, q_norm_weight, k_norm_weight, rope_table, max_positions, positions,
+          slot_mapping, active_mask, static_cast<f16*>(kv_pool_layer), num_pages * block_size, num_tokens,
+          num_q_heads, num_kv_heads, eps);
+      return ifn_launch_status();
+    }
+  }
   auto kernel = head_dim <= 128 ? qk_norm_rope_append_kernel<1> : qk_norm_rope_append_kernel<2>;
-  kernel<<<dim3(unsigned(num_tokens)), dim3(kPrepThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
+  kernel<<<dim3(unsigned(num_tokens)), dim3(kPrepThreads), 0, s>>>(
       static_cast<f16*>(q_out), q, k, v, q_norm_weight, k_norm_weight, rope_table, max_positions, positions,
       slot_mapping, active_mask, static_cast<f16*>(kv_pool_layer), num_pages * block_size, num_q_heads,
       num_kv_heads, head_dim, eps);

@@ -192,58 +192,6 @@ __device__ __forceinline__ void pin_probs(f16x8 (&p)[RT][2]) {
 #endif
 }
 
-// ---- fused pre-append of a prefill chunk --------------------------------------------------
-// A row of D fp32 dims is normalised and rotated by D / 16 lanes, lane e of the row's group holding
-// the rotary pairs 8 e .. 8 e + 7: dims 8 e .. 8 e + 7 (x1) and D / 2 + 8 e .. (x2).
-// ifn_qk_norm_rope_append holds pair p in lane p of a wave and adds the pairs' squares with a
-// butterfly over lane offsets 1, 2, 4, ..; here the butterfly's first three levels are this lane's
-// own eight pairs, paired the same way, and the remaining levels lane offsets 1, 2, 4 within the
-// row's group.  The same additions of the same operands give the same sum, bit for bit (for D = 64
-// that kernel's last level adds its idle lanes' zeros to a non-negative sum, which changes
-// nothing); the per-pair arithmetic is the shared norm_rope_pair, so q and k are identical to its.
-template <int D>
-struct PrepRows {
-  static constexpr int kLanes = D / 16;         // lanes per row
-  static constexpr int kRows = kWave / kLanes;  // rows per wave pass
-};
-struct Pairs8 {
-  f32x4 a[2];  // element 8 e .. 8 e + 7 of the row's first half
-  f32x4 b[2];  // element D / 2 + 8 e .. of its second half
-};
-template <int D>
-__device__ __forceinline__ Pairs8 load_pairs8(const float* row, int e) {
-  const f32x4* p = reinterpret_cast<const f32x4*>(row + 8 * e);
-  const f32x4* s = reinterpret_cast<const f32x4*>(row + D / 2 + 8 * e);
-  return Pairs8{{p[0], p[1]}, {s[0], s[1]}};
-}
-__device__ __forceinline__ u32x4 pack_f16x8(const f32x4& lo, const f32x4& hi) {
-  return __builtin_bit_cast(u32x4, f16x8{f16(lo[0]), f16(lo[1]), f16(lo[2]), f16(lo[3]), f16(hi[0]), f16(hi[1]),
-                                          f16(hi[2]), f16(hi[3])});
-}
-// x normalised with the weights w and rotated by the table row cs ([cos | sin]); fp16 results as
-// two 16-byte chunks: dims 8 e .. (lo) and D / 2 + 8 e .. (hi).  Every lane of a row's group calls it.
-template <int D>
-__device__ __forceinline__ void norm_rope_row(const Pairs8& x, const Pairs8& w, const Pairs8& cs, float eps,
-                                              u32x4& lo, u32x4& hi) {
-  float s[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) s[j] = pair_sq(x.a[j / 4][j % 4], x.b[j / 4][j % 4]);
-  float ss = ((s[0] + s[1]) + (s[2] + s[3])) + ((s[4] + s[5]) + (s[6] + s[7]));
-#pragma unroll
-  for (int o = 1; o < PrepRows<D>::kLanes; o <<= 1) ss += __shfl_xor(ss, o);
-  const float rs = rms_inv(ss, D, eps);
-  f32x4 y1[2], y2[2];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    float a = x.a[j / 4][j % 4], b = x.b[j / 4][j % 4];
-    norm_rope_pair(a, b, rs, w.a[j / 4][j % 4], w.b[j / 4][j % 4], cs.a[j / 4][j % 4], cs.b[j / 4][j % 4]);
-    y1[j / 4][j % 4] = a;
-    y2[j / 4][j % 4] = b;
-  }
-  lo = pack_f16x8(y1[0], y1[1]);
-  hi = pack_f16x8(y2[0], y2[1]);
-}
-
 template <int D, int G, int RT, int W, bool kAppend, bool kPrep>
 __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
