@@ -194,11 +194,14 @@ struct DecodeWorkspace {
 // leaves the segment's unnormalised state (m, l, O) in state nstates - 1 for
 // cascade_combine_kernel; the whole-row kernel merges the prefix states itself and writes fp16.
 // Shorter rows are attended in full and written directly.  pages == 0: ordinary decode.
+// The whole-row kernel reads the prefix states' outputs from oh instead: O / l in fp16 (a convex
+// combination of value rows, so fp16 keeps it to a relative 2^-11), at the same indices.
 struct DecodePrefix {
   float* ml;
   float* o;
   int32_t pages;
   int32_t nstates;
+  const f16* oh;
 };
 
 // Fused append: store new_k / new_v of every active row at slot_mapping[row] (the store_kv
@@ -342,12 +345,14 @@ struct PrefillPrep {
 // mask) and each key split writes its result unnormalised, as the state (m, l, O), for a later
 // merge: ml[((seg * stride + split) * G + g) * 2 + {0,1}], o[((seg * stride + split) * G + g) * D + dim]
 // with seg = row * Hkv + kv head (stride >= nsplit).  No cross-workgroup merge happens here.
+// With oh set, the output goes there instead, normalised (O / l) in fp16, at the same indices.
 // key_len == 0 is ordinary causal prefill.
 struct PrefixOut {
   float* ml;
   float* o;
   int32_t key_len;
   int32_t stride;
+  f16* oh;
 };
 
 static inline size_t align256(size_t x) { return (x + 255) & ~size_t(255); }
@@ -373,9 +378,10 @@ inline int device_cu_count() {
 // px_ml[((seg * stride + split) * G + g) * 2 + {0,1}] / px_o[((seg * stride + split) * G + g) * D + dim],
 // seg = row * Hkv + kv head, stride >= the split count.
 int prefix_pass_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus);
+// With px_oh set the outputs go there as O / l in fp16 (PrefixOut::oh) and px_o is not written.
 int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
                 int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
-                int32_t stride, int cus, hipStream_t stream);
+                f16* px_oh, int32_t stride, int cus, hipStream_t stream);
 
 // Chunked prefill with 64 query rows per wavefront (paged_prefill_wide.hip): the entry points'
 // kernel for the (head_dim, group) it compiles; the key-split workspace it needs.
@@ -389,7 +395,7 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
 int wide_prefix_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_t key_len, int cus);
 int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
                      int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
-                     int32_t stride, int cus, hipStream_t stream);
+                     f16* px_oh, int32_t stride, int cus, hipStream_t stream);
 
 // Whole-row decode (paged_decode_rows.hip), used by the decode entry points when the token row
 // (num_kv_heads x head_dim fp16) is 2 KiB and its (head_dim, group) is compiled; and its step plan.

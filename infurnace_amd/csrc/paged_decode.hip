@@ -814,7 +814,7 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
   k<<<dim3(unsigned(blocks)), dim3(kDecodeThreads), 0, reinterpret_cast<hipStream_t>(stream)>>>(
       static_cast<f16*>(out), static_cast<const f16*>(query),
       static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
-      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws, DecodePrefix{nullptr, nullptr, 0, 0},
+      seq_lens, active_mask, batch, num_kv_heads, max_seq_len, scale * kLog2e, ws, DecodePrefix{nullptr, nullptr, 0, 0, nullptr},
       ap);
   return ifn_launch_status();
 }
@@ -1033,13 +1033,14 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   IFN_CHECK_ALIGN16(workspace);
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
   uint8_t* wsb = static_cast<uint8_t*>(workspace);
+  // (the whole-row kernel takes the prefix outputs as O / l in fp16, in the same region)
   const DecodePrefix px{reinterpret_cast<float*>(wsb + L.st_ml), reinterpret_cast<float*>(wsb + L.st_o),
-                        shared_pages, L.nstates};
+                        shared_pages, L.nstates, rows ? reinterpret_cast<const f16*>(wsb + L.st_o) : nullptr};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
   // 1. every row's queries against the shared pages, once (states 0 .. nstates - 2)
   int rc = prefix_pass(static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
                        prefix_pages, key_len, batch, num_q_heads, num_kv_heads, head_dim, scale * kLog2e, px.ml,
-                       px.o, L.nstates, cus, s);
+                       px.o, const_cast<f16*>(px.oh), L.nstates, cus, s);
   if (rc != IFN_OK) return rc;
   // 2. the private pages.  Whole-row kernel: each cascade row's own keys merged with its prefix
   // states, to fp16.  Per-segment kernel: its state goes to state nstates - 1 (other rows are

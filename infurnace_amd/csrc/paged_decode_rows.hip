@@ -416,11 +416,12 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   const int bid = int(blockIdx.x), nbi = nb_arg;
   const int64_t blk = (nbi % kRowsXcds) == 0 ? (bid % kRowsXcds) * (nbi / kRowsXcds) + bid / kRowsXcds : bid;
   // kCascade: dims 4 d4 .. 4 d4 + 3 of query head qh of cascade row b, from the row's own state
-  // (M, L, unnormalised O) merged with the prefix states, 4 per round trip.  The caller loads the
-  // first 4 into pb with px_load before the row's own merge, so that their round trip overlaps it.
+  // (M, L, unnormalised O) merged with the prefix states (m, l and O / l in fp16), 4 per round
+  // trip.  The caller loads the first 4 into pb with px_load before the row's own merge, so that
+  // their round trip overlaps it.
   struct PxBatch {
     f32x2 ml[4];
-    f32x4 o[4];
+    f16x4 o[4];
   };
   auto px_load = [&](int64_t b, int qh, int d4, int s0, PxBatch& pb) __attribute__((always_inline)) {
     const int npx = px.nstates - 1;
@@ -429,7 +430,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     for (int u = 0; u < 4; ++u) {
       const int64_t st = st0 + int64_t(min(s0 + u, npx - 1)) * G;
       pb.ml[u] = *reinterpret_cast<const f32x2*>(px.ml + st * 2);
-      pb.o[u] = *reinterpret_cast<const f32x4*>(px.o + st * D + 4 * d4);
+      pb.o[u] = *reinterpret_cast<const f16x4*>(px.oh + st * D + 4 * d4);
     }
   };
   auto cascade_out = [&](int64_t b, int qh, int d4, float M, float L, f32x4 O, PxBatch& pb)
@@ -438,15 +439,15 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     for (int s0 = 0; s0 < npx; s0 += 4) {
       if (s0 > 0) px_load(b, qh, d4, s0, pb);
       const f32x2* mlv = pb.ml;
-      const f32x4* ov = pb.o;
+      const f16x4* ov = pb.o;
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         if (s0 + u < npx) {
           const float nm = fmaxf(M, mlv[u][0]);
-          const float a = exp2_fast(M - nm), c = exp2_fast(mlv[u][0] - nm);
-          L = fmaf(L, a, c * mlv[u][1]);
-          O = f32x4{fmaf(O[0], a, c * ov[u][0]), fmaf(O[1], a, c * ov[u][1]), fmaf(O[2], a, c * ov[u][2]),
-                    fmaf(O[3], a, c * ov[u][3])};
+          const float a = exp2_fast(M - nm), cl = exp2_fast(mlv[u][0] - nm) * mlv[u][1];
+          L = fmaf(L, a, cl);
+          O = f32x4{fmaf(O[0], a, cl * float(ov[u][0])), fmaf(O[1], a, cl * float(ov[u][1])),
+                    fmaf(O[2], a, cl * float(ov[u][2])), fmaf(O[3], a, cl * float(ov[u][3]))};
           M = nm;
         }
       }
@@ -1189,7 +1190,7 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
   ws.ml = reinterpret_cast<float*>(wsb + off_ml);
   ws.o = reinterpret_cast<float*>(wsb + off_o);
   const DecodePrep pp = prep != nullptr ? *prep : DecodePrep{};
-  const DecodePrefix pf = px != nullptr ? *px : DecodePrefix{nullptr, nullptr, 0, 0};
+  const DecodePrefix pf = px != nullptr ? *px : DecodePrefix{nullptr, nullptr, 0, 0, nullptr};
   k<<<dim3(unsigned(blocks)), dim3(kRowsThreads), 0, stream>>>(px != nullptr ? nullptr : plan, pool, block_tables, q,
                                                                 batch, max_pages, max_len, blocks, num_pages, out,
                                                                 seq_lens, active, scale_log2, ws, ap, pp, pf);

@@ -60,10 +60,10 @@ int prefix_pass_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_
 
 int prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
                 int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
-                int32_t stride, int cus, hipStream_t stream) {
+                f16* px_oh, int32_t stride, int cus, hipStream_t stream) {
   if (!wide_prefill_supported(hq, hkv, d)) return IFN_ERR_UNSUPPORTED;
   return wide_prefix_pass(q, pool, num_pages, prefix_pages, key_len, batch, hq, hkv, d, scale_log2, px_ml, px_o,
-                          stride, cus, stream);
+                          px_oh, stride, cus, stream);
 }
 
 }  // namespace ifn

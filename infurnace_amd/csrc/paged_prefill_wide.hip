@@ -868,16 +868,22 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     o[u] = y;
   }
 
-  if (prefix_mode) {  // this split's unnormalised state of (row my_q, kv head kvh, head g)
+  if (prefix_mode) {  // this split's state of (row my_q, kv head kvh, head g)
     if (!q_ok[rt_own]) return;
     const int g = my_head[rt_own] - kvh * G;
     const int64_t pslot = ((int64_t(my_q[rt_own]) * num_kv_heads + kvh) * px.stride + split) * G + g;
     if (grp < RT && half == 0) *reinterpret_cast<f32x2*>(px.ml + pslot * 2) = f32x2{mfin, lfin};
+    const float inv = lfin > 0.f ? 1.f / lfin : 0.f;
 #pragma unroll
     for (int u = 0; u < C::kOwnU; ++u) {  // dims 32 dt + 8 r4 + 4 half + 0..3 of block p
       int p, r4;
       own(u, p, r4);
-      *reinterpret_cast<f32x4*>(px.o + pslot * D + 32 * (p / RT) + 8 * r4 + 4 * half) = o[u];
+      const int64_t at = pslot * D + 32 * (p / RT) + 8 * r4 + 4 * half;
+      if (px.oh != nullptr)  // (uniform) normalised, fp16
+        *reinterpret_cast<f16x4*>(px.oh + at) =
+            f16x4{f16(o[u][0] * inv), f16(o[u][1] * inv), f16(o[u][2] * inv), f16(o[u][3] * inv)};
+      else
+        *reinterpret_cast<f32x4*>(px.o + at) = o[u];
     }
     return;
   }
@@ -1022,7 +1028,7 @@ int wide_prefill_launch(f16* out, const f16* q, const f16* pool, int64_t num_pag
   }
   k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(unsigned(p.w * kWave)), 0, stream>>>(
       out, q, pool, num_pages, table, query_start, T, hkv, int(p.n_qb), p.nsplit, scale_log2, ws, ap,
-      PrefixOut{nullptr, nullptr, 0, 0}, prep != nullptr ? *prep : PrefillPrep{});
+      PrefixOut{nullptr, nullptr, 0, 0, nullptr}, prep != nullptr ? *prep : PrefillPrep{});
   return ifn_launch_status();
 }
 
@@ -1032,7 +1038,7 @@ int wide_prefix_splits(int32_t batch, int32_t hq, int32_t hkv, int32_t d, int32_
 
 int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages, int32_t key_len,
                      int32_t batch, int32_t hq, int32_t hkv, int32_t d, float scale_log2, float* px_ml, float* px_o,
-                     int32_t stride, int cus, hipStream_t stream) {
+                     f16* px_oh, int32_t stride, int cus, hipStream_t stream) {
   if (key_len < 1) return IFN_ERR_INVALID_ARGUMENT;
   const WidePlan p = plan_wide(batch, 0, hq, hkv, d, cus, key_len);
   WideKernel k = pick_wide(d, hq / hkv, p.rt, p.w, WideMode::kPlain);
@@ -1041,7 +1047,7 @@ int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int
   k<<<dim3(unsigned(p.n_qb * hkv * p.nsplit)), dim3(unsigned(p.w * kWave)), 0, stream>>>(
       nullptr, q, pool, num_pages, prefix_pages, 0, batch, hkv, int(p.n_qb), p.nsplit, scale_log2,
       PrefillWorkspace{nullptr, nullptr, nullptr}, PrefillAppend{nullptr, nullptr, nullptr},
-      PrefixOut{px_ml, px_o, key_len, stride}, PrefillPrep{});
+      PrefixOut{px_ml, px_o, key_len, stride, px_oh}, PrefillPrep{});
   return ifn_launch_status();
 }
 
