@@ -265,6 +265,42 @@ int ifn_paged_decode_shared_prefix(void* out, const void* query, const void* kv_
                                    size_t workspace_bytes, void* stream);
 
 /*
+ * The step plan of a shared-prefix decode step (ifn_paged_decode_plan for
+ * the whole-row kernel's shared-prefix mode): the split of the rows' own keys
+ * after the first shared_pages pages, built once per step from the lengths,
+ * the active mask and the tables that every layer shares.  plan_bytes as
+ * ifn_paged_decode_plan_bytes; block_size 16.  Shapes decoded without a plan
+ * (token rows other than 2 KiB) return IFN_OK and write nothing.  With
+ * shared_pages == 0 it is ifn_paged_decode_plan without appended slots.
+ * Replaces: nothing in the reference (see ifn_paged_decode_plan); this is the
+ * per-step half of the shared-prefix decode below.
+ */
+int ifn_paged_decode_shared_prefix_plan(void* plan, size_t plan_bytes, const int32_t* block_tables,
+                                        int32_t max_pages_per_seq, const int32_t* seq_lens,
+                                        const uint8_t* active_mask, int32_t shared_pages, int64_t num_pages,
+                                        int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                        int32_t head_dim, int32_t block_size, int32_t max_seq_len,
+                                        void* stream);
+
+/*
+ * ifn_paged_decode_shared_prefix with a step plan from
+ * ifn_paged_decode_shared_prefix_plan (NULL: none).  Same arguments,
+ * workspace and output otherwise (bit-identical to the unplanned call); a
+ * plan for other shapes, batch size or shared_pages is detected and ignored,
+ * one built from other lengths or tables of the same shapes gives wrong
+ * results.
+ * Replaces: as ifn_paged_decode_shared_prefix.
+ */
+int ifn_paged_decode_shared_prefix_planned(void* out, const void* query, const void* kv_pool_layer,
+                                           int64_t num_pages, const int32_t* prefix_pages, int32_t shared_pages,
+                                           const int32_t* block_tables, int32_t max_pages_per_seq,
+                                           const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                                           int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                           int32_t block_size, int32_t max_seq_len, float scale,
+                                           const void* plan, size_t plan_bytes, void* workspace,
+                                           size_t workspace_bytes, void* stream);
+
+/*
  * One prefill chunk's append and causal attention: the result (output and
  * pool) equals storing new_k / new_v ([num_q_tokens][num_kv_heads][head_dim]
  * fp16) at slot block_table[p / 16] * 16 + p % 16 for p = query_start + t

@@ -52,6 +52,13 @@ SIGNATURES: dict[str, tuple] = {
     "ifn_paged_decode_shared_prefix_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "ifn_paged_decode_shared_prefix": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _i32, _p, _p, _i32, _i32,
                                                       _i32, _i32, _i32, _i32, _f32, _p, _sz, _p]),
+    "ifn_paged_decode_shared_prefix_planned": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _i32, _p, _p, _i32,
+                                                              _i32, _i32, _i32, _i32, _i32, _f32, _p, _sz, _p, _sz,
+                                                              _p]),
+    # plan, bytes, block_tables, max_pages, seq_lens, active, shared_pages, num_pages, batch, hq, hkv, d, bs, msl,
+    # stream
+    "ifn_paged_decode_shared_prefix_plan": (ctypes.c_int, [_p, _sz, _p, _i32, _p, _p, _i32, _i64, _i32, _i32, _i32,
+                                                           _i32, _i32, _i32, _p]),
     "ifn_paged_prefill_workspace_bytes": (_sz, [_i32, _i32, _i32, _i32, _i32, _i32]),
     "ifn_paged_prefill": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _i32, _i32, _i32, _i32, _i32,
                                          _i32, _f32, _p, _sz, _p]),

@@ -405,9 +405,11 @@ bool rows_decode_supported(int32_t batch, int32_t hq, int32_t hkv, int32_t d, in
                            int32_t block_size = 16, bool append = false);
 size_t rows_decode_ws_bytes(int32_t batch, int32_t hq, int32_t d, int blocks);
 size_t rows_plan_bytes(int32_t batch, int blocks);
+// prefix_keys > 0: a plan for the shared-prefix mode (rows of at least that many keys stream only
+// the keys after them; no appended slots).
 int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
                      const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
-                     int blocks, hipStream_t stream, int32_t block_size = 16);
+                     int blocks, hipStream_t stream, int32_t block_size = 16, int32_t prefix_keys = 0);
 // prep (non-null): the fused pre-append variant; ap then carries the slots and the pool, and q is unused.
 // px (non-null): shared-prefix mode (DecodePrefix), without append or plan.
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,

@@ -990,18 +990,19 @@ extern "C" size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, 
   return shared > rows ? shared : rows;
 }
 
-extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, const void* kv_pool_layer,
-                                              int64_t num_pages, const int32_t* prefix_pages, int32_t shared_pages,
-                                              const int32_t* block_tables, int32_t max_pages_per_seq,
-                                              const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
-                                              int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
-                                              int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
-                                              size_t workspace_bytes, void* stream) {
-  using namespace ifn;
+namespace ifn {
+
+static int shared_prefix_entry(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                               const int32_t* prefix_pages, int32_t shared_pages, const int32_t* block_tables,
+                               int32_t max_pages_per_seq, const int32_t* seq_lens, const uint8_t* active_mask,
+                               int32_t batch, int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                               int32_t block_size, int32_t max_seq_len, float scale, const void* plan,
+                               size_t plan_bytes, void* workspace, size_t workspace_bytes, void* stream) {
   if (shared_pages == 0)  // no common leading run: plain decode with cached page loads
     return decode_entry(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
                         active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
-                        workspace, workspace_bytes, stream, DecodeAppend{nullptr, nullptr, nullptr, nullptr}, true);
+                        workspace, workspace_bytes, stream, DecodeAppend{nullptr, nullptr, nullptr, nullptr}, true,
+                        plan, plan_bytes);
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_tables == nullptr ||
       seq_lens == nullptr || prefix_pages == nullptr)
     return IFN_ERR_INVALID_ARGUMENT;
@@ -1046,11 +1047,15 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   // states, to fp16.  Per-segment kernel: its state goes to state nstates - 1 (other rows are
   // written directly), merged by the combine below.
   if (rows) {
+    if (plan != nullptr) {  // the kernel reads this workgroup's record before checking the header
+      if (plan_bytes < rows_plan_bytes(batch, blocks)) return IFN_ERR_WORKSPACE;
+      IFN_CHECK_ALIGN16(plan);
+    }
     rc = rows_decode_launch(static_cast<f16*>(out), static_cast<const f16*>(query),
                             static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
                             seq_lens, active_mask, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
                             scale * kLog2e, workspace, blocks, DecodeAppend{nullptr, nullptr, nullptr, nullptr}, false,
-                            nullptr, s, nullptr, &px);
+                            static_cast<const int32_t*>(plan), s, nullptr, &px);
   } else {
     DecodeWorkspace ws;
     ws.count = reinterpret_cast<uint32_t*>(wsb);
@@ -1070,4 +1075,59 @@ extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, cons
   kc<<<dim3(unsigned(segs * g)), dim3(kWave), 0, s>>>(
       static_cast<f16*>(out), seq_lens, active_mask, batch, num_kv_heads, g, cap, px);
   return ifn_launch_status();
+}
+
+}  // namespace ifn
+
+extern "C" int ifn_paged_decode_shared_prefix(void* out, const void* query, const void* kv_pool_layer,
+                                              int64_t num_pages, const int32_t* prefix_pages, int32_t shared_pages,
+                                              const int32_t* block_tables, int32_t max_pages_per_seq,
+                                              const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                                              int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                              int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
+                                              size_t workspace_bytes, void* stream) {
+  return ifn::shared_prefix_entry(out, query, kv_pool_layer, num_pages, prefix_pages, shared_pages, block_tables,
+                                  max_pages_per_seq, seq_lens, active_mask, batch, num_q_heads, num_kv_heads,
+                                  head_dim, block_size, max_seq_len, scale, nullptr, 0, workspace, workspace_bytes,
+                                  stream);
+}
+
+extern "C" int ifn_paged_decode_shared_prefix_planned(void* out, const void* query, const void* kv_pool_layer,
+                                                      int64_t num_pages, const int32_t* prefix_pages,
+                                                      int32_t shared_pages, const int32_t* block_tables,
+                                                      int32_t max_pages_per_seq, const int32_t* seq_lens,
+                                                      const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
+                                                      int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                                      int32_t max_seq_len, float scale, const void* plan,
+                                                      size_t plan_bytes, void* workspace, size_t workspace_bytes,
+                                                      void* stream) {
+  return ifn::shared_prefix_entry(out, query, kv_pool_layer, num_pages, prefix_pages, shared_pages, block_tables,
+                                  max_pages_per_seq, seq_lens, active_mask, batch, num_q_heads, num_kv_heads,
+                                  head_dim, block_size, max_seq_len, scale, plan, plan_bytes, workspace,
+                                  workspace_bytes, stream);
+}
+
+extern "C" int ifn_paged_decode_shared_prefix_plan(void* plan, size_t plan_bytes, const int32_t* block_tables,
+                                                   int32_t max_pages_per_seq, const int32_t* seq_lens,
+                                                   const uint8_t* active_mask, int32_t shared_pages,
+                                                   int64_t num_pages, int32_t batch, int32_t num_q_heads,
+                                                   int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                                   int32_t max_seq_len, void* stream) {
+  using namespace ifn;
+  if (block_tables == nullptr || seq_lens == nullptr) return IFN_ERR_INVALID_ARGUMENT;
+  if (batch < 0 || num_pages < 1 || max_pages_per_seq < 1 || num_q_heads < 1 || num_kv_heads < 1 || head_dim < 1 ||
+      max_seq_len < 0 || num_q_heads % num_kv_heads != 0 || shared_pages < 0 || shared_pages > max_pages_per_seq)
+    return IFN_ERR_INVALID_ARGUMENT;
+  if (block_size < 1) return IFN_ERR_INVALID_ARGUMENT;
+  if (batch == 0) return IFN_OK;
+  if (block_size != kBlock) return IFN_ERR_UNSUPPORTED;
+  if (!rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len, block_size))
+    return IFN_OK;  // these shapes decode without a plan
+  const int blocks = decode_blocks();
+  if (plan == nullptr || plan_bytes < rows_plan_bytes(batch, blocks)) return IFN_ERR_WORKSPACE;
+  IFN_CHECK_ALIGN16(plan);
+  if (device_cu_count() < 1) return IFN_ERR_HIP;
+  return rows_plan_launch(static_cast<int32_t*>(plan), block_tables, max_pages_per_seq, seq_lens, active_mask, nullptr,
+                          num_pages, batch, max_seq_len, blocks, reinterpret_cast<hipStream_t>(stream), block_size,
+                          shared_pages * block_size);
 }

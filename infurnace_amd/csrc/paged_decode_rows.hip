@@ -74,10 +74,12 @@ __device__ __forceinline__ int64_t range_count(int64_t nb, int64_t T) {
 }
 
 // Step plan (int32 words).  Header: magic, batch, ranges nr, virtual positions T, grid, whether
-// appended slots were given, the row-length cap, 0.  Then the rows' offsets cum[batch + 1], then one
-// record per workgroup range: [0] pieces of the range; [1 + 6 p ..] piece p < kPlanPieces: row,
-// first key a, end key e, first range of the row, ranges of the row, appended slot of the row;
-// [64 + i] page id i of the first piece's first window.
+// appended slots were given, the row-length cap, the shared-prefix keys pk (0: none).  Then the
+// rows' offsets cum[batch + 1], then one record per workgroup range: [0] pieces of the range;
+// [1 + 6 p ..] piece p < kPlanPieces: row, first key a, end key e, first range of the row, ranges of
+// the row, and the row's appended slot (or, in shared-prefix mode, which has no append, the key of
+// the row's first streamed key: pk for a cascade row, else 0); [64 + i] page id i of the first
+// piece's first window.
 constexpr int32_t kPlanMagic = 0x504c4e31;
 constexpr int kPlanHdr = 16;
 constexpr int kPlanRec = 128;
@@ -181,7 +183,7 @@ template <int PB>  // tokens per page
 __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
     int32_t* __restrict__ plan, const int32_t* __restrict__ block_tables, int32_t max_pages,
     const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, const int32_t* __restrict__ slots,
-    int64_t num_pages, int32_t batch, int32_t max_len, int32_t nb) {
+    int64_t num_pages, int32_t batch, int32_t max_len, int32_t nb, int32_t pk) {
   __shared__ int s_cum[kRowsMaxBatch + 1];
   __shared__ int s_wsum[kPlanThreads / kWave];
   __shared__ int s_p0[3][kPlanThreads];  // first piece of range r: row, a, e (rows < 0: none)
@@ -232,7 +234,8 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
     }
   }
   __syncthreads();
-  const int T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap, 0, nullptr, s_len);
+  // (pk > 0: a row of at least pk keys streams only its keys after the first pk)
+  const int T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap, pk, nullptr, s_len);
   const int nr = int(range_count(nb, T));
   if (tid == 0) {
     plan[0] = kPlanMagic;
@@ -242,7 +245,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
     plan[4] = nb;
     plan[5] = slots != nullptr ? 1 : 0;
     plan[6] = cap;
-    plan[7] = 0;
+    plan[7] = pk;
   }
   for (int i = tid; i <= batch; i += kPlanThreads) plan[kPlanHdr + i] = s_cum[i];
   int32_t* recs = plan + plan_rec0(batch);
@@ -270,12 +273,13 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
               pc[2] = e;
               pc[3] = first;
               pc[4] = range_of(int64_t(cb) + len - 1) - first + 1;
-              pc[5] = slots != nullptr ? s_slot[b] : -1;
+              pc[5] = slots != nullptr ? s_slot[b] : (pk > 0 && s_len[b] >= pk ? pk : 0);
             }
-            if (n == 0) {
+            if (n == 0) {  // (the first window's pages count from the row's first key)
+              const int off = pk > 0 && s_len[b] >= pk ? pk : 0;
               p0b = b;
-              p0a = a;
-              p0e = e;
+              p0a = a + off;
+              p0e = e + off;
             }
             ++n;
           }
@@ -468,7 +472,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
   int ids_pl = 0, cum_pf = 0;
   i32x4 rec_a = i32x4{0, 0, 0, 0}, rec_b = i32x4{0, 0, 0, 0};  // rec[0 .. 7]: pieces, piece 0 (6 words), -
   const int32_t* rec = nullptr;
-  if (!kCascade && plan != nullptr) {
+  if (plan != nullptr) {
     rec = plan + plan_rec0(batch) + blk * kPlanRec;
     const i32x4 h0 = *reinterpret_cast<const i32x4*>(plan);      // magic, batch, ranges, T
     const i32x4 h1 = *reinterpret_cast<const i32x4*>(plan + 4);  // grid, slots given, cap, 0
@@ -477,7 +481,7 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     ids_pl = rec[64 + lane];
     cum_pf = plan[kPlanHdr + min(tid, batch)];
     planned = (h0[0] == kPlanMagic) & (h0[1] == batch) & (h1[0] == int(nb)) & (h1[2] == cap) &
-              (!kApp | (h1[1] != 0));
+              (!kApp | (h1[1] != 0)) & (h1[3] == pk);
     T = h0[3];
     rec_n = rec_a[0];
   }
@@ -638,7 +642,8 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
       P.first = int(range_of(cb));
       P.nranges = int(range_of(int64_t(cb) + len - 1)) - P.first + 1;
       P.slot = kApp ? row_slot(ap.slots, active, b, num_slots) : -1;
-      if (kCascade && s_casc[b] != 0) {
+      // (planned: s_casc is not built; a piece the record does not hold is rare)
+      if (kCascade && (planned ? row_keys(seq_lens, active, b, cap) >= pk : s_casc[b] != 0)) {
         P.off = pk;
         P.a += pk;
         P.e += pk;
@@ -659,12 +664,13 @@ __global__ __launch_bounds__(kRowsThreads) void decode_rows_kernel(
     }
     RowPiece P;
     P.b = min(max(pc[0], 0), batch - 1);
-    P.a = min(max(pc[1], 0), cap - 1);
-    P.e = min(max(pc[2], P.a + 1), cap);
+    // (kCascade: word 5 is the row's first streamed key, 0 or pk; the keys stay inside the cap)
+    P.off = kCascade ? (pc[5] == pk ? pk : 0) : 0;
+    P.a = min(max(pc[1] + P.off, 0), cap - 1);
+    P.e = min(max(pc[2] + P.off, P.a + 1), cap);
     P.first = min(max(pc[3], 0), int(nr) - 1);
     P.nranges = min(max(pc[4], 1), int(nr) - P.first);
-    P.slot = pc[5];
-    P.off = 0;
+    P.slot = kCascade ? -1 : pc[5];
     return P;
   };
 
@@ -1165,12 +1171,13 @@ size_t rows_plan_bytes(int32_t batch, int blocks) { return plan_words(batch, blo
 
 int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
                      const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
-                     int blocks, hipStream_t stream, int32_t block_size) {
+                     int blocks, hipStream_t stream, int32_t block_size, int32_t prefix_keys) {
   auto k = block_size == 64 ? decode_plan_kernel<64> : block_size == 32 ? decode_plan_kernel<32>
                                                                          : decode_plan_kernel<kRowsBlock>;
   if (block_size != kRowsBlock && block_size != 32 && block_size != 64) return IFN_ERR_UNSUPPORTED;
+  if (prefix_keys < 0 || (prefix_keys > 0 && slots != nullptr)) return IFN_ERR_INVALID_ARGUMENT;
   k<<<dim3(1), dim3(kPlanThreads), 0, stream>>>(plan, block_tables, max_pages, seq_lens, active, slots, num_pages,
-                                                batch, max_len, blocks);
+                                                batch, max_len, blocks, prefix_keys);
   return ifn_launch_status();
 }
 

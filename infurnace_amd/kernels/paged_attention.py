@@ -84,24 +84,30 @@ class DecodePlan:
         return None if self.buf is None else self.buf.data_ptr()
 
 
-def _plan_key(query_shape, slot_mapping, pool_layer, block_tables, sequence_lengths, active_mask, max_seq_len):
+def _plan_key(query_shape, slot_mapping, pool_layer, block_tables, sequence_lengths, active_mask, max_seq_len,
+              shared_pages=None):
     """What a plan depends on, by tensor identity: shapes, the pool's page geometry, the tables,
-    lengths, mask, slots and the length cap."""
+    lengths, mask, slots, the length cap and (shared-prefix plans) the number of shared pages."""
     return (tuple(query_shape), None if slot_mapping is None else slot_mapping.data_ptr(),
             tuple(pool_layer.shape), block_tables.data_ptr(), tuple(block_tables.shape),
-            sequence_lengths.data_ptr(), None if active_mask is None else active_mask.data_ptr(), int(max_seq_len))
+            sequence_lengths.data_ptr(), None if active_mask is None else active_mask.data_ptr(), int(max_seq_len),
+            None if shared_pages is None else int(shared_pages))
 
 
 @accepts_carriers
 def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, sequence_lengths: torch.Tensor,
                 active_mask: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None, *,
-                layer: int = 0, block_size: int = 16, max_seq_len: int | None = None) -> DecodePlan:
+                layer: int = 0, block_size: int = 16, max_seq_len: int | None = None,
+                shared_prefix_pages: torch.Tensor | None = None) -> DecodePlan:
     """Build the step plan for decode calls with these tables, lengths, mask and (optionally) slots.
 
     ``query_shape`` is the decode query's shape [B, Hq, D].  The plan is computed on the
     current stream.  Pass it as ``plan=`` to ``paged_attention`` / ``store_kv_and_decode`` for
-    every layer of the step; with ``slot_mapping`` it also serves the fused append.  Shapes
-    that decode without a plan give an empty plan, which the calls accept and ignore.
+    every layer of the step; with ``slot_mapping`` it also serves the fused append.  With
+    ``shared_prefix_pages`` (the tensor the step's ``paged_attention`` calls pass; only its
+    length matters here) it is the plan of the shared-prefix decode
+    (``ifn_paged_decode_shared_prefix_plan``) and takes no slots.  Shapes that decode without a
+    plan give an empty plan, which the calls accept and ignore.
     """
     pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
     dev = pool_layer.device
@@ -125,7 +131,16 @@ def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, 
     msl = cap if max_seq_len is None else min(int(max_seq_len), cap)
     if msl < 0:
         raise PagedAttentionError("max_seq_len must be non-negative")
-    key = _plan_key((n, hq, d), slot_mapping, pool_layer, block_tables, sequence_lengths, active_mask, msl)
+    sp = None
+    if shared_prefix_pages is not None:
+        if not isinstance(shared_prefix_pages, torch.Tensor) or shared_prefix_pages.ndim != 1:
+            raise PagedAttentionError("shared_prefix_pages must be a rank-1 int32 tensor")
+        sp = shared_prefix_pages.shape[0]
+        if sp > max_pages:
+            raise PagedAttentionError(f"{sp} shared pages exceed the table's {max_pages} columns")
+        if slot_mapping is not None:
+            raise PagedAttentionError("a shared-prefix plan takes no slot_mapping (that decode has no fused append)")
+    key = _plan_key((n, hq, d), slot_mapping, pool_layer, block_tables, sequence_lengths, active_mask, msl, sp)
     if n == 0:
         return DecodePlan(None, 0, key)
     lib = _capi.lib()
@@ -134,12 +149,18 @@ def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, 
         return DecodePlan(None, 0, key)
     # zero-filled, so that words the kernel leaves unwritten compare equal between two plans
     buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
-    _capi.call("ifn_paged_decode_plan", buf.data_ptr(), nbytes, ptr(block_tables), max_pages, ptr(sequence_lengths),
-               ptr(active_mask), ptr(slot_mapping), P, n, hq, hkv, d, bs, msl, current_stream(dev))
+    if sp is None:
+        _capi.call("ifn_paged_decode_plan", buf.data_ptr(), nbytes, ptr(block_tables), max_pages,
+                   ptr(sequence_lengths), ptr(active_mask), ptr(slot_mapping), P, n, hq, hkv, d, bs, msl,
+                   current_stream(dev))
+    else:
+        _capi.call("ifn_paged_decode_shared_prefix_plan", buf.data_ptr(), nbytes, ptr(block_tables), max_pages,
+                   ptr(sequence_lengths), ptr(active_mask), sp, P, n, hq, hkv, d, bs, msl, current_stream(dev))
 
     def rebuild():
         return decode_plan(query_shape, kv_pool, block_tables, sequence_lengths, active_mask, slot_mapping,
-                           layer=layer, block_size=block_size, max_seq_len=max_seq_len)
+                           layer=layer, block_size=block_size, max_seq_len=max_seq_len,
+                           shared_prefix_pages=shared_prefix_pages)
     return DecodePlan(buf, nbytes, key, rebuild)
 
 
@@ -212,8 +233,9 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
     pages (non-temporal loads, each page expected to be read by one row); an
     empty ``shared_prefix_pages`` declares rows that share pages outside a
     common leading run, and the decode then keeps pages in the caches.
-    ``plan`` (decode only, from ``decode_plan`` over the same tensors) is the
-    step's precomputed split; the result is bit-identical without it.
+    ``plan`` (decode only, from ``decode_plan`` over the same tensors, with the same
+    ``shared_prefix_pages`` when they are given) is the step's precomputed split; the result is
+    bit-identical without it.
 
     ``validate=True`` (a debug mode: it synchronises) checks, before the launch,
     what the kernels otherwise trust: that every table entry a row reads names a
@@ -283,6 +305,14 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
                 _validate_shared_prefix(block_tables, keys, shared_prefix_pages, bs)
             nbytes = lib.ifn_paged_decode_shared_prefix_workspace_bytes(n, hq, hkv, d, bs, sp)
             ws = workspace_for(dev, stream, nbytes)
+            if plan is not None:  # a plan from decode_plan(..., shared_prefix_pages=...)
+                key = _plan_key((n, hq, d), None, pool_layer, block_tables, sequence_lengths, active_mask, msl, sp)
+                pp = plan.ptr_for(key, False)
+                _capi.call("ifn_paged_decode_shared_prefix_planned", ptr(out), ptr(query), ptr(pool_layer), P,
+                           ptr(shared_prefix_pages), sp, ptr(block_tables), max_pages, ptr(sequence_lengths),
+                           ptr(active_mask), n, hq, hkv, d, bs, msl, float(scale), pp, plan.nbytes if pp else 0,
+                           ptr(ws), ws.numel(), stream)
+                return out
             _capi.call("ifn_paged_decode_shared_prefix", ptr(out), ptr(query), ptr(pool_layer), P,
                        ptr(shared_prefix_pages), sp, ptr(block_tables), max_pages, ptr(sequence_lengths),
                        ptr(active_mask), n, hq, hkv, d, bs, msl, float(scale), ptr(ws), ws.numel(), stream)

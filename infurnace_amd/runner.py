@@ -108,6 +108,7 @@ class _Step:
                                     layer=layer, max_seq_len=self.max_len, out=out, plan=self._decode_plan(q))
         else:
             store_kv(kv, self.slot_mapping, self.active, k, v, layer=layer)
+            # (unplanned: a shared-prefix step plan measures no faster than the kernel's own split)
             o = paged_attention(q, kv, self.block_tables, self.seq_lens, self.active, layer=layer,
                                 max_seq_len=self.max_len, out=out, shared_prefix_pages=self.shared_prefix)
         self._launched()

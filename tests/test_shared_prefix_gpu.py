@@ -186,3 +186,78 @@ def test_no_common_prefix_cached_loads_equal_streaming(dev, hq, hkv, d):
     streamed = paged_attention(*args)
     assert torch.equal(cached.view(torch.int16), streamed.view(torch.int16))
     assert_attn_close(cached, oracle.paged_attention(q, pool, table, lens), f"hq={hq} hkv={hkv} d={d}")
+
+
+def _planned_equal(dev, pool, table, lens, q, prefix, active=None, what=""):
+    """The planned shared-prefix decode equals the unplanned one bit for bit."""
+    from infurnace_amd.kernels import decode_plan
+    t, l = to_dev(table, dev), to_dev(lens, dev)
+    p, qd = (pool if isinstance(pool, torch.Tensor) else to_dev(pool, dev)), to_dev(q, dev)
+    pf = to_dev(prefix, dev) if not isinstance(prefix, torch.Tensor) else prefix
+    am = None if active is None else to_dev(active, dev)
+    o1 = torch.full_like(qd, 7.0)
+    o2 = torch.full_like(qd, 7.0)
+    paged_attention(qd, p, t, l, am, out=o1, shared_prefix_pages=pf)
+    plan = decode_plan(qd.shape, p, t, l, am, shared_prefix_pages=pf)
+    for _ in range(2):  # the plan serves every layer of the step
+        paged_attention(qd, p, t, l, am, out=o2, shared_prefix_pages=pf, plan=plan)
+        torch.cuda.synchronize()
+        assert torch.equal(o1.view(torch.int16), o2.view(torch.int16)), f"{what}: planned differs"
+    return o2
+
+
+@pytest.mark.parametrize("hq", [16, 32])
+def test_planned_equals_unplanned(dev, hq):
+    """A step plan of the shared-prefix decode (ifn_paged_decode_shared_prefix_plan): rows longer
+    than the prefix, exactly the prefix, shorter than it, inactive and empty; with rows split over
+    several workgroups and with ranges holding more rows than a plan record describes."""
+    say(f"shared-prefix planned == unplanned hq={hq}")
+    rng = np.random.default_rng(60 + hq)
+    suffix = [5, 200, 0, 64, 77, 1, 3000, 31, 9, 0, 450] + [2] * 40
+    pool, table, lens, q, prefix = _shared(rng, 12, suffix, hq, 8, 128, short_rows=[(1, 40), (4, 191), (7, 0)])
+    active = np.ones(len(suffix), np.uint8)
+    active[[3, 6]] = 0
+    out = _planned_equal(dev, pool, table, lens, q, prefix, active, "ragged")
+    live = [i for i in range(len(suffix)) if active[i] and lens[i] > 0]
+    assert_attn_close(out[live], oracle.paged_attention(q[live], pool, table[live], lens[live]), "planned ragged")
+    # every cascade row exactly the prefix (the token list holds only the short rows)
+    pool, table, lens, q, prefix = _shared(rng, 9, [0, 0, 0, 0], hq, 8, 128, short_rows=[(2, 17)])
+    _planned_equal(dev, pool, table, lens, q, prefix, None, "prefix only")
+    # 1500 rows of one private key: about 8 pieces per range, past the 3 a plan record holds
+    pool, table, lens, q, prefix = _shared(rng, 2, [1] * 1500 + [2000], hq, 8, 128)
+    out = _planned_equal(dev, pool, table, lens, q, prefix, None, "many pieces per range")
+    rows = [0, 1, 700, 1499, 1500]
+    assert_attn_close(out[rows], oracle.paged_attention(q[rows], pool, table[rows], lens[rows]), "many pieces")
+
+
+def test_planned_config5_and_mismatched_plans(dev):
+    """Config 5 at full size: planned == unplanned.  A plan built for a different shared-page count is
+    refused by the wrapper; passed to the C entry point it is detected there and ignored (same bits)."""
+    from infurnace_amd import _capi
+    from infurnace_amd.kernels import decode_plan
+    say("shared-prefix planned config5")
+    w = workloads.config5()
+    g = torch.Generator(device=dev).manual_seed(515)
+    pool = randn16((2, w.num_pages, 16, 8, 128), g, dev)
+    q = randn16((w.batch, 32, 128), g, dev)
+    sp = w.shared_prefix_pages
+    prefix = to_dev(w.block_tables[0, :sp].copy(), dev)
+    out = _planned_equal(dev, pool, w.block_tables, w.seq_lens, q.cpu().numpy(), prefix, None, "config5")
+    rows = [0, 31, 63]
+    assert_attn_close(out[rows], oracle_decode(pool, w.block_tables, w.seq_lens, q, rows=rows), "config5 rows")
+    t, l = to_dev(w.block_tables, dev), to_dev(w.seq_lens, dev)
+    other = decode_plan(q.shape, pool, t, l, shared_prefix_pages=prefix[:sp - 1])
+    with pytest.raises(Exception):
+        paged_attention(q, pool, t, l, None, shared_prefix_pages=prefix, plan=other)
+    L = _capi.lib()
+    nb = L.ifn_paged_decode_shared_prefix_workspace_bytes(w.batch, 32, 8, 128, 16, sp)
+    ws = torch.zeros(nb, dtype=torch.uint8, device=dev)
+    o3 = torch.empty_like(q)
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    rc = L.ifn_paged_decode_shared_prefix_planned(o3.data_ptr(), q.data_ptr(), pool.data_ptr(), w.num_pages,
+                                                  prefix.data_ptr(), sp, t.data_ptr(), t.shape[1], l.data_ptr(), None,
+                                                  w.batch, 32, 8, 128, 16, int(w.seq_lens.max()), 0.0,
+                                                  other.buf.data_ptr(), other.nbytes, ws.data_ptr(), nb, stream)
+    assert rc == 0
+    torch.cuda.synchronize()
+    assert torch.equal(o3.view(torch.int16), out.view(torch.int16)), "a plan for another prefix was not ignored"
