@@ -199,3 +199,50 @@ def test_prep_and_page_ops_host_validation():
     assert L.ifn_zero_pages(A, 2, 64, A, 0, 8, 128, 16, None) == _capi.IFN_OK
     assert L.ifn_copy_pages(A, 2, 64, None, A, 3, 8, 128, 16, None) == _capi.IFN_ERR_INVALID_ARGUMENT
     assert L.ifn_copy_pages(A, 2, 64, A, A, 0, 8, 128, 16, None) == _capi.IFN_OK
+
+
+def test_prefill_prep_append_host_validation():
+    """ifn_paged_prefill_prep_append rejects bad arguments before any HIP call."""
+    L = _capi.lib()
+    ok = dict(out=A, q=A, k=A, v=A, wq=A, wk=A, rope=A, maxpos=8192, pool=A, P=256, table=A, mp=64, qs=512, T=512,
+              hq=16, hkv=8, d=128, bs=16, eps=1e-6)
+
+    def call(**kw):
+        a = {**ok, **kw}
+        return L.ifn_paged_prefill_prep_append(a["out"], a["q"], a["k"], a["v"], a["wq"], a["wk"], a["rope"],
+                                               a["maxpos"], a["pool"], a["P"], a["table"], a["mp"], a["qs"], a["T"],
+                                               a["hq"], a["hkv"], a["d"], a["bs"], a["eps"], 0.0, None, 0, None)
+
+    assert call(q=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(rope=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(hq=12) == _capi.IFN_ERR_INVALID_ARGUMENT            # not a multiple of the kv heads
+    assert call(eps=-1.0) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert call(bs=32) == _capi.IFN_ERR_UNSUPPORTED
+    assert call(d=256) == _capi.IFN_ERR_UNSUPPORTED                 # no prefill kernel for this head dim
+    assert call(qs=48) == _capi.IFN_ERR_UNSUPPORTED                 # not a multiple of 32: run the two launches
+    assert call(k=A + 4) == _capi.IFN_ERR_ALIGNMENT
+    assert call(rope=A + 8) == _capi.IFN_ERR_ALIGNMENT
+    assert call(T=0) == _capi.IFN_OK
+    assert call(qs=512, T=1024) == _capi.IFN_ERR_INVALID_ARGUMENT   # past the table's 1024 keys
+    assert call(maxpos=1000) == _capi.IFN_ERR_INVALID_ARGUMENT      # positions past the rotary table
+
+
+def test_shared_prefix_plan_host_validation():
+    """The shared-prefix plan rejects bad arguments on the host; planned and unplanned entries agree on them."""
+    L = _capi.lib()
+    ok = dict(plan=A, nb=1 << 20, bt=A, mp=288, sl=A, act=None, sp=256, P=4096, B=64, hq=32, hkv=8, d=128, bs=16,
+              msl=4608)
+
+    def plan(**kw):
+        a = {**ok, **kw}
+        return L.ifn_paged_decode_shared_prefix_plan(a["plan"], a["nb"], a["bt"], a["mp"], a["sl"], a["act"], a["sp"],
+                                                     a["P"], a["B"], a["hq"], a["hkv"], a["d"], a["bs"], a["msl"], None)
+
+    assert plan(bt=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert plan(sp=-1) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert plan(sp=289) == _capi.IFN_ERR_INVALID_ARGUMENT           # more shared pages than table columns
+    assert plan(hq=30) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert plan(bs=32) == _capi.IFN_ERR_UNSUPPORTED
+    assert plan(B=0) == _capi.IFN_OK
+    assert plan(nb=64) == _capi.IFN_ERR_WORKSPACE                   # buffer smaller than the plan
+    assert plan(plan=A + 4) == _capi.IFN_ERR_ALIGNMENT
