@@ -602,8 +602,10 @@ def run_page_size_sweep(lib, hip, dev, g, stream, layers: int = 8, reps: int = 1
 
 def run_config1(lib, hip, dev, stream, reps: int = 200) -> dict:
     """Config 1 (the CPU-runnable case): one token's append at position 511 and single-row decode over
-    512 tokens, timed as two launches (ifn_store_kv + ifn_paged_decode) and as one fused launch
-    (ifn_paged_decode_append); µs per call from HIP events, median over ``reps`` calls."""
+    512 tokens, timed as two launches (ifn_store_kv + ifn_paged_decode), as one fused launch
+    (ifn_paged_decode_append) and as one fused launch with the step plan (the plan's own launch
+    timed beside it and charged per layer of a 28-layer step); µs per call from HIP events, median
+    over ``reps`` calls."""
     import torch
     c = workloads_mod().config1()
     pool = torch.from_numpy(c["pool"]).to(dev)
@@ -629,8 +631,24 @@ def run_config1(lib, hip, dev, stream, reps: int = 200) -> dict:
                                            sl.data_ptr(), None, slots.data_ptr(), k.data_ptr(), v.data_ptr(), 1, 16,
                                            8, 128, 16, 512, scale, ws.data_ptr(), ws_bytes, stream)
 
+    # the step plan of a one-row decode step (built once per step, shared by its layers)
+    plan_bytes = lib.ifn_paged_decode_plan_bytes(1, 16, 8, 128, 16, 32, 512)
+    plan = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
+
+    def mkplan():
+        return lib.ifn_paged_decode_plan(plan.data_ptr(), plan_bytes, bt.data_ptr(), 32, sl.data_ptr(), None,
+                                         slots.data_ptr(), P, 1, 16, 8, 128, 16, 512, stream)
+
+    def fused_planned():
+        return lib.ifn_paged_decode_append_planned(out.data_ptr(), q.data_ptr(), pool.data_ptr(), P, bt.data_ptr(), 32,
+                                                   sl.data_ptr(), None, slots.data_ptr(), k.data_ptr(), v.data_ptr(), 1,
+                                                   16, 8, 128, 16, 512, scale, plan.data_ptr(), plan_bytes,
+                                                   ws.data_ptr(), ws_bytes, stream)
+
+    if mkplan():
+        raise RuntimeError("config 1: plan launch failed")
     res = {"workload": "config 1: B=1, context 512, 64-page pool, one layer (append at 511 + decode)"}
-    for name, fn in (("two_launch", two), ("fused", fused)):
+    for name, fn in (("two_launch", two), ("fused", fused), ("fused_planned", fused_planned), ("plan", mkplan)):
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
@@ -648,6 +666,8 @@ def run_config1(lib, hip, dev, stream, reps: int = 200) -> dict:
                                                    for r in range(reps)])) * 1e3, 2)
         res[f"{name}_host_us_per_call"] = round(wall_us, 2)  # launch rate through ctypes, back to back
         hip.destroy(evs)
+    # a 28-layer step of the planned fused form: one plan, then 28 launches
+    res["fused_planned_us_per_layer_with_plan"] = round(res["fused_planned_us"] + res["plan_us"] / 28, 2)
     return res
 
 
