@@ -76,7 +76,7 @@ struct WideCfg {
   static constexpr int kQInstr = kQBytes / 16 / kThreads;  // 16-byte loads per lane
   static constexpr int kQRowsPerWave = kRows / W;          // rows each wave stages
   static constexpr int kMlFloats = W * RT * 32 * 2;
-  static constexpr int kMergeBytes = kMlFloats * 4 + W * kBlocks * 16 * kWave * 4;
+  static constexpr int kMergeBytes = kMlFloats * 4 + W * kBlocks * 16 * kWave * 2;  // (m, l) + O / l in fp16
   static constexpr int kLdsBytes = kTileBytes + kQBytes > kMergeBytes ? kTileBytes + kQBytes : kMergeBytes;
   static_assert(RT == 1 || RT == 2, "one or two row tiles");
   static_assert(kQw * G == kRows, "32 RT rows per workgroup");
@@ -807,9 +807,11 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
   float lt[RT];
 #pragma unroll
   for (int rt = 0; rt < RT; ++rt) lt[rt] = lsum[rt] + __shfl_xor(lsum[rt], 32);
-  // Key-group merge: every wave writes its (m, l) and all its blocks to LDS; block p = (dim tile
-  // p / RT, row tile p % RT) is then finished, quarter by quarter, by the waves that own it, from
-  // the W groups' copies in group order.  Every quarter a wave finishes has row tile rt_own.
+  // Key-group merge: every wave writes its (m, l) and all its blocks, normalised (O / l) in fp16,
+  // to LDS (half the bytes of fp32 accumulators; O / l is a convex combination of fp16 value rows,
+  // so fp16 keeps it to a relative 2^-11); block p = (dim tile p / RT, row tile p % RT) is then
+  // finished, quarter by quarter, by the waves that own it, from the W groups' copies in group
+  // order, each weighted by e^(m - M) l.  Every quarter a wave finishes has row tile rt_own.
   auto own = [&](int u, int& p, int& r4) __attribute__((always_inline)) {  // owned quarter u
     if constexpr (C::kBlocks >= W) {
       p = grp + W * (u / 4);
@@ -821,7 +823,7 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
   };
   const int rt_own = (C::kBlocks >= W ? grp : grp % C::kBlocks) % RT;
   float* mlb = reinterpret_cast<float*>(smem);                 // [wave][rt][32][2]
-  f32x4* accb = reinterpret_cast<f32x4*>(mlb + C::kMlFloats);  // [wave][block][4][lane]
+  f16x4* accb = reinterpret_cast<f16x4*>(mlb + C::kMlFloats);  // [wave][block][4][lane]: O / l in fp16
   if (half == 0) {
 #pragma unroll
     for (int rt = 0; rt < RT; ++rt) {
@@ -829,12 +831,17 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
       mlb[((grp * RT + rt) * 32 + col) * 2 + 1] = lt[rt];
     }
   }
+  float linv[RT];
+#pragma unroll
+  for (int rt = 0; rt < RT; ++rt) linv[rt] = lt[rt] > 0.f ? 1.f / lt[rt] : 0.f;
 #pragma unroll
   for (int p = 0; p < C::kBlocks; ++p)
 #pragma unroll
     for (int r4 = 0; r4 < 4; ++r4) {
       const f32x16& a = acc[p / RT][p % RT];
-      accb[((grp * C::kBlocks + p) * 4 + r4) * kWave + lane] = f32x4{a[4 * r4], a[4 * r4 + 1], a[4 * r4 + 2], a[4 * r4 + 3]};
+      const float iv = linv[p % RT];
+      accb[((grp * C::kBlocks + p) * 4 + r4) * kWave + lane] =
+          f16x4{f16(a[4 * r4] * iv), f16(a[4 * r4 + 1] * iv), f16(a[4 * r4 + 2] * iv), f16(a[4 * r4 + 3] * iv)};
     }
   __syncthreads();
   float mk[W], lk[W];
@@ -852,18 +859,21 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
   float lfin = wk[0] * lk[0];
 #pragma unroll
   for (int k = 1; k < W; ++k) lfin = fmaf(wk[k], lk[k], lfin);
+  float wl[W];  // weight of wave k's O / l
+#pragma unroll
+  for (int k = 0; k < W; ++k) wl[k] = wk[k] * lk[k];
   f32x4 o[C::kOwnU];  // the quarters this wave finishes
 #pragma unroll
   for (int u = 0; u < C::kOwnU; ++u) {
     int p, r4;
     own(u, p, r4);
-    f32x4 x = accb[((0 * C::kBlocks + p) * 4 + r4) * kWave + lane];
-    f32x4 y = x * wk[0];
+    f16x4 x = accb[((0 * C::kBlocks + p) * 4 + r4) * kWave + lane];
+    f32x4 y = f32x4{wl[0] * float(x[0]), wl[0] * float(x[1]), wl[0] * float(x[2]), wl[0] * float(x[3])};
 #pragma unroll
     for (int k = 1; k < W; ++k) {
       x = accb[((k * C::kBlocks + p) * 4 + r4) * kWave + lane];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) y[e] = fmaf(wk[k], x[e], y[e]);
+      for (int e = 0; e < 4; ++e) y[e] = fmaf(wl[k], float(x[e]), y[e]);
     }
     o[u] = y;
   }
