@@ -102,8 +102,9 @@ def run_cpu_baseline(w, pool_layer, q, seconds: float) -> dict:
 
     value: torch-CPU float32 scaled_dot_product_attention(enable_gqa=True) per row -- the contiguous
     SDPA of model.py:196-200 -- after gathering the row's pages (index_select) and upcasting them, on
-    all the process's host threads (the attention a CPU host would run for this step).  c_port: the oracle (plain C port of
-    the same algorithm) on all rows per pass, rows split over the same threads, then on one thread."""
+    all the process's host threads (the attention a CPU host would run for this step).  c_port: the
+    oracle (plain C port of the same algorithm) on all rows per pass, rows split over the same
+    threads, then on one thread."""
     import torch
     import torch.nn.functional as F
 
