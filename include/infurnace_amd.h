@@ -238,12 +238,18 @@ size_t ifn_paged_decode_shared_prefix_workspace_bytes(int32_t batch, int32_t num
  * ifn_paged_decode for a batch whose rows share leading pages (a prefix-cache
  * hit): prefix_pages[0 .. shared_pages) are pages that every row of at least
  * shared_pages * block_size keys holds, in that order, at the start of its
- * block table.  Launches on `stream`: the shared pages are read once for all
- * rows (an MFMA pass of every row's queries over them, split over keys), then
- * each row streams only its own pages and is merged with the shared pages'
- * partial softmax states -- inside that decode launch when the token row
- * (num_kv_heads x head_dim fp16) is 2 KiB, else by a third, combine launch per
- * (row, kv head).  Same arguments, output and rules as
+ * block table.  The shared pages are read once for all rows (an MFMA pass of
+ * every row's queries over them, split over keys), each row streams only its
+ * own pages, and the two are merged as partial softmax states.  For head_dim
+ * 128 with 8 kv heads and 16 or 32 query heads, and batches whose prefix pass
+ * fits half the CUs (prefixes up to 8192 keys), that is one launch: part of
+ * the grid runs the prefix pass while the rest streams the private pages, and
+ * whichever workgroup finishes a (row, kv head) last merges it.  Otherwise
+ * the prefix pass is one launch and the decode a second, which merges the
+ * states itself when the token row (num_kv_heads x head_dim fp16) is 2 KiB,
+ * else a third, combine launch per (row, kv head) does.  Inputs must be
+ * finite (the one-launch form shares the prefill kernel's assumption that
+ * scores are never NaN).  Same arguments, output and rules as
  * ifn_paged_decode otherwise; rows shorter than the prefix are attended in
  * full through their own table.  shared_pages == 0 is ifn_paged_decode with
  * cached page loads, for batches whose rows share pages anywhere in their
@@ -285,7 +291,9 @@ int ifn_paged_decode_shared_prefix_plan(void* plan, size_t plan_bytes, const int
 /*
  * ifn_paged_decode_shared_prefix with a step plan from
  * ifn_paged_decode_shared_prefix_plan (NULL: none).  Same arguments,
- * workspace and output otherwise (bit-identical to the unplanned call); a
+ * workspace and output otherwise (bit-identical to the unplanned call; the
+ * one-launch form splits the private keys over its own share of the CUs and
+ * does not read the plan); a
  * plan for other shapes, batch size or shared_pages is detected and ignored,
  * one built from other lengths or tables of the same shapes gives wrong
  * results.

@@ -41,6 +41,8 @@ DEVICE_FLAGS = [
 # that are never NaN for finite inputs (masked keys are -inf), so fmaxf needs no NaN-quieting of
 # its operands.  The precondition -- finite queries and K/V -- is part of the documented interface
 # (the header's layout notes); with a NaN or Inf among the inputs the prefill output is unspecified.
+# The one-launch shared-prefix decode, which runs the prefill body on some of its workgroups, is in
+# the same file and shares both.
 FILE_FLAGS = {
     "paged_prefill_wide.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form", "-fno-honor-nans"],
     # The whole-row decode kernel's first nine arguments (plan, pool, tables, query, sizes, grid) are

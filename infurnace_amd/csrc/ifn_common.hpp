@@ -110,6 +110,15 @@ __device__ __forceinline__ void st_dev(float* p, float v) {
 __device__ __forceinline__ float ld_dev(const float* p) {
   return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
+// The same for 8 bytes at an 8-byte aligned address (one instruction each).
+__device__ __forceinline__ void st_dev8(void* p, f32x2 v) {
+  __hip_atomic_store(static_cast<uint64_t*>(p), __builtin_bit_cast(uint64_t, v), __ATOMIC_RELAXED,
+                     __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ f32x2 ld_dev8(const void* p) {
+  return __builtin_bit_cast(f32x2, __hip_atomic_load(static_cast<uint64_t*>(const_cast<void*>(p)), __ATOMIC_RELAXED,
+                                                     __HIP_MEMORY_SCOPE_AGENT));
+}
 
 // Device-coherent 8- and 16-byte accesses through a buffer resource: the same sc1 cache policy
 // as st_dev / ld_dev (agent scope: written through to, and read from, the device coherence
@@ -411,13 +420,22 @@ int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pag
                      const uint8_t* active, const int32_t* slots, int64_t num_pages, int32_t batch, int32_t max_len,
                      int blocks, hipStream_t stream, int32_t block_size = 16, int32_t prefix_keys = 0);
 // prep (non-null): the fused pre-append variant; ap then carries the slots and the pool, and q is unused.
-// px (non-null): shared-prefix mode (DecodePrefix), without append or plan.
+// px (non-null): shared-prefix mode (DecodePrefix), without append (plan: one built for px.pages).
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
                        const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
                        const DecodePrep* prep = nullptr, const DecodePrefix* px = nullptr, int32_t block_size = 16);
 bool rows_prep_supported(int32_t hq, int32_t hkv, int32_t d);
+// The shared-prefix decode as one launch (prefix pass and private-page decode in one grid), for the
+// shapes and sizes it is built for; IFN_ERR_UNSUPPORTED otherwise (the caller then runs the two
+// launches).  workspace: the whole-row decode's layout for `blocks` workgroups at offset 0; px: the
+// prefix states' region, room for max_states states per segment (px.nstates is set here).
+int shared_prefix_fused_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages,
+                               const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
+                               const uint8_t* active, int32_t batch, int32_t hq, int32_t hkv, int32_t d,
+                               int32_t max_len, float scale_log2, void* workspace, int blocks, const DecodePrefix& px,
+                               int max_states, int cus, hipStream_t stream);
 
 }  // namespace ifn
 

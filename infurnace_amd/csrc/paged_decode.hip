@@ -1038,6 +1038,13 @@ static int shared_prefix_entry(void* out, const void* query, const void* kv_pool
   const DecodePrefix px{reinterpret_cast<float*>(wsb + L.st_ml), reinterpret_cast<float*>(wsb + L.st_o),
                         shared_pages, L.nstates, rows ? reinterpret_cast<const f16*>(wsb + L.st_o) : nullptr};
   const hipStream_t s = reinterpret_cast<hipStream_t>(stream);
+  if (rows) {  // one launch where it is built for the shape (the step plan is then not used)
+    const int rc = shared_prefix_fused_launch(
+        static_cast<f16*>(out), static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
+        prefix_pages, block_tables, max_pages_per_seq, seq_lens, active_mask, batch, num_q_heads, num_kv_heads,
+        head_dim, max_seq_len, scale * kLog2e, workspace, blocks, px, L.nstates, cus, s);
+    if (rc != IFN_ERR_UNSUPPORTED) return rc;
+  }
   // 1. every row's queries against the shared pages, once (states 0 .. nstates - 2)
   int rc = prefix_pass(static_cast<const f16*>(query), static_cast<const f16*>(kv_pool_layer), num_pages,
                        prefix_pages, key_len, batch, num_q_heads, num_kv_heads, head_dim, scale * kLog2e, px.ml,

@@ -33,6 +33,7 @@
 //    read and writes them to the pool, and the workgroup prepares its own queries straight into the
 //    LDS staging; the attention then runs as in the plain kernel.
 #include "ifn_common.hpp"
+#include "decode_rows.hpp"
 
 namespace ifn {
 
@@ -192,11 +193,12 @@ __device__ __forceinline__ void pin_probs(f16x8 (&p)[RT][2]) {
 #endif
 }
 
+// The kernel's body, run by workgroup bid of grid, with its LDS at smem (WideCfg::kLdsBytes).
 template <int D, int G, int RT, int W, bool kAppend, bool kPrep>
-__global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
-    f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
-    const int32_t* __restrict__ table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb,
-    int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap, PrefixOut px, PrefillPrep pp) {
+__device__ __forceinline__ void prefill_wide_body(
+    unsigned char* smem, const int bid, const int grid, f16* out, const f16* q, const f16* pool, int64_t num_pages,
+    const int32_t* table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb, int32_t nsplit,
+    float scale_log2, PrefillWorkspace ws, PrefillAppend ap, PrefixOut px, PrefillPrep pp) {
   static_assert(!(kAppend && kPrep), "one form of the fused append");
   using C = WideCfg<D, G, RT, W>;
   constexpr int kKS = C::kKSteps;
@@ -204,9 +206,9 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
   constexpr int kQw = C::kQw;
   // Workgroup i runs on XCD i % 8: kv head = i % Hkv keeps each head's K/V in one XCD's L2 (for
   // Hkv = 8); query blocks go longest key range first.
-  const int kvh = int(blockIdx.x) % num_kv_heads;
-  const int split = (int(blockIdx.x) / num_kv_heads) % nsplit;
-  const int qb = n_qb - 1 - int(blockIdx.x) / (num_kv_heads * nsplit);
+  const int kvh = bid % num_kv_heads;
+  const int split = (bid / num_kv_heads) % nsplit;
+  const int qb = n_qb - 1 - bid / (num_kv_heads * nsplit);
   const int tid = threadIdx.x;
   const int grp = __builtin_amdgcn_readfirstlane(tid / kWave);  // key group = wave
   const int lane = tid % kWave;
@@ -234,7 +236,6 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     my_pos[rt] = prefix_mode ? total - 1 : query_start + my_q[rt];
     q_ok[rt] = my_q[rt] < T;
   }
-  __shared__ __attribute__((aligned(16))) unsigned char smem[C::kLdsBytes];
 
   const int64_t tok_stride = int64_t(num_kv_heads) * D;
   const int64_t v_off = num_pages * kWBlock * tok_stride;
@@ -245,7 +246,7 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
 
   if constexpr (kAppend)
     wide_store_chunk(ap.pool, num_pages, table, query_start, T, num_kv_heads, D, ap.new_k, ap.new_v,
-                     int(blockIdx.x) * C::kThreads + tid, int(gridDim.x) * C::kThreads);
+                     bid * C::kThreads + tid, grid * C::kThreads);
 
   // Page ids: a tile of 32 keys spans two pages.  Lane l of a window holds page 2 * tile + (l & 1) of
   // the wave's (l / 2)-th tile of that window (32 tiles), read with v_readlane.  A tile's K and V
@@ -882,7 +883,8 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
     if (!q_ok[rt_own]) return;
     const int g = my_head[rt_own] - kvh * G;
     const int64_t pslot = ((int64_t(my_q[rt_own]) * num_kv_heads + kvh) * px.stride + split) * G + g;
-    if (grp < RT && half == 0) *reinterpret_cast<f32x2*>(px.ml + pslot * 2) = f32x2{mfin, lfin};
+    // (8-byte stores at the device coherence point: a workgroup of the same launch may merge them)
+    if (grp < RT && half == 0) st_dev8(px.ml + pslot * 2, f32x2{mfin, lfin});
     const float inv = lfin > 0.f ? 1.f / lfin : 0.f;
 #pragma unroll
     for (int u = 0; u < C::kOwnU; ++u) {  // dims 32 dt + 8 r4 + 4 half + 0..3 of block p
@@ -890,8 +892,8 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
       own(u, p, r4);
       const int64_t at = pslot * D + 32 * (p / RT) + 8 * r4 + 4 * half;
       if (px.oh != nullptr)  // (uniform) normalised, fp16
-        *reinterpret_cast<f16x4*>(px.oh + at) =
-            f16x4{f16(o[u][0] * inv), f16(o[u][1] * inv), f16(o[u][2] * inv), f16(o[u][3] * inv)};
+        st_dev8(px.oh + at, __builtin_bit_cast(f32x2, f16x4{f16(o[u][0] * inv), f16(o[u][1] * inv),
+                                                          f16(o[u][2] * inv), f16(o[u][3] * inv)}));
       else
         *reinterpret_cast<f32x4*>(px.o + at) = o[u];
     }
@@ -988,6 +990,16 @@ __global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
   }
 }
 
+template <int D, int G, int RT, int W, bool kAppend, bool kPrep>
+__global__ __launch_bounds__(W * kWave) void prefill_wide_kernel(
+    f16* __restrict__ out, const f16* __restrict__ q, const f16* __restrict__ pool, int64_t num_pages,
+    const int32_t* __restrict__ table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb,
+    int32_t nsplit, float scale_log2, PrefillWorkspace ws, PrefillAppend ap, PrefixOut px, PrefillPrep pp) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[WideCfg<D, G, RT, W>::kLdsBytes];
+  prefill_wide_body<D, G, RT, W, kAppend, kPrep>(smem, int(blockIdx.x), int(gridDim.x), out, q, pool, num_pages, table,
+                                                 query_start, T, num_kv_heads, n_qb, nsplit, scale_log2, ws, ap, px, pp);
+}
+
 typedef void (*WideKernel)(f16*, const f16*, const f16*, int64_t, const int32_t*, int32_t, int32_t, int32_t, int32_t,
                            int32_t, float, PrefillWorkspace, PrefillAppend, PrefixOut, PrefillPrep);
 
@@ -1058,6 +1070,159 @@ int wide_prefix_pass(const f16* q, const f16* pool, int64_t num_pages, const int
       nullptr, q, pool, num_pages, prefix_pages, 0, batch, hkv, int(p.n_qb), p.nsplit, scale_log2,
       PrefillWorkspace{nullptr, nullptr, nullptr}, PrefillAppend{nullptr, nullptr, nullptr},
       PrefixOut{px_ml, px_o, key_len, stride, px_oh}, PrefillPrep{});
+  return ifn_launch_status();
+}
+
+
+// ---- shared-prefix decode in one launch ------------------------------------------------------
+// Rows that begin with the same prefix pages (a cascade row: at least px.pages pages long) are
+// decoded by one grid of two kinds of workgroup, one per CU:
+//  * workgroups [0, npre): the prefix pass -- prefill_wide_body in prefix mode over the prefix keys
+//    (32 query rows of one kv head and one key split per workgroup), which leaves a state per
+//    (row, kv head, head of the group, split) at the device coherence point;
+//  * workgroups [npre, npre + ndec): the whole-row decode of the rows' own keys (decode_rows_body,
+//    kFused: a cascade row's states are always published).
+// Each (cascade row, kv head) has one ticket, counting the decode ranges that hold the row's keys
+// and the prefix workgroups (one per key split) that hold its query rows.  Whichever arrives last -- either kind --
+// merges the row's heads of that kv head (its split states in range order, then its prefix states:
+// the same arithmetic either way) and writes them.  No workgroup waits for another, so the two kinds run side by side: the prefix pass's MFMA
+// work on its CUs while the others stream the private pages.  Shorter rows are decoded as usual.
+template <int D, int G, int HKV>
+struct FusedLayout {  // the decode role's LDS arrays, laid over the prefix role's tile buffers
+  using L = RowsLds<D, G, HKV, false, true, 2 * HKV>;
+  static constexpr size_t kAcc = 0;
+  static constexpr size_t kM = kAcc + sizeof(f32x4) * kRowsWaves * HKV * L::GR * (D / 4);
+  static constexpr size_t kL = kM + sizeof(float) * kRowsWaves * L::HQ;
+  static constexpr size_t kApp = (kL + sizeof(float) * kRowsWaves * L::HQ + 15) / 16 * 16;
+  static constexpr size_t kQ = kApp + 16;
+  static constexpr size_t kWsum = kQ + 16;
+  static constexpr size_t kTicket = kWsum + sizeof(int) * kRowsWaves;
+  static constexpr size_t kCum = kTicket + 2 * HKV * sizeof(uint32_t);
+  static constexpr size_t kCasc = kCum + sizeof(int) * (kRowsMaxBatch + 1);
+  static constexpr size_t kBytes = kCasc + kRowsMaxBatch;
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(8 * kWave) void shared_prefix_fused_kernel(
+    const f16* __restrict__ pool, const int32_t* __restrict__ block_tables, const f16* __restrict__ q, int32_t batch,
+    int32_t max_pages, int32_t max_len, int32_t ndec, int64_t num_pages, f16* __restrict__ out,
+    const int32_t* __restrict__ seq_lens, const uint8_t* __restrict__ active, float scale_log2, DecodeWorkspace ws,
+    DecodePrefix px, const int32_t* __restrict__ prefix_pages, int32_t n_qb, int32_t nsplit, int32_t npre) {
+  constexpr int HKV = 8;
+  using C = WideCfg<D, G, 1, 8>;
+  using FL = FusedLayout<D, G, HKV>;
+  using L = typename FL::L;
+  static_assert(C::kThreads == kRowsThreads, "both roles run 8 waves");
+  constexpr size_t kBytes = C::kLdsBytes > FL::kBytes ? C::kLdsBytes : FL::kBytes;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[kBytes];
+  const int bid = int(blockIdx.x), tid = int(threadIdx.x);
+  const int pk = px.pages * kRowsBlock;  // prefix keys
+  const int cap = min(max_pages * kRowsBlock, max_len);
+
+  if (bid >= npre) {  // the private pages
+    L sh{*reinterpret_cast<int(*)[kRowsMaxBatch + 1]>(smem + FL::kCum),
+         *reinterpret_cast<int(*)[kRowsWaves]>(smem + FL::kWsum),
+         *reinterpret_cast<float(*)[kRowsWaves][L::HQ]>(smem + FL::kM),
+         *reinterpret_cast<float(*)[kRowsWaves][L::HQ]>(smem + FL::kL),
+         *reinterpret_cast<f32x4(*)[kRowsWaves][HKV * L::GR][D / 4]>(smem + FL::kAcc),
+         *reinterpret_cast<uint32_t(*)[2 * HKV]>(smem + FL::kTicket),
+         *reinterpret_cast<uint8_t(*)[kRowsMaxBatch]>(smem + FL::kCasc),
+         *reinterpret_cast<f16(*)[1][8]>(smem + FL::kApp),
+         *reinterpret_cast<f16(*)[1][8]>(smem + FL::kQ)};
+    decode_rows_body<D, G, HKV, kRowsStages, false, true, false, true, kRowsBlock, true>(
+        sh, bid - npre, nullptr, pool, block_tables, q, batch, max_pages, max_len, ndec, num_pages, out, seq_lens,
+        active, scale_log2, ws, DecodeAppend{nullptr, nullptr, nullptr, nullptr}, DecodePrep{}, px);
+    return;
+  }
+
+  // The prefix pass for (query block qb, kv head bid % Hkv, key split): its states, stored at the
+  // device coherence point.
+  prefill_wide_body<D, G, 1, 8, false, false>(
+      smem, bid, npre, out, q, pool, num_pages, prefix_pages, 0, batch, HKV, n_qb, nsplit, scale_log2,
+      PrefillWorkspace{nullptr, nullptr, nullptr}, PrefillAppend{nullptr, nullptr, nullptr},
+      PrefixOut{px.ml, px.o, pk, px.nstates, const_cast<f16*>(px.oh)}, PrefillPrep{});
+  wait_all_mem();   // this wave's state stores acknowledged
+  __syncthreads();  // ... and every other wave's; the tile buffers are free
+  // The decode role's split of the rows' own keys (the same offsets and ranges), to find where a
+  // cascade row's split states sit.
+  int* s_cum = reinterpret_cast<int*>(smem);
+  int* s_wsum = s_cum + kRowsMaxBatch + 1;
+  int* s_rec = s_wsum + kRowsWaves;  // per query row of the block: (first range, ranges) if last, else -1
+  const int T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap, pk);
+  const int64_t nr = range_count(ndec, T);
+  constexpr int kQw = C::kQw;  // batch rows per query block
+  const int q0 = (n_qb - 1 - bid / (HKV * nsplit)) * kQw;
+  const int kvh = bid % HKV;
+  const int npx = px.nstates - 1;  // prefix states per (row, head): nsplit
+  if (tid < kQw) {
+    const int b = q0 + tid;
+    int first = -1, nrg = 0;
+    if (b < batch && row_keys(seq_lens, active, b, cap) >= pk) {
+      const int cb = s_cum[b] + kRowStartCost, len = s_cum[b + 1] - cb;
+      int f = 0;
+      if (len > 0) {  // (T >= len > 0)
+        f = int(div_floor((int64_t(cb) + 1) * nr - 1, T));
+        nrg = int(div_floor((int64_t(cb) + len) * nr - 1, T)) - f + 1;
+      }
+      const uint32_t t = __hip_atomic_fetch_add(fused_ticket(ws.count, batch, HKV, b, kvh), 1u, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+      if (t == uint32_t(nrg + npx - 1)) first = f;
+    }
+    s_rec[2 * tid] = first;
+    s_rec[2 * tid + 1] = nrg;
+  }
+  __syncthreads();
+  compiler_fence();  // the merge loads below stay behind the tickets
+  const uint32_t n_slots = uint32_t(batch) + uint32_t(ndec);
+  const RowsMerge<D, G, HKV, true, kFusedMergeBatch> mg{make_rsrc(ws.o, n_slots * L::HQ * D * 2u),
+                                      make_rsrc(ws.ml, n_slots * L::HQ * 2u * 4u), px, out};
+  // the block's rows this workgroup arrived last at: heads kvh * G .. kvh * G + G - 1 of each
+  constexpr int D4 = D / 4;
+  for (int idx = tid; idx < kQw * G * D4; idx += kRowsThreads) {
+    const int j = idx / (G * D4), rem = idx % (G * D4);
+    const int first = s_rec[2 * j];
+    if (first < 0) continue;
+    const int64_t b = q0 + j;
+    mg.item(b, b + first, s_rec[2 * j + 1], true, kvh * G + rem / D4, rem % D4);
+  }
+  if (tid < kQw && s_rec[2 * tid] >= 0) reset_ticket(fused_ticket(ws.count, batch, HKV, q0 + tid, kvh));
+}
+
+int shared_prefix_fused_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* prefix_pages,
+                               const int32_t* block_tables, int32_t max_pages, const int32_t* seq_lens,
+                               const uint8_t* active, int32_t batch, int32_t hq, int32_t hkv, int32_t d,
+                               int32_t max_len, float scale_log2, void* workspace, int blocks, const DecodePrefix& px,
+                               int max_states, int cus, hipStream_t stream) {
+  // Built for head dim 128, 8 kv heads and groups 2 and 4 (Qwen3-0.6B, Qwen3-8B).  The prefix pass
+  // takes npre = ceil(batch / (32 / G)) x 8 x nsplit workgroups: two key splits while that is at most
+  // half the CUs, else one while it is at most a quarter; the rest of the CUs decode the private
+  // pages.  (Config 5, 36 layers: 128 + 128 workgroups measured 47.5 us, 64 + 192 52.3 us -- the
+  // prefix pass reads HBM under the decode's stream, and its workgroups' key loops are latency
+  // bound; when the prefixes stay in the last-level cache, as with a few layers, 64 + 192 is the
+  // faster, 42.3 against 45.6 us.)  Prefixes of at most 8192 keys (a prefix workgroup's share grows
+  // with the prefix); otherwise the two launches.
+  if (d != 128 || hkv != 8 || (hq != 16 && hq != 32) || px.pages < 1) return IFN_ERR_UNSUPPORTED;
+  const int g = hq / hkv;
+  const int64_t n_qb = (int64_t(batch) + 32 / g - 1) / (32 / g);
+  const int64_t key_len = int64_t(px.pages) * kRowsBlock;
+  const int nsplit = 2 * (n_qb * hkv * 2) <= cus && max_states >= 3 ? 2 : 1;
+  const int64_t npre = n_qb * hkv * nsplit;
+  const int64_t ndec = (int64_t(cus) - npre) / kRowsXcds * kRowsXcds;
+  if (nsplit + 1 > max_states || (nsplit == 1 && 4 * npre > cus) || ndec < kRowsXcds || ndec > blocks ||
+      key_len > 8192 || int64_t(batch) * (hkv + 1) > kMaxTickets)  // (a ticket per row, then per (cascade row, kv head))
+    return IFN_ERR_UNSUPPORTED;
+  uint8_t* wsb = static_cast<uint8_t*>(workspace);
+  size_t off_ml, off_o;
+  rows_ws_layout(batch, hq, d, blocks, &off_ml, &off_o);
+  DecodeWorkspace ws;
+  ws.count = reinterpret_cast<uint32_t*>(wsb);
+  ws.ml = reinterpret_cast<float*>(wsb + off_ml);
+  ws.o = reinterpret_cast<float*>(wsb + off_o);
+  const DecodePrefix pxf{px.ml, px.o, px.pages, nsplit + 1, px.oh};
+  auto k = g == 4 ? shared_prefix_fused_kernel<128, 4> : shared_prefix_fused_kernel<128, 2>;
+  k<<<dim3(unsigned(npre + ndec)), dim3(kRowsThreads), 0, stream>>>(
+      pool, block_tables, q, batch, max_pages, max_len, int32_t(ndec), num_pages, out, seq_lens, active, scale_log2,
+      ws, pxf, prefix_pages, int32_t(n_qb), nsplit, int32_t(npre));
   return ifn_launch_status();
 }
 
