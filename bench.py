@@ -3,16 +3,19 @@
 
 Workload (config 2): Qwen3-0.6B ragged batched decode over all 28 layers, fp16,
 batch 32, context lengths U[128, 4096], 16-token pages in a 16384-page pool per
-layer.  One step = the step plan (one launch: the split of the batch's keys over
-the CUs, shared by all layers), then for each of the 28 layers store_kv (one new
-token per sequence) and paged decode attention, launched back to back on one
-stream through the C ABI (no Python validation inside the timed region).
+layer.  One step = for each of the 28 layers store_kv (one new token per sequence)
+and paged decode attention, launched back to back on one stream through the C ABI
+(no Python validation inside the timed region).  Layer 0's decode also writes the
+step plan (the split of the batch's keys over the CUs, which every layer shares;
+ifn_paged_decode_planning) and layers 1-27 read it (ifn_paged_decode_planned).
 
 Reported:
-  value            paged-decode attention HBM GB/s = algorithmic decode bytes /
-                   (decode kernel time + the step plan's time / 28), summed over
-                   the K timed steps; the times come from HIP events recorded on the
-                   launch stream around every launch
+  value            paged-decode attention HBM GB/s = algorithmic decode bytes / mean
+                   decode kernel time over the 28 layers of the K timed steps; the
+                   times come from HIP events recorded on the launch stream around
+                   every launch
+  plan_kernel_step the same step with the plan as a launch of its own first
+                   (ifn_paged_decode_plan), for comparison
   kv_append_us_per_layer   the same events around every store_kv launch
   roofline         the decode kernel against 8 TB/s HBM (its own launches); traffic
                    (HBM bytes per launch from rocprofv3 FETCH_SIZE/WRITE_SIZE) is read
@@ -646,10 +649,19 @@ def run_config1(lib, hip, dev, stream, reps: int = 200) -> dict:
                                                    16, 8, 128, 16, 512, scale, plan.data_ptr(), plan_bytes,
                                                    ws.data_ptr(), ws_bytes, stream)
 
+    plan2 = torch.zeros(plan_bytes, dtype=torch.uint8, device=dev)
+
+    def fused_planning():  # the step's first layer: decodes unplanned and writes the plan
+        return lib.ifn_paged_decode_append_planning(out.data_ptr(), q.data_ptr(), pool.data_ptr(), P, bt.data_ptr(),
+                                                    32, sl.data_ptr(), None, slots.data_ptr(), k.data_ptr(),
+                                                    v.data_ptr(), 1, 16, 8, 128, 16, 512, scale, plan2.data_ptr(),
+                                                    plan_bytes, ws.data_ptr(), ws_bytes, stream)
+
     if mkplan():
         raise RuntimeError("config 1: plan launch failed")
     res = {"workload": "config 1: B=1, context 512, 64-page pool, one layer (append at 511 + decode)"}
-    for name, fn in (("two_launch", two), ("fused", fused), ("fused_planned", fused_planned), ("plan", mkplan)):
+    for name, fn in (("two_launch", two), ("fused", fused), ("fused_planned", fused_planned), ("plan", mkplan),
+                     ("fused_planning", fused_planning)):
         for _ in range(10):
             fn()
         torch.cuda.synchronize()
@@ -667,8 +679,10 @@ def run_config1(lib, hip, dev, stream, reps: int = 200) -> dict:
                                                    for r in range(reps)])) * 1e3, 2)
         res[f"{name}_host_us_per_call"] = round(wall_us, 2)  # launch rate through ctypes, back to back
         hip.destroy(evs)
-    # a 28-layer step of the planned fused form: one plan, then 28 launches
+    # a 28-layer step of the planned fused form: one plan, then 28 launches; or the first layer writing the
+    # plan and 27 planned
     res["fused_planned_us_per_layer_with_plan"] = round(res["fused_planned_us"] + res["plan_us"] / 28, 2)
+    res["fused_step_us_per_layer"] = round((res["fused_planning_us"] + 27 * res["fused_planned_us"]) / 28, 2)
     return res
 
 
@@ -858,25 +872,19 @@ def main() -> int:
                  w.max_pages, sl.data_ptr(), None, B, hq, hkv, d, 16, max_len, scale, plan.data_ptr(), plan_bytes,
                  ws.data_ptr(), ws_bytes, stream) for i in range(L)]
     plan_fn, store_fn, dec_fn = lib.ifn_paged_decode_plan, lib.ifn_store_kv, lib.ifn_paged_decode_planned
+    planning_fn = lib.ifn_paged_decode_planning  # layer 0: decodes unplanned and writes the step's plan
     hip = HipEvents()
-    E = 2 + 3 * L  # events per step: the plan, then store_kv and decode per layer
+    E = 3 * L  # events per step: store_kv and decode per layer
 
     def step(evs=None, base=0):
-        if evs is not None:
-            hip.hip.hipEventRecord(evs[base], stream)
-        rc = plan_fn(*plan_args)
-        if evs is not None:
-            hip.hip.hipEventRecord(evs[base + 1], stream)
-        if rc:
-            raise RuntimeError(f"plan launch failed: {_capi.status_string(rc)}")
         for i in range(L):
-            b = base + 2 + 3 * i
+            b = base + 3 * i
             if evs is not None:
                 hip.hip.hipEventRecord(evs[b], stream)
             rc = store_fn(*store_args[i])
             if evs is not None:
                 hip.hip.hipEventRecord(evs[b + 1], stream)
-            rc |= dec_fn(*dec_args[i])
+            rc |= (planning_fn if i == 0 else dec_fn)(*dec_args[i])
             if evs is not None:
                 hip.hip.hipEventRecord(evs[b + 2], stream)
             if rc:
@@ -893,13 +901,41 @@ def main() -> int:
         step(evs, E * s_)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    plan_ms = [hip.elapsed_ms(evs[E * s_], evs[E * s_ + 1]) for s_ in range(K)]
-    dec_ms = [hip.elapsed_ms(evs[E * s_ + 2 + 3 * i + 1], evs[E * s_ + 2 + 3 * i + 2]) for s_ in range(K)
-              for i in range(L)]
-    app_ms = [hip.elapsed_ms(evs[E * s_ + 2 + 3 * i], evs[E * s_ + 2 + 3 * i + 1]) for s_ in range(K)
-              for i in range(L)]
+    dec_ms = [hip.elapsed_ms(evs[E * s_ + 3 * i + 1], evs[E * s_ + 3 * i + 2]) for s_ in range(K) for i in range(L)]
+    app_ms = [hip.elapsed_ms(evs[E * s_ + 3 * i], evs[E * s_ + 3 * i + 1]) for s_ in range(K) for i in range(L)]
     hip.destroy(evs)
     print(f"[bench] timed {K} steps x {L} layers in {wall:.3f} s", file=sys.stderr, flush=True)
+
+    # The same step with the plan as its own launch (ifn_paged_decode_plan, then 28 planned decodes), for
+    # comparison: the plan launch's time, and the planned layers'.
+    PE = 2 + 2 * L
+
+    def plan_step(evs=None, base=0):
+        if evs is not None:
+            hip.hip.hipEventRecord(evs[base], stream)
+        rc = plan_fn(*plan_args)
+        if evs is not None:
+            hip.hip.hipEventRecord(evs[base + 1], stream)
+        for i in range(L):
+            rc |= store_fn(*store_args[i])
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 2 + 2 * i], stream)
+            rc |= dec_fn(*dec_args[i])
+            if evs is not None:
+                hip.hip.hipEventRecord(evs[base + 3 + 2 * i], stream)
+            if rc:
+                raise RuntimeError(f"launch failed in layer {i}: {_capi.status_string(rc)}")
+
+    plan_step()
+    torch.cuda.synchronize()
+    pevs = hip.create(PE * K)
+    for s_ in range(K):
+        plan_step(pevs, PE * s_)
+    torch.cuda.synchronize()
+    plan_ms = [hip.elapsed_ms(pevs[PE * s_], pevs[PE * s_ + 1]) for s_ in range(K)]
+    planned_ms = [hip.elapsed_ms(pevs[PE * s_ + 2 + 2 * i], pevs[PE * s_ + 3 + 2 * i]) for s_ in range(K)
+                  for i in range(L)]
+    hip.destroy(pevs)
 
     # The same decode launches without a plan (each launch splits the batch itself), for comparison.
     unplanned_args = [a[:15] + a[17:] for a in dec_args]
@@ -921,21 +957,17 @@ def main() -> int:
                    w.max_pages, sl.data_ptr(), None, slots.data_ptr(), nk[i].data_ptr(), nv[i].data_ptr(), B, hq,
                    hkv, d, 16, max_len, scale, plan.data_ptr(), plan_bytes, ws.data_ptr(), ws_bytes, stream)
                   for i in range(L)]
-    fused_fn = lib.ifn_paged_decode_append_planned
-    EF = 2 + 2 * L
+    fused_fn, fused_planning_fn = lib.ifn_paged_decode_append_planned, lib.ifn_paged_decode_append_planning
+    EF = 2 * L
 
     def fused_step(evs=None, base=0):
-        if evs is not None:
-            hip.hip.hipEventRecord(evs[base], stream)
-        rc = plan_fn(*plan_args)
-        if evs is not None:
-            hip.hip.hipEventRecord(evs[base + 1], stream)
+        rc = 0
         for i in range(L):
             if evs is not None:
-                hip.hip.hipEventRecord(evs[base + 2 + 2 * i], stream)
-            rc |= fused_fn(*fused_args[i])
+                hip.hip.hipEventRecord(evs[base + 2 * i], stream)
+            rc |= (fused_planning_fn if i == 0 else fused_fn)(*fused_args[i])
             if evs is not None:
-                hip.hip.hipEventRecord(evs[base + 3 + 2 * i], stream)
+                hip.hip.hipEventRecord(evs[base + 1 + 2 * i], stream)
             if rc:
                 raise RuntimeError(f"fused launch failed in layer {i}: {_capi.status_string(rc)}")
 
@@ -948,15 +980,15 @@ def main() -> int:
         fused_step(fevs, EF * s_)
     torch.cuda.synchronize()
     fused_wall = time.perf_counter() - t0
-    fused_ms = [hip.elapsed_ms(fevs[EF * s_ + 2 + 2 * i], fevs[EF * s_ + 3 + 2 * i]) for s_ in range(K)
-                for i in range(L)]
+    fused_ms = [hip.elapsed_ms(fevs[EF * s_ + 2 * i], fevs[EF * s_ + 1 + 2 * i]) for s_ in range(K) for i in range(L)]
     hip.destroy(fevs)
     prep_step = run_prep_step(lib, hip, dev, g, stream, w, pool, plan, plan_bytes, ws, ws_bytes, steps=4)
 
     dec_bytes = w.decode_bytes()
-    dec_s = float(np.mean(dec_ms)) / 1e3            # the decode kernel, per launch
-    plan_s = float(np.mean(plan_ms)) / 1e3          # the step plan, once per step
-    layer_s = dec_s + plan_s / L                    # a layer's share of the step's decode work
+    dec_s = float(np.mean(dec_ms)) / 1e3            # the decode kernel, per launch (layer 0 writes the plan)
+    plan_s = float(np.mean(plan_ms)) / 1e3          # the plan as its own launch, once per step (comparison)
+    planned_s = float(np.mean(planned_ms)) / 1e3    # a planned layer after that plan launch (comparison)
+    layer_s = dec_s                                 # the step has no other decode work
     gbps = dec_bytes / layer_s / 1e9
     kernel_gbps = dec_bytes / dec_s / 1e9
     traffic = None
@@ -1053,13 +1085,16 @@ def main() -> int:
                    "pages_per_layer": P, "context_tokens": int(w.seq_lens.sum()), "layers": L, "seed": w.seed},
         "decode_frac_of_peak": round(gbps / HBM_PEAK_GBPS, 4),
         "decode_us_per_layer": round(dec_s * 1e6, 3),
-        "plan_us_per_step": round(plan_s * 1e6, 3),
+        "planning_layer_us": round(float(np.mean(dec_ms[::L])) * 1e3, 3),
+        "plan_kernel_step": {"plan_us_per_step": round(plan_s * 1e6, 3),
+                             "planned_decode_us_per_layer": round(planned_s * 1e6, 3),
+                             "us_per_layer_with_plan": round((planned_s + plan_s / L) * 1e6, 3)},
         "decode_kernel_GB/s": round(kernel_gbps, 2),
         "unplanned_decode_us_per_layer": round(unplanned_us, 3),
         "decode_bytes_per_layer": dec_bytes,
         "kv_append_us_per_layer": round(float(np.mean(app_ms)) * 1e3, 3),
-        "fused_step": {"entry": "ifn_paged_decode_append_planned (store_kv + paged decode in one launch per "
-                                "layer, after the step plan)",
+        "fused_step": {"entry": "ifn_paged_decode_append_planning (layer 0: writes the step plan), then "
+                                "ifn_paged_decode_append_planned (store_kv + paged decode in one launch per layer)",
                        "us_per_layer": round(float(np.mean(fused_ms)) * 1e3, 3),
                        "two_launch_us_per_layer": round((float(np.mean(app_ms)) + float(np.mean(dec_ms))) * 1e3, 3),
                        # what the append adds to a decode launch when fused into it

@@ -206,6 +206,47 @@ int ifn_paged_decode_append_planned(void* out, const void* query, void* kv_pool_
                                     size_t workspace_bytes, void* stream);
 
 /*
+ * The first layer's decode of a step, building the step's plan as it goes:
+ * the same arguments as the *_planned calls above (and as
+ * ifn_paged_decode_prep_append below), but `plan` is written, not read.  The
+ * call decodes as the unplanned one does (bit-identical output) and leaves in
+ * `plan` exactly the words ifn_paged_decode_plan would write for its inputs
+ * (with slot_mapping for the append and pre-append forms, without for the plain
+ * one), so the step's later layers run planned with no separate plan launch.
+ * plan_bytes as ifn_paged_decode_plan_bytes; shapes that decode without a plan
+ * (plan_bytes == 0) ignore `plan` and write nothing.  Later calls must be
+ * ordered after this one (the same stream, or an event).
+ * Replaces: as the unplanned calls (paged_attention's decode,
+ * docs/architecture.md:245-246); it folds ifn_paged_decode_plan, which has no
+ * reference counterpart, into the step's first launch.
+ */
+int ifn_paged_decode_planning(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                              const int32_t* block_tables, int32_t max_pages_per_seq,
+                              const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                              int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                              int32_t block_size, int32_t max_seq_len, float scale, void* plan,
+                              size_t plan_bytes, void* workspace, size_t workspace_bytes, void* stream);
+int ifn_paged_decode_append_planning(void* out, const void* query, void* kv_pool_layer, int64_t num_pages,
+                                     const int32_t* block_tables, int32_t max_pages_per_seq,
+                                     const int32_t* seq_lens, const uint8_t* active_mask,
+                                     const int32_t* slot_mapping, const void* new_k, const void* new_v,
+                                     int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                     int32_t head_dim, int32_t block_size, int32_t max_seq_len, float scale,
+                                     void* plan, size_t plan_bytes, void* workspace,
+                                     size_t workspace_bytes, void* stream);
+int ifn_paged_decode_prep_append_planning(void* out, const float* q, const float* k, const float* v,
+                                          const float* q_norm_weight, const float* k_norm_weight,
+                                          const float* rope_table, int32_t max_positions,
+                                          const int32_t* positions, const int32_t* slot_mapping,
+                                          void* kv_pool_layer, int64_t num_pages, const int32_t* block_tables,
+                                          int32_t max_pages_per_seq, const int32_t* seq_lens,
+                                          const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
+                                          int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                          int32_t max_seq_len, float scale, float eps, void* plan,
+                                          size_t plan_bytes, void* workspace, size_t workspace_bytes,
+                                          void* stream);
+
+/*
  * ifn_paged_decode without a workspace argument: for callers that cannot
  * allocate device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  It allocates nothing: the split-KV

@@ -46,6 +46,11 @@ SIGNATURES: dict[str, tuple] = {
                                                 _i32, _f32, _p, _sz, _p, _sz, _p]),
     "ifn_paged_decode_append_planned": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _p, _p, _p, _p, _i32, _i32,
                                                        _i32, _i32, _i32, _i32, _f32, _p, _sz, _p, _sz, _p]),
+    # the first layer's decode of a step, writing the step's plan (same arguments as the planned calls)
+    "ifn_paged_decode_planning": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _p, _i32, _i32, _i32, _i32, _i32,
+                                                 _i32, _f32, _p, _sz, _p, _sz, _p]),
+    "ifn_paged_decode_append_planning": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _p, _p, _p, _p, _i32, _i32,
+                                                        _i32, _i32, _i32, _i32, _f32, _p, _sz, _p, _sz, _p]),
     "ifn_paged_decode_noalloc_max_bytes": (_sz, []),
     "ifn_paged_decode_noalloc": (ctypes.c_int, [_p, _p, _p, _i64, _p, _i32, _p, _p, _i32, _i32, _i32, _i32,
                                                 _i32, _i32, _f32, _p]),
@@ -69,6 +74,9 @@ SIGNATURES: dict[str, tuple] = {
     "ifn_paged_decode_prep_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i64, _p, _i32,
                                                     _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32, _f32, _p,
                                                     _sz, _p, _sz, _p]),
+    "ifn_paged_decode_prep_append_planning": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _p, _p, _i64, _p,
+                                                             _i32, _p, _p, _i32, _i32, _i32, _i32, _i32, _i32, _f32,
+                                                             _f32, _p, _sz, _p, _sz, _p]),
     # out, q, k, v, q_norm_weight, k_norm_weight, rope_table, max_positions, pool, num_pages, block_table,
     # max_pages, query_start, T, hq, hkv, head_dim, block_size, eps, scale, workspace, bytes, stream
     "ifn_paged_prefill_prep_append": (ctypes.c_int, [_p, _p, _p, _p, _p, _p, _p, _i32, _p, _i64, _p, _i32, _i32,

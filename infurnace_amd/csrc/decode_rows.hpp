@@ -742,6 +742,24 @@ __device__ __forceinline__ void decode_rows_body(
   // Planned: they go to LDS at the first merge barrier, for pieces the record does not describe.
   if (!planned) T = build_offsets(s_cum, s_wsum, seq_lens, active, batch, cap, pk, kCascade ? s_casc : nullptr);
   bool have_cum = !planned;
+  // ws.plan_out (an unplanned call that builds the step's plan for the later layers): the same words
+  // decode_plan_kernel writes -- workgroup 0 the header and the offsets, each workgroup its range's
+  // record as it finds its pieces.
+  int32_t* const pout = kFused || planned ? nullptr : ws.plan_out;
+  int32_t* const prec = pout != nullptr ? pout + plan_rec0(batch) + blk * kPlanRec : nullptr;
+  if (pout != nullptr && bid == 0) {
+    if (tid == 0) {
+      pout[0] = kPlanMagic;
+      pout[1] = batch;
+      pout[2] = int(range_count(nb, T));
+      pout[3] = int(T);
+      pout[4] = int(nb);
+      pout[5] = kApp ? 1 : 0;
+      pout[6] = cap;
+      pout[7] = pk;
+    }
+    for (int i = tid; i <= batch; i += kRowsThreads) pout[kPlanHdr + i] = s_cum[i];
+  }
   auto ensure_cum = [&]() __attribute__((always_inline)) {  // planned: s_cum valid after the next barrier
     if (!have_cum) {
       if (tid <= batch) s_cum[tid] = cum_pf;
@@ -754,6 +772,7 @@ __device__ __forceinline__ void decode_rows_body(
   // range may still hold no key (only virtual positions); it then has no piece and takes no ticket.
   const int64_t nr = range_count(nb, T);
   if (blk >= nr) {
+    if (prec != nullptr && tid <= kPlanIds) prec[tid == kPlanIds ? 0 : kPlanIds + tid] = 0;  // no piece
     finish();
     return;
   }
@@ -823,6 +842,7 @@ __device__ __forceinline__ void decode_rows_body(
   const int d4i = tid % D4;
 
   int prev = -1;
+  int npieces = 0;
   for (int pi = 0;; ++pi) {  // one piece (row segment) per iteration; uniform over the workgroup
     if (planned && pi >= rec_n) break;
     const bool from_plan = planned && pi < kPlanPieces;
@@ -830,6 +850,12 @@ __device__ __forceinline__ void decode_rows_body(
     if (P.b >= batch) break;
     const int b = P.b, a = P.a, e = P.e, slot_b = P.slot;
     prev = b;
+    npieces = pi + 1;
+    if (prec != nullptr && pi < kPlanPieces && tid < 6) {  // the piece's record (keys before the prefix offset)
+      const int w = tid == 0 ? b : tid == 1 ? a - P.off : tid == 2 ? e - P.off : tid == 3 ? P.first
+                  : tid == 4 ? P.nranges : (kApp ? slot_b : P.off);
+      prec[1 + 6 * pi + tid] = w;
+    }
 
     // Query rows (b, hd * G + g), chunks col and col + LPH; the piece's page ids, one per lane.
     f16x8 qv[G][2];
@@ -900,6 +926,7 @@ __device__ __forceinline__ void decode_rows_body(
     const int32_t* bt = block_tables + int64_t(b) * max_pages + pg0;
     int ids0 = pi == 0 && from_plan ? ids_pl : bt[min(lane, npg - 1)];
     int ids1 = bt[min(lane + kWave, npg - 1)];
+    if (prec != nullptr && pi == 0 && wave == 0) prec[kPlanIds + lane] = ids0;  // the first window's page ids
     int cur_w = 0;
 
     // this wave's tokens: positions a + wave + 8 i, i < nw
@@ -1144,6 +1171,10 @@ __device__ __forceinline__ void decode_rows_body(
     }
   }
 
+  if (prec != nullptr) {
+    if (tid == 0) prec[0] = npieces;
+    if (npieces == 0 && tid < kPlanIds) prec[kPlanIds + tid] = 0;  // (only virtual positions)
+  }
   if (!kFused && pend_n > 0) {
     // Tickets for the range's split rows: every partial store of the workgroup acknowledged first.
     wait_all_mem();

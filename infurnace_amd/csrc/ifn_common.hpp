@@ -193,6 +193,7 @@ struct DecodeWorkspace {
   uint32_t* count;  // one ticket per segment; every call returns the tickets it used to zero
   float* ml;        // [slot][heads][2]
   float* o;         // [slot][heads][head_dim]: fp32 O (per-segment kernel) or fp16 O / l (whole-row kernel)
+  int32_t* plan_out = nullptr;  // whole-row kernel, unplanned: where to write the step's plan (or null)
 };
 
 // Shared-prefix (cascade) mode: the first `pages` pages of every row at least pages * block_size
@@ -421,11 +422,14 @@ int rows_plan_launch(int32_t* plan, const int32_t* block_tables, int32_t max_pag
                      int blocks, hipStream_t stream, int32_t block_size = 16, int32_t prefix_keys = 0);
 // prep (non-null): the fused pre-append variant; ap then carries the slots and the pool, and q is unused.
 // px (non-null): shared-prefix mode (DecodePrefix), without append (plan: one built for px.pages).
+// plan_out (non-null, with plan null): the call also writes the step's plan there, as
+// rows_plan_launch would.
 int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_pages, const int32_t* block_tables,
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
                        const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
-                       const DecodePrep* prep = nullptr, const DecodePrefix* px = nullptr, int32_t block_size = 16);
+                       const DecodePrep* prep = nullptr, const DecodePrefix* px = nullptr, int32_t block_size = 16,
+                       int32_t* plan_out = nullptr);
 bool rows_prep_supported(int32_t hq, int32_t hkv, int32_t d);
 // The shared-prefix decode as one launch (prefix pass and private-page decode in one grid), for the
 // shapes and sizes it is built for; IFN_ERR_UNSUPPORTED otherwise (the caller then runs the two

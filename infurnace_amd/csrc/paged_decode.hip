@@ -754,7 +754,8 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
                         const uint8_t* active_mask, int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
                         int32_t head_dim, int32_t block_size, int32_t max_seq_len, float scale, void* workspace,
                         size_t workspace_bytes, void* stream, const DecodeAppend& ap, bool cached = false,
-                        const void* plan = nullptr, size_t plan_bytes = 0, const DecodePrep* prep = nullptr) {
+                        const void* plan = nullptr, size_t plan_bytes = 0, const DecodePrep* prep = nullptr,
+                        bool build_plan = false) {
   const bool append = ap.pool != nullptr;
   if (out == nullptr || query == nullptr || kv_pool_layer == nullptr || block_tables == nullptr ||
       seq_lens == nullptr)
@@ -793,15 +794,20 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
   if (device_cu_count() < 1) return IFN_ERR_HIP;
   if (scale <= 0.f) scale = 1.0f / sqrtf(float(head_dim));
   if (rows) {
-    if (plan != nullptr) {  // the kernel reads this workgroup's record before checking the header
+    // planned: the kernel reads this workgroup's record before checking the header; build_plan: every
+    // workgroup writes its record
+    if (build_plan && plan == nullptr) return IFN_ERR_INVALID_ARGUMENT;
+    if (plan != nullptr) {
       if (plan_bytes < rows_plan_bytes(batch, blocks)) return IFN_ERR_WORKSPACE;
       IFN_CHECK_ALIGN16(plan);
     }
     return rows_decode_launch(static_cast<f16*>(out), static_cast<const f16*>(query),
                               static_cast<const f16*>(kv_pool_layer), num_pages, block_tables, max_pages_per_seq,
                               seq_lens, active_mask, batch, num_q_heads, num_kv_heads, head_dim, max_seq_len,
-                              scale * kLog2e, workspace, blocks, ap, cached, static_cast<const int32_t*>(plan),
-                              reinterpret_cast<hipStream_t>(stream), prep, nullptr, block_size);
+                              scale * kLog2e, workspace, blocks, ap, cached,
+                              build_plan ? nullptr : static_cast<const int32_t*>(plan),
+                              reinterpret_cast<hipStream_t>(stream), prep, nullptr, block_size,
+                              build_plan ? static_cast<int32_t*>(const_cast<void*>(plan)) : nullptr);
   }
   size_t off_ml, off_o;
   decode_ws_layout(batch, num_kv_heads, num_q_heads / num_kv_heads, head_dim, int64_t(blocks) * kWavesPerBlock,
@@ -912,18 +918,45 @@ extern "C" int ifn_paged_decode_append_planned(void* out, const void* query, voi
                            false, plan, plan_bytes);
 }
 
-extern "C" int ifn_paged_decode_prep_append(void* out, const float* q, const float* k, const float* v,
-                                            const float* q_norm_weight, const float* k_norm_weight,
-                                            const float* rope_table, int32_t max_positions,
-                                            const int32_t* positions, const int32_t* slot_mapping,
-                                            void* kv_pool_layer, int64_t num_pages, const int32_t* block_tables,
-                                            int32_t max_pages_per_seq, const int32_t* seq_lens,
-                                            const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
-                                            int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
-                                            int32_t max_seq_len, float scale, float eps, const void* plan,
-                                            size_t plan_bytes, void* workspace, size_t workspace_bytes,
-                                            void* stream) {
-  using namespace ifn;
+extern "C" int ifn_paged_decode_planning(void* out, const void* query, const void* kv_pool_layer, int64_t num_pages,
+                                         const int32_t* block_tables, int32_t max_pages_per_seq,
+                                         const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch,
+                                         int32_t num_q_heads, int32_t num_kv_heads, int32_t head_dim,
+                                         int32_t block_size, int32_t max_seq_len, float scale, void* plan,
+                                         size_t plan_bytes, void* workspace, size_t workspace_bytes, void* stream) {
+  return ifn::decode_entry(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                           active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
+                           workspace, workspace_bytes, stream, ifn::DecodeAppend{nullptr, nullptr, nullptr, nullptr},
+                           false, plan, plan_bytes, nullptr, true);
+}
+
+extern "C" int ifn_paged_decode_append_planning(void* out, const void* query, void* kv_pool_layer, int64_t num_pages,
+                                                const int32_t* block_tables, int32_t max_pages_per_seq,
+                                                const int32_t* seq_lens, const uint8_t* active_mask,
+                                                const int32_t* slot_mapping, const void* new_k, const void* new_v,
+                                                int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                                int32_t head_dim, int32_t block_size, int32_t max_seq_len,
+                                                float scale, void* plan, size_t plan_bytes, void* workspace,
+                                                size_t workspace_bytes, void* stream) {
+  if (kv_pool_layer == nullptr) return IFN_ERR_INVALID_ARGUMENT;
+  return ifn::decode_entry(out, query, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                           active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale,
+                           workspace, workspace_bytes, stream,
+                           ifn::DecodeAppend{static_cast<const ifn::f16*>(new_k), static_cast<const ifn::f16*>(new_v),
+                                             slot_mapping, static_cast<ifn::f16*>(kv_pool_layer)},
+                           false, plan, plan_bytes, nullptr, true);
+}
+
+namespace ifn {
+
+static int prep_append_entry(void* out, const float* q, const float* k, const float* v, const float* q_norm_weight,
+                             const float* k_norm_weight, const float* rope_table, int32_t max_positions,
+                             const int32_t* positions, const int32_t* slot_mapping, void* kv_pool_layer,
+                             int64_t num_pages, const int32_t* block_tables, int32_t max_pages_per_seq,
+                             const int32_t* seq_lens, const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
+                             int32_t num_kv_heads, int32_t head_dim, int32_t block_size, int32_t max_seq_len,
+                             float scale, float eps, const void* plan, size_t plan_bytes, void* workspace,
+                             size_t workspace_bytes, void* stream, bool build_plan) {
   if (q == nullptr || k == nullptr || v == nullptr || q_norm_weight == nullptr || k_norm_weight == nullptr ||
       rope_table == nullptr || positions == nullptr || slot_mapping == nullptr || kv_pool_layer == nullptr)
     return IFN_ERR_INVALID_ARGUMENT;
@@ -938,7 +971,43 @@ extern "C" int ifn_paged_decode_prep_append(void* out, const float* q, const flo
   return decode_entry(out, q, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens, active_mask,
                       batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len, scale, workspace,
                       workspace_bytes, stream, DecodeAppend{nullptr, nullptr, slot_mapping, static_cast<f16*>(kv_pool_layer)},
-                      false, plan, plan_bytes, &pp);
+                      false, plan, plan_bytes, &pp, build_plan);
+}
+
+}  // namespace ifn
+
+extern "C" int ifn_paged_decode_prep_append(void* out, const float* q, const float* k, const float* v,
+                                            const float* q_norm_weight, const float* k_norm_weight,
+                                            const float* rope_table, int32_t max_positions,
+                                            const int32_t* positions, const int32_t* slot_mapping,
+                                            void* kv_pool_layer, int64_t num_pages, const int32_t* block_tables,
+                                            int32_t max_pages_per_seq, const int32_t* seq_lens,
+                                            const uint8_t* active_mask, int32_t batch, int32_t num_q_heads,
+                                            int32_t num_kv_heads, int32_t head_dim, int32_t block_size,
+                                            int32_t max_seq_len, float scale, float eps, const void* plan,
+                                            size_t plan_bytes, void* workspace, size_t workspace_bytes,
+                                            void* stream) {
+  return ifn::prep_append_entry(out, q, k, v, q_norm_weight, k_norm_weight, rope_table, max_positions, positions,
+                                slot_mapping, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                                active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len,
+                                scale, eps, plan, plan_bytes, workspace, workspace_bytes, stream, false);
+}
+
+extern "C" int ifn_paged_decode_prep_append_planning(void* out, const float* q, const float* k, const float* v,
+                                                     const float* q_norm_weight, const float* k_norm_weight,
+                                                     const float* rope_table, int32_t max_positions,
+                                                     const int32_t* positions, const int32_t* slot_mapping,
+                                                     void* kv_pool_layer, int64_t num_pages,
+                                                     const int32_t* block_tables, int32_t max_pages_per_seq,
+                                                     const int32_t* seq_lens, const uint8_t* active_mask,
+                                                     int32_t batch, int32_t num_q_heads, int32_t num_kv_heads,
+                                                     int32_t head_dim, int32_t block_size, int32_t max_seq_len,
+                                                     float scale, float eps, void* plan, size_t plan_bytes,
+                                                     void* workspace, size_t workspace_bytes, void* stream) {
+  return ifn::prep_append_entry(out, q, k, v, q_norm_weight, k_norm_weight, rope_table, max_positions, positions,
+                                slot_mapping, kv_pool_layer, num_pages, block_tables, max_pages_per_seq, seq_lens,
+                                active_mask, batch, num_q_heads, num_kv_heads, head_dim, block_size, max_seq_len,
+                                scale, eps, plan, plan_bytes, workspace, workspace_bytes, stream, true);
 }
 
 namespace ifn {

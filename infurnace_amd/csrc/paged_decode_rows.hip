@@ -82,7 +82,7 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
                        int32_t max_pages, const int32_t* seq_lens, const uint8_t* active, int32_t batch, int32_t hq,
                        int32_t hkv, int32_t d, int32_t max_len, float scale_log2, void* workspace, int blocks,
                        const DecodeAppend& ap, bool cached, const int32_t* plan, hipStream_t stream,
-                       const DecodePrep* prep, const DecodePrefix* px, int32_t block_size) {
+                       const DecodePrep* prep, const DecodePrefix* px, int32_t block_size, int32_t* plan_out) {
   if (px != nullptr && (ap.pool != nullptr || prep != nullptr)) return IFN_ERR_UNSUPPORTED;
   RowsKernel k = pick_rows(d, hq / hkv, hkv, ap.pool != nullptr, !cached, prep != nullptr, px != nullptr, block_size);
   if (k == nullptr) return IFN_ERR_UNSUPPORTED;
@@ -93,6 +93,7 @@ int rows_decode_launch(f16* out, const f16* q, const f16* pool, int64_t num_page
   ws.count = reinterpret_cast<uint32_t*>(wsb);
   ws.ml = reinterpret_cast<float*>(wsb + off_ml);
   ws.o = reinterpret_cast<float*>(wsb + off_o);
+  ws.plan_out = plan == nullptr ? plan_out : nullptr;
   const DecodePrep pp = prep != nullptr ? *prep : DecodePrep{};
   const DecodePrefix pf = px != nullptr ? *px : DecodePrefix{nullptr, nullptr, 0, 0, nullptr};
   k<<<dim3(unsigned(blocks)), dim3(kRowsThreads), 0, stream>>>(plan, pool, block_tables, q,

@@ -218,12 +218,13 @@ def qk_norm_rope_store_and_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
     lib = _capi.lib()
     nbytes = lib.ifn_paged_decode_workspace_bytes(n, hq, hkv, d, bs, msl)
     ws = workspace_for(dev, stream, nbytes)
-    pp, pbytes = None, 0
+    pp, pbytes, entry = None, 0, lib.ifn_paged_decode_prep_append
     if plan is not None:
         key = _plan_key((n, hq, d), sm, pool_layer, block_tables, sequence_lengths, active_mask, msl)
         pp = plan.ptr_for(key, True)
         pbytes = plan.nbytes if pp else 0
-    status = lib.ifn_paged_decode_prep_append(
+        entry = getattr(lib, plan.entry("ifn_paged_decode_prep_append", "ifn_paged_decode_prep_append_planning"))
+    status = entry(
         ptr(out), ptr(q), ptr(k), ptr(v), ptr(q_norm_weight), ptr(k_norm_weight), ptr(rope), rope.shape[0],
         ptr(positions), ptr(sm), ptr(pool_layer), P, ptr(block_tables), max_pages, ptr(sequence_lengths),
         ptr(active_mask), n, hq, hkv, d, bs, msl, float(scale), float(eps), pp, pbytes, ptr(ws), ws.numel(), stream)
@@ -233,6 +234,8 @@ def qk_norm_rope_store_and_decode(q: torch.Tensor, k: torch.Tensor, v: torch.Ten
         return paged_attention(q16, kv_pool, block_tables, sequence_lengths, active_mask, layer=layer, scale=scale,
                                out=out, block_size=block_size, max_seq_len=max_seq_len, plan=plan)
     _capi.check("ifn_paged_decode_prep_append", status)
+    if plan is not None:
+        plan.built()
     return out
 
 

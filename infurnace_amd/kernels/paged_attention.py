@@ -60,15 +60,22 @@ class DecodePlan:
     tensors and shapes are passed (any layer of the same pool), and with
     ``validate=True`` also their contents (the plan is rebuilt and compared byte
     for byte).
+
+    A lazy plan (``decode_plan(..., lazy=True)``) is built by the first decode call
+    that takes it (``ifn_paged_decode_planning`` and its append / pre-append forms):
+    that call decodes unplanned and writes the plan, so the step needs no plan
+    launch of its own.  It takes the form of that call: built by a call without
+    slots, it serves the fused-append calls only as an unplanned split.
     """
 
-    def __init__(self, buf, nbytes: int, key: tuple, rebuild=None):
+    def __init__(self, buf, nbytes: int, key: tuple, rebuild=None, pending: bool = False):
         self.buf, self.nbytes, self.key, self._rebuild = buf, nbytes, key, rebuild
+        self.pending = pending and buf is not None
 
     def check_current(self) -> None:
         """Validate mode: raise unless a plan built now from the same tensors is identical
         (their contents were not changed since this one was built)."""
-        if self.buf is None or self._rebuild is None:
+        if self.buf is None or self._rebuild is None or self.pending:
             return
         fresh = self._rebuild()
         if not torch.equal(fresh.buf, self.buf):
@@ -82,6 +89,14 @@ class DecodePlan:
         if key[0] != self.key[0] or key[2:] != self.key[2:] or (need_slots and key[1] != self.key[1]):
             raise PagedAttentionError("this DecodePlan was built for other tensors or shapes")
         return None if self.buf is None else self.buf.data_ptr()
+
+    def entry(self, planned: str, planning: str) -> str:
+        """The C entry point for the next call: ``planning`` while the plan is still to be built."""
+        return planning if self.pending else planned
+
+    def built(self) -> None:
+        """The call that builds a lazy plan has been enqueued."""
+        self.pending = False
 
 
 def _plan_key(query_shape, slot_mapping, pool_layer, block_tables, sequence_lengths, active_mask, max_seq_len,
@@ -98,7 +113,7 @@ def _plan_key(query_shape, slot_mapping, pool_layer, block_tables, sequence_leng
 def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, sequence_lengths: torch.Tensor,
                 active_mask: torch.Tensor | None = None, slot_mapping: torch.Tensor | None = None, *,
                 layer: int = 0, block_size: int = 16, max_seq_len: int | None = None,
-                shared_prefix_pages: torch.Tensor | None = None) -> DecodePlan:
+                shared_prefix_pages: torch.Tensor | None = None, lazy: bool = False) -> DecodePlan:
     """Build the step plan for decode calls with these tables, lengths, mask and (optionally) slots.
 
     ``query_shape`` is the decode query's shape [B, Hq, D].  The plan is computed on the
@@ -107,7 +122,8 @@ def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, 
     ``shared_prefix_pages`` (the tensor the step's ``paged_attention`` calls pass; only its
     length matters here) it is the plan of the shared-prefix decode
     (``ifn_paged_decode_shared_prefix_plan``) and takes no slots.  Shapes that decode without a
-    plan give an empty plan, which the calls accept and ignore.
+    plan give an empty plan, which the calls accept and ignore.  ``lazy``: allocate the plan
+    only; the step's first decode call builds it (not for the shared-prefix decode).
     """
     pool_layer, (P, bs, hkv, d) = check_pool(kv_pool, layer, PagedAttentionError)
     dev = pool_layer.device
@@ -140,6 +156,8 @@ def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, 
             raise PagedAttentionError(f"{sp} shared pages exceed the table's {max_pages} columns")
         if slot_mapping is not None:
             raise PagedAttentionError("a shared-prefix plan takes no slot_mapping (that decode has no fused append)")
+        if lazy:
+            raise PagedAttentionError("a shared-prefix plan is built by decode_plan itself (lazy=False)")
     key = _plan_key((n, hq, d), slot_mapping, pool_layer, block_tables, sequence_lengths, active_mask, msl, sp)
     if n == 0:
         return DecodePlan(None, 0, key)
@@ -149,6 +167,13 @@ def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, 
         return DecodePlan(None, 0, key)
     # zero-filled, so that words the kernel leaves unwritten compare equal between two plans
     buf = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+
+    def rebuild():
+        return decode_plan(query_shape, kv_pool, block_tables, sequence_lengths, active_mask, slot_mapping,
+                           layer=layer, block_size=block_size, max_seq_len=max_seq_len,
+                           shared_prefix_pages=shared_prefix_pages)
+    if lazy:
+        return DecodePlan(buf, nbytes, key, rebuild, pending=True)
     if sp is None:
         _capi.call("ifn_paged_decode_plan", buf.data_ptr(), nbytes, ptr(block_tables), max_pages,
                    ptr(sequence_lengths), ptr(active_mask), ptr(slot_mapping), P, n, hq, hkv, d, bs, msl,
@@ -156,11 +181,6 @@ def decode_plan(query_shape, kv_pool: torch.Tensor, block_tables: torch.Tensor, 
     else:
         _capi.call("ifn_paged_decode_shared_prefix_plan", buf.data_ptr(), nbytes, ptr(block_tables), max_pages,
                    ptr(sequence_lengths), ptr(active_mask), sp, P, n, hq, hkv, d, bs, msl, current_stream(dev))
-
-    def rebuild():
-        return decode_plan(query_shape, kv_pool, block_tables, sequence_lengths, active_mask, slot_mapping,
-                           layer=layer, block_size=block_size, max_seq_len=max_seq_len,
-                           shared_prefix_pages=shared_prefix_pages)
     return DecodePlan(buf, nbytes, key, rebuild)
 
 
@@ -306,6 +326,8 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
             nbytes = lib.ifn_paged_decode_shared_prefix_workspace_bytes(n, hq, hkv, d, bs, sp)
             ws = workspace_for(dev, stream, nbytes)
             if plan is not None:  # a plan from decode_plan(..., shared_prefix_pages=...)
+                if plan.pending:
+                    raise PagedAttentionError("a lazy DecodePlan cannot serve the shared-prefix decode")
                 key = _plan_key((n, hq, d), None, pool_layer, block_tables, sequence_lengths, active_mask, msl, sp)
                 pp = plan.ptr_for(key, False)
                 _capi.call("ifn_paged_decode_shared_prefix_planned", ptr(out), ptr(query), ptr(pool_layer), P,
@@ -322,9 +344,10 @@ def paged_attention(query: torch.Tensor, kv_pool: torch.Tensor, block_tables: to
         if plan is not None:
             key = _plan_key((n, hq, d), None, pool_layer, block_tables, sequence_lengths, active_mask, msl)
             pp = plan.ptr_for(key, False)
-            _capi.call("ifn_paged_decode_planned", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables),
-                       max_pages, ptr(sequence_lengths), ptr(active_mask), n, hq, hkv, d, bs, msl, float(scale),
-                       pp, plan.nbytes if pp else 0, ptr(ws), ws.numel(), stream)
+            _capi.call(plan.entry("ifn_paged_decode_planned", "ifn_paged_decode_planning"), ptr(out), ptr(query),
+                       ptr(pool_layer), P, ptr(block_tables), max_pages, ptr(sequence_lengths), ptr(active_mask), n,
+                       hq, hkv, d, bs, msl, float(scale), pp, plan.nbytes if pp else 0, ptr(ws), ws.numel(), stream)
+            plan.built()
             return out
         _capi.call("ifn_paged_decode", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables),
                    max_pages, ptr(sequence_lengths), ptr(active_mask), n, hq, hkv, d, bs, msl,
@@ -437,9 +460,11 @@ def store_kv_and_decode(query: torch.Tensor, kv_pool: torch.Tensor, block_tables
     if plan is not None:
         key = _plan_key((n, hq, d), sm, pool_layer, block_tables, sequence_lengths, active_mask, msl)
         pp = plan.ptr_for(key, True)
-        _capi.call("ifn_paged_decode_append_planned", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables),
-                   max_pages, ptr(sequence_lengths), ptr(active_mask), ptr(sm), ptr(new_k), ptr(new_v), n, hq, hkv,
-                   d, bs, msl, float(scale), pp, plan.nbytes if pp else 0, ptr(ws), ws.numel(), stream)
+        _capi.call(plan.entry("ifn_paged_decode_append_planned", "ifn_paged_decode_append_planning"), ptr(out),
+                   ptr(query), ptr(pool_layer), P, ptr(block_tables), max_pages, ptr(sequence_lengths),
+                   ptr(active_mask), ptr(sm), ptr(new_k), ptr(new_v), n, hq, hkv, d, bs, msl, float(scale), pp,
+                   plan.nbytes if pp else 0, ptr(ws), ws.numel(), stream)
+        plan.built()
         return out
     _capi.call("ifn_paged_decode_append", ptr(out), ptr(query), ptr(pool_layer), P, ptr(block_tables), max_pages,
                ptr(sequence_lengths), ptr(active_mask), ptr(sm), ptr(new_k), ptr(new_v), n, hq, hkv, d, bs, msl,

@@ -85,9 +85,10 @@ class _Step:
         self.event.record()
 
     def _decode_plan(self, q: torch.Tensor):
+        # (lazy: the step's first layer decodes unplanned and writes the plan the others read)
         if self.plan is None:
             self.plan = decode_plan(q.shape, self.runner.cache.kv, self.block_tables, self.seq_lens, self.active,
-                                    self.slot_mapping, max_seq_len=self.max_len)
+                                    self.slot_mapping, max_seq_len=self.max_len, lazy=True)
         return self.plan
 
     def store_attend(self, layer: int, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
