@@ -138,6 +138,27 @@ def test_config5_full_size_with_churn(dev):
         assert_attn_close(out, plain.cpu().numpy(), f"config5 step {step} vs ifn_paged_decode")
 
 
+def test_config5_one_launch_deterministic(dev):
+    """Config 5 decodes in one launch whose prefix and private-page workgroups finish at about the same
+    time, so which of them merges a (row, kv head) varies from call to call; the output must not.
+    Ten calls bit-identical, and the G = 2 form (Qwen3-0.6B heads over the same tables) too."""
+    say("shared-prefix config5 one-launch determinism")
+    w = workloads.config5()
+    g = torch.Generator(device=dev).manual_seed(55)
+    prefix = to_dev(w.block_tables[0, :w.shared_prefix_pages].copy(), dev)
+    tdev, ldev = to_dev(w.block_tables, dev), to_dev(w.seq_lens, dev)
+    for hq in (32, 16):
+        pool = randn16((2, w.num_pages, 16, 8, 128), g, dev)
+        q = randn16((w.batch, hq, 128), g, dev)
+        first = paged_attention(q, pool, tdev, ldev, None, shared_prefix_pages=prefix)
+        for i in range(9):
+            again = paged_attention(q, pool, tdev, ldev, None, shared_prefix_pages=prefix)
+            assert torch.equal(first.view(torch.int16), again.view(torch.int16)), f"hq={hq}: call {i + 1} differs"
+        rows = [0, 17, 40, 63]
+        assert_attn_close(first[rows], oracle_decode(pool, w.block_tables, w.seq_lens, q, rows=rows),
+                          f"hq={hq} rows")
+
+
 def test_large_batch_many_splits(dev):
     """200 rows over a 2000-token prefix: several query blocks and key splits in the prefix pass."""
     say("shared-prefix B=200 prefix 2000")
