@@ -766,8 +766,9 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
       num_kv_heads < 1 || head_dim < 1 || max_seq_len < 0 || num_q_heads % num_kv_heads != 0)
     return IFN_ERR_INVALID_ARGUMENT;
   if (batch > kMaxBatch || int64_t(batch) * num_kv_heads > kMaxTickets) return IFN_ERR_UNSUPPORTED;
-  const bool rows = rows_decode_supported(batch, num_q_heads, num_kv_heads, head_dim, max_pages_per_seq, max_seq_len,
-                                          block_size, append && prep == nullptr);
+  // (an empty batch is checked as one row: it returns IFN_OK below, whichever kernel the shape has)
+  const bool rows = rows_decode_supported(std::max(batch, 1), num_q_heads, num_kv_heads, head_dim, max_pages_per_seq,
+                                          max_seq_len, block_size, append && prep == nullptr);
   // pages of other sizes than 16 tokens: the whole-row kernel, where it compiles them, only
   if (block_size != kBlock && (!rows || prep != nullptr)) return IFN_ERR_UNSUPPORTED;
   DecodeKernel k = rows ? nullptr
@@ -777,6 +778,8 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
   if (!rows && k == nullptr) return IFN_ERR_UNSUPPORTED;
   if (prep != nullptr && (!rows || !rows_prep_supported(num_q_heads, num_kv_heads, head_dim)))
     return IFN_ERR_UNSUPPORTED;
+  // (a call that builds the step's plan needs somewhere to write it, where the shape has a plan)
+  if (build_plan && rows && batch > 0 && plan == nullptr) return IFN_ERR_INVALID_ARGUMENT;
   IFN_CHECK_ALIGN16(out);
   IFN_CHECK_ALIGN16(query);
   IFN_CHECK_ALIGN16(kv_pool_layer);
@@ -796,7 +799,6 @@ static int decode_entry(void* out, const void* query, const void* kv_pool_layer,
   if (rows) {
     // planned: the kernel reads this workgroup's record before checking the header; build_plan: every
     // workgroup writes its record
-    if (build_plan && plan == nullptr) return IFN_ERR_INVALID_ARGUMENT;
     if (plan != nullptr) {
       if (plan_bytes < rows_plan_bytes(batch, blocks)) return IFN_ERR_WORKSPACE;
       IFN_CHECK_ALIGN16(plan);

@@ -227,6 +227,45 @@ def test_prefill_prep_append_host_validation():
     assert call(maxpos=1000) == _capi.IFN_ERR_INVALID_ARGUMENT      # positions past the rotary table
 
 
+def test_planning_entries_host_validation():
+    """The three planning entries (the step's first decode, which writes the step plan) reject a
+    missing plan buffer, and otherwise check what their unplanned forms check, before any HIP call."""
+    L = _capi.lib()
+    ok = dict(out=A, q=A, pool=A, P=1024, bt=A, W=256, sl=A, am=None, sm=A, nk=A, nv=A, B=32, hq=16, hkv=8,
+              d=128, bs=16, msl=4096, plan=A, pb=1 << 20, ws=None, wsb=0)
+
+    def plain(**kw):
+        a = {**ok, **kw}
+        return L.ifn_paged_decode_planning(a["out"], a["q"], a["pool"], a["P"], a["bt"], a["W"], a["sl"], a["am"],
+                                           a["B"], a["hq"], a["hkv"], a["d"], a["bs"], a["msl"], 0.0, a["plan"],
+                                           a["pb"], a["ws"], a["wsb"], None)
+
+    def append(**kw):
+        a = {**ok, **kw}
+        return L.ifn_paged_decode_append_planning(a["out"], a["q"], a["pool"], a["P"], a["bt"], a["W"], a["sl"],
+                                                  a["am"], a["sm"], a["nk"], a["nv"], a["B"], a["hq"], a["hkv"],
+                                                  a["d"], a["bs"], a["msl"], 0.0, a["plan"], a["pb"], a["ws"],
+                                                  a["wsb"], None)
+
+    def prep(**kw):
+        a = {**ok, **kw}
+        return L.ifn_paged_decode_prep_append_planning(a["out"], A, A, A, A, A, A, 8192, A, a["sm"], a["pool"],
+                                                       a["P"], a["bt"], a["W"], a["sl"], a["am"], a["B"], a["hq"],
+                                                       a["hkv"], a["d"], a["bs"], a["msl"], 0.0, 1e-6, a["plan"],
+                                                       a["pb"], a["ws"], a["wsb"], None)
+
+    for call in (plain, append, prep):
+        assert call(plan=None) == _capi.IFN_ERR_INVALID_ARGUMENT, call.__name__
+        assert call(out=None) == _capi.IFN_ERR_INVALID_ARGUMENT, call.__name__
+        assert call(hq=24) == _capi.IFN_ERR_UNSUPPORTED, call.__name__
+        assert call(B=0) == _capi.IFN_OK, call.__name__
+        assert call(B=0, plan=None) == _capi.IFN_OK, call.__name__  # nothing to decode, nothing to plan
+        assert call() == _capi.IFN_ERR_WORKSPACE, call.__name__
+    assert append(sm=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert append(pool=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+    assert prep(sm=None) == _capi.IFN_ERR_INVALID_ARGUMENT
+
+
 def test_shared_prefix_plan_host_validation():
     """The shared-prefix plan rejects bad arguments on the host; planned and unplanned entries agree on them."""
     L = _capi.lib()
