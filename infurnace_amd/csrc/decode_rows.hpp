@@ -12,9 +12,10 @@
 //
 //  * Workgroup ranges over the flat token list.  The tokens of all rows, row after row, form one
 //    list; workgroup w (one per CU, 8 waves) takes positions [T w / N, T (w+1) / N), so ragged
-//    batches cost every CU the same bytes.  Every non-empty row is counted kRowStartCost
-//    positions longer than its keys (virtual positions in front of it): a range that ends one
-//    row and starts the next pays a second start-up and merge, and gets that many keys fewer.
+//    batches cost every CU the same bytes.  In a call of several rows every non-empty row is counted
+//    kRowStartCost positions longer than its keys (virtual positions in front of it): a range
+//    that ends one row and starts the next pays a second start-up and merge, and gets that many
+//    keys fewer.
 //    Workgroups are remapped so that each XCD streams a contiguous eighth of the list.  A range is
 //    cut into pieces at row boundaries.
 //  * Inside a piece the 8 waves interleave by token: wave w takes positions a + w + 8 i, so at
@@ -59,9 +60,13 @@ constexpr int kRowsStages = 2;       // tokens in flight per wave (the ring's de
 // next pays a second start-up, a second merge of its waves and possibly two split merges, so the
 // split counts each non-empty row as kRowStartCost tokens longer (virtual tokens in front of it).
 constexpr int kRowStartCost = 24;
+// The cost the split charges a call's rows: none for a single row (every range then holds one
+// piece of it, so no range starts a second row), which keeps one row of 512 keys at 16 ranges
+// of 32 keys -- one burst per wave and one round trip of split states in the final merge.
+__host__ __device__ __forceinline__ int row_start_cost(int batch) { return batch > 1 ? kRowStartCost : 0; }
 // Fewest virtual positions per range.  A row split over n ranges is merged by one workgroup that
 // reads n partial states (Hq x D floats each), so short batches are split over fewer workgroups:
-// one row of 512 keys takes 17 ranges of about 32 positions instead of one range per CU.
+// one row of 512 keys takes 16 ranges of 32 positions instead of one range per CU.
 constexpr int kMinRangePositions = 32;
 
 // floor(num / den) for 0 <= num < 2^52 and den > 0: a double quotient (off by less than one)
@@ -124,7 +129,7 @@ __device__ __forceinline__ int row_slot(const int32_t* slots, const uint8_t* act
 
 // Offsets of the rows in the split's virtual token list, into s_cum[0 .. batch] (all threads of the
 // workgroup call it; returns the total).  Row b occupies [s_cum[b], s_cum[b + 1]); its keys are the
-// last of those positions, after kRowStartCost virtual ones when it has any.  Shared-prefix mode
+// last of those positions, after row_start_cost(batch) virtual ones when it has any.  Shared-prefix mode
 // (pk > 0): a row of at least pk keys (a cascade row, flagged in s_casc) streams only its keys
 // after the first pk.
 // s_len (optional): the rows' keys, already in LDS (and published by a barrier).
@@ -139,7 +144,7 @@ __device__ __forceinline__ int build_offsets(int* s_cum, int* s_wsum, const int3
     const bool casc = pk > 0 && len >= pk;
     if (s_casc != nullptr && i < batch) s_casc[i] = casc ? 1 : 0;
     if (casc) len -= pk;
-    if (len > 0) len += kRowStartCost;
+    if (len > 0) len += row_start_cost(batch);
     int x = len;
 #pragma unroll
     for (int o = 1; o < kWave; o <<= 1) {
@@ -263,7 +268,7 @@ __global__ __launch_bounds__(kPlanThreads) void decode_plan_kernel(
       auto range_of = [&](int64_t t) -> int { return int(div_floor((t + 1) * nr - 1, T)); };
       int b = locate_row(s_cum, batch, t0);
       while (b < batch) {
-        const int cb = s_cum[b] + kRowStartCost;
+        const int cb = s_cum[b] + row_start_cost(batch);
         const int len = s_cum[b + 1] - cb;
         if (len > 0) {
           if (cb >= t1) break;
@@ -786,7 +791,7 @@ __device__ __forceinline__ void decode_rows_body(
     P.nranges = 1;
     int b = prev < 0 ? locate_row(s_cum, batch, t0) : prev + 1;
     for (; b < batch; ++b) {
-      const int cb = s_cum[b] + kRowStartCost;
+      const int cb = s_cum[b] + row_start_cost(batch);
       const int len = s_cum[b + 1] - cb;
       if (len <= 0) continue;
       if (cb >= t1) break;

@@ -1158,7 +1158,7 @@ __global__ __launch_bounds__(8 * kWave) void shared_prefix_fused_kernel(
     const int b = q0 + tid;
     int first = -1, nrg = 0;
     if (b < batch && row_keys(seq_lens, active, b, cap) >= pk) {
-      const int cb = s_cum[b] + kRowStartCost, len = s_cum[b + 1] - cb;
+      const int cb = s_cum[b] + row_start_cost(batch), len = s_cum[b + 1] - cb;
       int f = 0;
       if (len > 0) {  // (T >= len > 0)
         f = int(div_floor((int64_t(cb) + 1) * nr - 1, T));
