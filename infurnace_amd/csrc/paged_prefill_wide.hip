@@ -194,7 +194,9 @@ __device__ __forceinline__ void pin_probs(f16x8 (&p)[RT][2]) {
 }
 
 // The kernel's body, run by workgroup bid of grid, with its LDS at smem (WideCfg::kLdsBytes).
-template <int D, int G, int RT, int W, bool kAppend, bool kPrep>
+// kPrefix: the caller runs only the shared-prefix pass (px.key_len > 0), so the causal limits are
+// compiled out (in the one-launch shared-prefix kernel this keeps the loop within its registers).
+template <int D, int G, int RT, int W, bool kAppend, bool kPrep, bool kPrefix = false>
 __device__ __forceinline__ void prefill_wide_body(
     unsigned char* smem, const int bid, const int grid, f16* out, const f16* q, const f16* pool, int64_t num_pages,
     const int32_t* table, int32_t query_start, int32_t T, int32_t num_kv_heads, int32_t n_qb, int32_t nsplit,
@@ -215,7 +217,7 @@ __device__ __forceinline__ void prefill_wide_body(
   const int col = lane % 32, half = lane / 32;
   const int hq = num_kv_heads * G;
   // (shared-prefix mode: every row sees keys [0, key_len), no causal limit)
-  const bool prefix_mode = px.key_len > 0;
+  const bool prefix_mode = kPrefix || px.key_len > 0;
   const int total = prefix_mode ? px.key_len : query_start + T;  // keys that exist
   const int q0 = qb * kQw;
   const int key_end = prefix_mode ? total : min(total, query_start + q0 + kQw);  // keys some row sees
@@ -1137,7 +1139,7 @@ __global__ __launch_bounds__(8 * kWave) void shared_prefix_fused_kernel(
 
   // The prefix pass for (query block qb, kv head bid % Hkv, key split): its states, stored at the
   // device coherence point.
-  prefill_wide_body<D, G, 1, 8, false, false>(
+  prefill_wide_body<D, G, 1, 8, false, false, true>(
       smem, bid, npre, out, q, pool, num_pages, prefix_pages, 0, batch, HKV, n_qb, nsplit, scale_log2,
       PrefillWorkspace{nullptr, nullptr, nullptr}, PrefillAppend{nullptr, nullptr, nullptr},
       PrefixOut{px.ml, px.o, pk, px.nstates, const_cast<f16*>(px.oh)}, PrefillPrep{});
