@@ -6,7 +6,7 @@ min(CUs, ceil(L / 32)) ranges, and the last arrival merges that many split state
 lengths around the page, burst, range and merge-batch edges (512 is config 1, whose 16 ranges
 make exactly one 16-state merge batch; 513 is the first length that needs 17):
 
-- the unplanned call against the oracle;
+- the unplanned call against the oracle (16-token pages, and 32- and 64-token pages);
 - planned and planning calls (the step's first decode, which writes the plan) bit-identical to
   the unplanned one, and the written plan byte-identical to the plan kernel's;
 - the fused append bit-identical to its planned and planning forms, and close to the oracle on
@@ -26,11 +26,11 @@ pytestmark = pytest.mark.gpu
 LENS = [1, 4, 15, 16, 31, 32, 33, 100, 255, 256, 257, 511, 512, 513, 544, 1000, 4096, 8191]
 
 
-def _row(rng, L, hq, hkv, d, extra_pages=3):
-    n = max(1, -(-L // 16))
+def _row(rng, L, hq, hkv, d, extra_pages=3, bs=16):
+    n = max(1, -(-L // bs))
     P = n + extra_pages
     table = rng.permutation(P)[:n].astype(np.int32)[None, :]
-    pool = rng.standard_normal((2, P, 16, hkv, d), dtype=np.float32).astype(np.float16)
+    pool = rng.standard_normal((2, P, bs, hkv, d), dtype=np.float32).astype(np.float16)
     q = rng.standard_normal((1, hq, d), dtype=np.float32).astype(np.float16)
     return pool, table, np.asarray([L], np.int32), q
 
@@ -59,6 +59,28 @@ def test_single_row_decode_forms(dev, hq, hkv, d):
             assert torch.equal(_bits(got), _bits(ref)), f"L={L}: {what} differs from unplanned"
         if eager.buf is not None:
             assert torch.equal(eager.buf, lazy.buf), f"L={L}: the written plan differs from the plan kernel's"
+
+
+@pytest.mark.parametrize("bs", [32, 64])
+def test_single_row_larger_pages(dev, bs):
+    """The 32- and 64-token page instantiations (their own kernels and plan kernels) split a single
+    row the same way."""
+    for L in (1, 31, 33, 512, 513, 2047, 5000):
+        say(f"single row L={L} page {bs}")
+        rng = np.random.default_rng(L + bs)
+        pool, table, lens, q = _row(rng, L, 16, 8, 128, bs=bs)
+        qd, p, bt, sl = to_dev(q, dev), to_dev(pool, dev), to_dev(table, dev), to_dev(lens, dev)
+        ref = paged_attention(qd, p, bt, sl, block_size=bs)
+        torch.cuda.synchronize()
+        assert_attn_close(ref, oracle.paged_attention(q, pool, table, lens), f"L={L} page {bs}")
+        eager = decode_plan(qd.shape, p, bt, sl, block_size=bs)
+        planned = paged_attention(qd, p, bt, sl, block_size=bs, plan=eager)
+        lazy = decode_plan(qd.shape, p, bt, sl, block_size=bs, lazy=True)
+        planning = paged_attention(qd, p, bt, sl, block_size=bs, plan=lazy)
+        torch.cuda.synchronize()
+        assert torch.equal(_bits(planned), _bits(ref)), f"L={L} page {bs}: planned differs"
+        assert torch.equal(_bits(planning), _bits(ref)), f"L={L} page {bs}: planning differs"
+        assert torch.equal(eager.buf, lazy.buf), f"L={L} page {bs}: the written plan differs"
 
 
 @pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128)])
